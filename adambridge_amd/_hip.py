@@ -1,0 +1,258 @@
+"""ctypes binding of libadambridge_hip.so (the HIP fused-update library).
+
+Plays the part of the reference's ``adambridge/native.py`` (NativeKernels,
+native.py:273-435): the same struct mirrors (``HParams``, ``Group``,
+``Segment``), ABI and struct-size checks at load, and a RuntimeError for every
+non-zero return code.  Pointers in segments are device pointers; a "pool" is a
+launch queue on a HIP stream.
+
+There is no fallback: if the library is missing or fails its checks, ``load()``
+raises.  ``torch`` must be imported first so that the library binds to the HIP
+runtime torch already loaded (same SONAME), and shares its streams.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+__all__ = ["HipKernels", "HParams", "Group", "Segment", "load", "LIB_PATH", "DT_NONE", "DT_F32", "DT_BF16",
+           "DT_FP8", "DT_F24", "MOMENT_CODES", "MASTER_CODES", "ALGORITHMS", "SIMD_NAMES"]
+
+LIB_PATH = Path(__file__).resolve().with_name("libadambridge_hip.so")
+ABI_VERSION = 5
+
+DT_NONE, DT_F32, DT_BF16, DT_FP8, DT_F24 = 0, 1, 2, 3, 4
+_DTYPE_CODES = {torch.float32: DT_F32, torch.bfloat16: DT_BF16}
+MOMENT_CODES = {"fp32": DT_F32, "bf16": DT_BF16, "fp8": DT_FP8}
+MASTER_CODES = {"fp32": DT_F32, "fp24": DT_F24}
+ALGORITHMS = {"adamw": 0, "lion": 1}
+SIMD_NAMES = {0: "scalar", 1: "avx2", 2: "avx512"}
+
+
+class HParams(ctypes.Structure):
+    """adambridge_hparams (include/adambridge_hip.h; reference kernels.c:77-88, native.py:58-70)."""
+    _fields_ = [("beta1", ctypes.c_float), ("beta2", ctypes.c_float),
+                ("one_minus_beta1", ctypes.c_float), ("one_minus_beta2", ctypes.c_float),
+                ("decay", ctypes.c_float), ("step_size", ctypes.c_float),
+                ("inv_sqrt_bc2", ctypes.c_float), ("eps", ctypes.c_float),
+                ("seed", ctypes.c_uint32), ("stochastic", ctypes.c_int32)]
+
+
+class Group(ctypes.Structure):
+    """adambridge_group (reference kernels.c:736-745, native.py:73-85)."""
+    _fields_ = [("lr", ctypes.c_double), ("beta1", ctypes.c_double), ("beta2", ctypes.c_double),
+                ("eps", ctypes.c_double), ("weight_decay", ctypes.c_double),
+                ("seed", ctypes.c_uint64), ("stochastic", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+
+class Segment(ctypes.Structure):
+    """adambridge_segment with device pointers (reference kernels.c:747-769, native.py:88-111)."""
+    _fields_ = [("p", ctypes.c_void_p), ("p_lo", ctypes.c_void_p), ("g", ctypes.c_void_p),
+                ("m", ctypes.c_void_p), ("v", ctypes.c_void_p), ("m_scale", ctypes.c_void_p),
+                ("v_scale", ctypes.c_void_p), ("out", ctypes.c_void_p), ("group", ctypes.POINTER(Group)),
+                ("n", ctypes.c_int64), ("step", ctypes.c_int64), ("index", ctypes.c_uint64),
+                ("offset", ctypes.c_int64), ("g_dtype", ctypes.c_int32), ("mv_dtype", ctypes.c_int32),
+                ("out_dtype", ctypes.c_int32), ("algorithm", ctypes.c_int32), ("p_dtype", ctypes.c_int32),
+                ("reserved", ctypes.c_int32)]
+
+
+_SegArray = ctypes.POINTER(ctypes.POINTER(Segment))
+
+# Every symbol include/adambridge_hip.h declares.
+EXPORTS = (
+    "adambridge_abi_version", "adambridge_detected_simd_level", "adambridge_simd_level",
+    "adambridge_set_simd_level", "adambridge_hparams_size", "adambridge_group_size", "adambridge_segment_size",
+    "adambridge_fused_adamw", "adambridge_pool_create", "adambridge_pool_destroy", "adambridge_pool_threads",
+    "adambridge_pool_set_spin", "adambridge_multi_step", "adambridge_multi_apply", "adambridge_pool_set_stream",
+    "adambridge_pool_sync", "adambridge_set_stream", "adambridge_last_error", "adambridge_backend",
+)
+
+
+def open_library(path: Path = LIB_PATH) -> ctypes.CDLL:
+    """dlopen the library and declare every entry point; checks the ABI and struct layouts.
+    Needs no GPU (no entry point that touches the device is called)."""
+    if not path.exists():
+        raise RuntimeError(f"{path} is not built: run `python -m adambridge_amd.build` (or __graft_entry__.build())")
+    lib = ctypes.CDLL(str(path))
+    i32, i64, u64, vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64, ctypes.c_void_p
+    sig = {
+        "adambridge_abi_version": (ctypes.c_int, []),
+        "adambridge_detected_simd_level": (ctypes.c_int, []),
+        "adambridge_simd_level": (ctypes.c_int, []),
+        "adambridge_set_simd_level": (ctypes.c_int, [ctypes.c_int]),
+        "adambridge_hparams_size": (ctypes.c_int, []),
+        "adambridge_group_size": (ctypes.c_int, []),
+        "adambridge_segment_size": (ctypes.c_int, []),
+        "adambridge_fused_adamw": (ctypes.c_int, [vp, vp, ctypes.c_int, vp, vp, ctypes.c_int, vp, ctypes.c_int,
+                                                  i64, u64, ctypes.POINTER(HParams)]),
+        "adambridge_pool_create": (vp, [i32, vp, i32]),
+        "adambridge_pool_destroy": (None, [vp]),
+        "adambridge_pool_threads": (i32, [vp]),
+        "adambridge_pool_set_spin": (None, [vp, i32]),
+        "adambridge_multi_step": (ctypes.c_int, [vp, _SegArray, i32, i32]),
+        "adambridge_multi_apply": (ctypes.c_int, [vp, _SegArray, ctypes.POINTER(HParams), i32, i32]),
+        "adambridge_pool_set_stream": (ctypes.c_int, [vp, vp]),
+        "adambridge_pool_sync": (ctypes.c_int, [vp]),
+        "adambridge_set_stream": (ctypes.c_int, [vp]),
+        "adambridge_last_error": (ctypes.c_char_p, []),
+        "adambridge_backend": (ctypes.c_char_p, []),
+    }
+    for name in EXPORTS:
+        fn = getattr(lib, name)
+        fn.restype, fn.argtypes = sig[name]
+    if lib.adambridge_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{path} has ABI {lib.adambridge_abi_version()}, expected {ABI_VERSION}")
+    for fn, struct in (("adambridge_hparams_size", HParams), ("adambridge_group_size", Group),
+                       ("adambridge_segment_size", Segment)):
+        if getattr(lib, fn)() != ctypes.sizeof(struct):
+            raise RuntimeError(f"{fn}: struct layout mismatch between the library and Python")
+    return lib
+
+
+class HipKernels:
+    """The loaded library (reference counterpart: NativeKernels, native.py:273-435)."""
+
+    def __init__(self, path: Path = LIB_PATH):
+        self.path = path
+        self._lib = open_library(path)
+
+    # -- identity and the SIMD level reproduced ------------------------------
+
+    @property
+    def backend(self) -> str:
+        return self._lib.adambridge_backend().decode()
+
+    @property
+    def simd_level(self) -> str:
+        return SIMD_NAMES[self._lib.adambridge_simd_level()]
+
+    @property
+    def detected_simd_level(self) -> str:
+        return SIMD_NAMES[self._lib.adambridge_detected_simd_level()]
+
+    def set_simd_level(self, name: str | None) -> str:
+        """Reproduce another reference ISA's rounding (``None`` restores AVX-512)."""
+        code = -1 if name is None else {v: k for k, v in SIMD_NAMES.items()}[name]
+        return SIMD_NAMES[self._lib.adambridge_set_simd_level(code)]
+
+    @staticmethod
+    def supports(grad_dtype: torch.dtype, moment_precision: str, out_dtype: torch.dtype | None) -> bool:
+        return (grad_dtype in _DTYPE_CODES and moment_precision in MOMENT_CODES
+                and (out_dtype is None or out_dtype in _DTYPE_CODES))
+
+    @staticmethod
+    def dtype_code(dtype: torch.dtype | None) -> int:
+        return DT_NONE if dtype is None else _DTYPE_CODES[dtype]
+
+    # -- queues --------------------------------------------------------------
+
+    def create_pool(self) -> int:
+        """A launch queue on the current device (reference: adambridge_pool_create)."""
+        handle = self._lib.adambridge_pool_create(0, None, 0)
+        if not handle:
+            raise RuntimeError(f"adambridge_pool_create failed: {self.last_error()}")
+        return handle
+
+    def destroy_pool(self, handle: int) -> None:
+        self._lib.adambridge_pool_destroy(handle)
+
+    def pool_threads(self, handle: int) -> int:
+        return self._lib.adambridge_pool_threads(handle)
+
+    def set_pool_stream(self, handle: int, stream: torch.cuda.Stream | int | None) -> None:
+        self._lib.adambridge_pool_set_stream(handle, _stream_handle(stream))
+
+    def pool_sync(self, handle: int | None) -> None:
+        self._check(self._lib.adambridge_pool_sync(handle), "adambridge_pool_sync")
+
+    def set_stream(self, stream: torch.cuda.Stream | int | None) -> None:
+        """The calling thread's stream for pool-less calls."""
+        self._lib.adambridge_set_stream(_stream_handle(stream))
+
+    def last_error(self) -> str:
+        return self._lib.adambridge_last_error().decode(errors="replace")
+
+    # -- updates ---------------------------------------------------------------
+
+    @staticmethod
+    def segment_array(segments: list) -> ctypes.Array:
+        """Array of Segment pointers for multi_step / multi_apply."""
+        return (ctypes.POINTER(Segment) * len(segments))(*segments)
+
+    def multi_step(self, pool: int | None, segments: ctypes.Array, threads: int = 0) -> None:
+        """Enqueue an update of every segment; coefficients from each segment's group and step."""
+        self._check(self._lib.adambridge_multi_step(pool, segments, len(segments), threads), "adambridge_multi_step")
+
+    def multi_apply(self, pool: int | None, segments: ctypes.Array, hparams: list, threads: int = 0) -> None:
+        """Like multi_step with explicit coefficients, one ``HParams`` per segment."""
+        hps = (HParams * len(hparams))(*hparams)
+        self._check(self._lib.adambridge_multi_apply(pool, segments, hps, len(segments), threads),
+                    "adambridge_multi_apply")
+
+    def fused_adamw(self, master: torch.Tensor, grad: torch.Tensor, m: torch.Tensor, v: torch.Tensor,
+                    out: torch.Tensor | None, hp: HParams, lo: int, hi: int) -> None:
+        """Update elements ``[lo, hi)`` of flat contiguous device tensors in place, synchronously
+        (reference: NativeKernels.fused_adamw, native.py:389-435, with the same checks)."""
+        n = master.numel()
+        tensors = {"master": master, "grad": grad, "m": m, "v": v, **({} if out is None else {"out": out})}
+        for name, t in tensors.items():
+            if not t.is_cuda or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous device tensor")
+            if t.numel() != n:
+                raise ValueError(f"{name} has {t.numel()} elements, master has {n}")
+            if t.device != master.device:
+                raise ValueError(f"{name} is on {t.device}, master on {master.device}")
+        if master.dtype != torch.float32:
+            raise TypeError("master must be float32")
+        for name, t in tensors.items():
+            if name != "master" and t.dtype not in _DTYPE_CODES:
+                raise TypeError(f"{name} must be float32 or bfloat16, got {t.dtype}")
+        if m.dtype != v.dtype:
+            raise TypeError("m and v must have the same dtype")
+        if not 0 <= lo <= hi <= n:
+            raise IndexError(f"range [{lo}, {hi}) outside 0..{n}")
+        with torch.cuda.device(master.device):
+            self.set_stream(torch.cuda.current_stream())
+            rc = self._lib.adambridge_fused_adamw(
+                master.data_ptr() + lo * 4, grad.data_ptr() + lo * grad.element_size(), _DTYPE_CODES[grad.dtype],
+                m.data_ptr() + lo * m.element_size(), v.data_ptr() + lo * v.element_size(), _DTYPE_CODES[m.dtype],
+                None if out is None else out.data_ptr() + lo * out.element_size(),
+                DT_NONE if out is None else _DTYPE_CODES[out.dtype], hi - lo, lo, ctypes.byref(hp))
+        self._check(rc, "adambridge_fused_adamw")
+
+    @staticmethod
+    def make_hparams(c, seed: int, stochastic: bool) -> HParams:
+        """From ``StepCoefficients`` (reference native.py:381-387)."""
+        return HParams(c.beta1, c.beta2, 1.0 - c.beta1, 1.0 - c.beta2, c.decay, c.step_size, c.inv_sqrt_bc2,
+                       c.eps, seed & 0xFFFFFFFF, int(stochastic))
+
+    def _check(self, rc: int, what: str) -> None:
+        if rc != 0:
+            detail = self.last_error() if rc == -20 else ""
+            raise RuntimeError(f"{what} rejected the update (code {rc}){': ' + detail if detail else ''}")
+
+
+def _stream_handle(stream) -> int | None:
+    if stream is None:
+        return None
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+_lock = threading.Lock()
+_loaded: HipKernels | None = None
+
+
+def load() -> HipKernels:
+    """The library, loaded once.  Raises RuntimeError if it is missing or inconsistent: there is no
+    other implementation to fall back to."""
+    global _loaded
+    with _lock:
+        if _loaded is None:
+            _loaded = HipKernels()
+        return _loaded

@@ -1,0 +1,482 @@
+// adambridge_hip.hip -- fused AdamW / Lion optimizer update for MI355X (gfx950)
+// and the C ABI declared in include/adambridge_hip.h.
+//
+// One launch updates every segment (tensor) of a call: the grid is a list of
+// tiles of kTile elements, each workgroup finds its segment by a binary search
+// of the per-segment first-tile table (uniform, scalar loads), then streams its
+// tile once: reads the gradient, the master and the moments, updates them in
+// registers and writes the master, the moments and the bf16 working weight.
+// 128-bit loads and stores, non-temporal, one pass: the bytes moved per
+// element are exactly the reference's minimum (benchmarks/bench_kernels.py:63-65).
+//
+// FP8 moments are handled 128-element block by block: 16 lanes x 8 elements
+// per block, the two block maxima reduced with cross-lane shuffles, codes and
+// scales written by the same lanes (kernels.c:1034-1059).
+//
+// Segment descriptors travel in the kernel arguments when a call has at most
+// kInline segments (the per-parameter hook path: no copy at all), otherwise in
+// a device table filled by one asynchronous copy from a pinned staging slot.
+
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <array>
+#include <atomic>
+#include <mutex>
+#include <utility>
+#include <new>
+#include <vector>
+
+#include "../../include/adambridge_hip.h"
+#include "abh_device.hpp"
+
+namespace abh {
+
+constexpr int kThreads = 256;
+constexpr int64_t kTile = 8192;   // elements per workgroup (a multiple of kFp8Block and of 8 * kThreads)
+constexpr int kInline = 7;        // segments carried in the kernel arguments
+
+// Per-segment launch descriptor (device side), 144 bytes.
+struct DevSeg {
+    void* p;
+    uint8_t* p_lo;
+    const void* g;
+    void* m;
+    void* v;
+    float* m_scale;
+    float* v_scale;
+    void* out;
+    int64_t n;
+    int64_t n_main;      // [0, n_main) take the fused form, [n_main, n) the scalar-tail form
+    int64_t tile_begin;  // first tile of this segment in the launch
+    uint32_t idx0;       // uint32(offset): element i draws rounding bits at idx0 + i
+    uint32_t flags;      // kVec: every pointer allows 16-byte access; kSR: stochastic rounding
+    Coef c;
+    uint32_t seed_m, seed_v, seed_p, pad;
+};
+static_assert(sizeof(DevSeg) == 144, "DevSeg layout");
+constexpr uint32_t kVec = 1u, kSR = 2u;
+
+struct Launch {
+    const DevSeg* table;  // device table when nsegs > kInline
+    int32_t nsegs;
+    int32_t pad;
+    DevSeg inl[kInline];
+};
+static_assert(sizeof(Launch) <= 1024 + 16, "kernel argument block");
+
+__device__ __forceinline__ const DevSeg* find_segment(const Launch& L, int64_t tile)
+{
+    const DevSeg* S = L.nsegs <= kInline ? L.inl : L.table;
+    int lo = 0, hi = L.nsegs - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (S[mid].tile_begin <= tile) lo = mid; else hi = mid - 1;
+    }
+    return S + lo;
+}
+
+// --------------------------------------------------------------- loads/stores
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Streaming accesses: every byte is touched once per step, so keep them out of the caches.
+template <typename T>
+__device__ __forceinline__ T ld(const T* p) { return __builtin_nontemporal_load(p); }
+template <typename T>
+__device__ __forceinline__ void st(T* p, T v) { __builtin_nontemporal_store(v, p); }
+
+// 8 consecutive values as FP32, from BF16 bits or FP32, 16-byte aligned.
+template <int DT>
+__device__ __forceinline__ void load8(const void* base, int64_t i, float (&x)[8])
+{
+    if constexpr (DT == DT_BF16) {
+        const u32x4 w = ld(reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + i));
+        const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            x[2 * k] = bitsf(u[k] << 16);
+            x[2 * k + 1] = bitsf(u[k] & 0xffff0000u);
+        }
+    } else {
+        const f32x4* q = reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + i);
+        const f32x4 a = ld(q), b = ld(q + 1);
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    }
+}
+
+__device__ __forceinline__ void store8_f32(void* base, int64_t i, const float (&x)[8])
+{
+    f32x4* q = reinterpret_cast<f32x4*>(static_cast<float*>(base) + i);
+    st(q, f32x4{x[0], x[1], x[2], x[3]});
+    st(q + 1, f32x4{x[4], x[5], x[6], x[7]});
+}
+
+__device__ __forceinline__ void store8_u16(void* base, int64_t i, const uint32_t (&h)[8])
+{
+    const u32x4 w = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+    st(reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + i), w);
+}
+
+// Master: FP32, or FP24 = hi plane (BF16 bits) << 16 | lo plane << 8.
+template <int PT>
+__device__ __forceinline__ void load_master8(const DevSeg& s, int64_t i, float (&x)[8])
+{
+    if constexpr (PT == DT_F24) {
+        const u32x4 h = ld(reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(s.p) + i));
+        const u32x2 l = ld(reinterpret_cast<const u32x2*>(s.p_lo + i));
+        const uint32_t hu[4] = {h.x, h.y, h.z, h.w};
+        const uint32_t lu[2] = {l.x, l.y};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t hi16 = (hu[k >> 1] >> (16 * (k & 1))) & 0xffffu;
+            const uint32_t lo8 = (lu[k >> 2] >> (8 * (k & 3))) & 0xffu;
+            x[k] = bitsf((hi16 << 16) | (lo8 << 8));
+        }
+    } else {
+        load8<DT_F32>(s.p, i, x);
+    }
+}
+
+// Rounds and stores 8 new master values; x becomes the values stored.
+template <int PT>
+__device__ __forceinline__ void store_master8(const DevSeg& s, int64_t i, float (&x)[8], bool sr, uint32_t idx)
+{
+    if constexpr (PT == DT_F24) {
+        uint32_t hi[8], lo[2] = {0u, 0u};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t b = f24_round(x[k], sr, sr ? hash32((idx + k) ^ s.seed_p) : 0u);
+            x[k] = bitsf(b);
+            hi[k] = b >> 16;
+            lo[k >> 2] |= ((b >> 8) & 0xffu) << (8 * (k & 3));
+        }
+        store8_u16(s.p, i, hi);
+        st(reinterpret_cast<u32x2*>(s.p_lo + i), u32x2{lo[0], lo[1]});
+    } else {
+        store8_f32(s.p, i, x);
+    }
+}
+
+template <int MV>
+__device__ __forceinline__ void store_moment8(void* base, int64_t i, const float (&x)[8], bool sr, uint32_t idx,
+                                              uint32_t seed)
+{
+    if constexpr (MV == DT_BF16) {
+        uint32_t h[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) h[k] = bf16_store(x[k], sr, sr ? hash32((idx + k) ^ seed) : 0u);
+        store8_u16(base, i, h);
+    } else {
+        store8_f32(base, i, x);
+    }
+}
+
+template <int OT>
+__device__ __forceinline__ void store_out8(void* base, int64_t i, const float (&x)[8])
+{
+    if constexpr (OT == DT_BF16) {
+        uint32_t h[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) h[k] = bf16_rne(x[k]);
+        store8_u16(base, i, h);
+    } else if constexpr (OT == DT_F32) {
+        store8_f32(base, i, x);
+    }
+}
+
+// ------------------------------------------------------------ scalar access
+
+template <int DT>
+__device__ __forceinline__ float load1(const void* base, int64_t i)
+{
+    if constexpr (DT == DT_BF16) return bitsf((uint32_t)static_cast<const uint16_t*>(base)[i] << 16);
+    else return static_cast<const float*>(base)[i];
+}
+
+template <int PT>
+__device__ __forceinline__ float load_master1(const DevSeg& s, int64_t i)
+{
+    if constexpr (PT == DT_F24)
+        return bitsf(((uint32_t)static_cast<const uint16_t*>(s.p)[i] << 16) | ((uint32_t)s.p_lo[i] << 8));
+    else return static_cast<const float*>(s.p)[i];
+}
+
+template <int PT>
+__device__ __forceinline__ float store_master1(const DevSeg& s, int64_t i, float x, bool sr, uint32_t idx)
+{
+    if constexpr (PT == DT_F24) {
+        const uint32_t b = f24_round(x, sr, sr ? hash32(idx ^ s.seed_p) : 0u);
+        static_cast<uint16_t*>(s.p)[i] = (uint16_t)(b >> 16);
+        s.p_lo[i] = (uint8_t)(b >> 8);
+        return bitsf(b);
+    } else {
+        static_cast<float*>(s.p)[i] = x;
+        return x;
+    }
+}
+
+template <int MV>
+__device__ __forceinline__ void store_moment1(void* base, int64_t i, float x, bool sr, uint32_t r)
+{
+    if constexpr (MV == DT_BF16) static_cast<uint16_t*>(base)[i] = (uint16_t)bf16_store(x, sr, r);
+    else static_cast<float*>(base)[i] = x;
+}
+
+template <int OT>
+__device__ __forceinline__ void store_out1(void* base, int64_t i, float x)
+{
+    if constexpr (OT == DT_BF16) static_cast<uint16_t*>(base)[i] = (uint16_t)bf16_rne(x);
+    else if constexpr (OT == DT_F32) static_cast<float*>(base)[i] = x;
+}
+
+// ------------------------------------------------- FP32 / BF16 moment kernel
+
+// ALGO: AdamW or Lion; MV: moment storage (F32 / BF16); PT: master (F32 / F24);
+// GT: gradient (F32 / BF16); OT: working-weight output (NONE / F32 / BF16).
+template <int ALGO, int MV, int PT, int GT, int OT>
+__global__ __launch_bounds__(kThreads) void k_update(Launch L)
+{
+    const int64_t tile = blockIdx.x;
+    const DevSeg& s = *find_segment(L, tile);
+    const int64_t n = s.n, n_main = s.n_main;
+    const int64_t lo = (tile - s.tile_begin) * kTile;
+    const int64_t hi = lo + kTile < n ? lo + kTile : n;
+    const bool sr = (s.flags & kSR) != 0;
+    const Coef c = s.c;
+    const int64_t nvec = (s.flags & kVec) ? (n_main & ~(int64_t)7) : 0;
+    int64_t vend = hi < nvec ? hi : nvec;
+    if (vend < lo) vend = lo;
+
+    // whole groups of 8 elements, every one of them in the fused range
+    for (int64_t i = lo + threadIdx.x * 8; i < vend; i += kThreads * 8) {
+        const uint32_t idx = s.idx0 + (uint32_t)i;
+        float g[8], m[8], v[8], p[8];
+        load8<GT>(s.g, i, g);
+        load8<MV>(s.m, i, m);
+        if constexpr (ALGO == ALGO_ADAMW) load8<MV>(s.v, i, v);
+        load_master8<PT>(s, i, p);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if constexpr (ALGO == ALGO_ADAMW) p[k] = adamw<true>(p[k], g[k], m[k], v[k], c);
+            else p[k] = lion(p[k], g[k], m[k], c);
+        }
+        store_master8<PT>(s, i, p, sr, idx);
+        store_moment8<MV>(s.m, i, m, sr, idx, s.seed_m);
+        if constexpr (ALGO == ALGO_ADAMW) store_moment8<MV>(s.v, i, v, sr, idx, s.seed_v);
+        store_out8<OT>(s.out, i, p);
+    }
+    // the rest one element per lane: misaligned buffers, ragged ends, the scalar tail
+    for (int64_t i = vend + threadIdx.x; i < hi; i += kThreads) {
+        const uint32_t idx = s.idx0 + (uint32_t)i;
+        const float g = load1<GT>(s.g, i);
+        float m = load1<MV>(s.m, i);
+        float p = load_master1<PT>(s, i);
+        if constexpr (ALGO == ALGO_ADAMW) {
+            float v = load1<MV>(s.v, i);
+            p = adamw_sel(p, g, m, v, c, i < n_main);
+            store_moment1<MV>(s.v, i, v, sr, sr ? hash32(idx ^ s.seed_v) : 0u);
+        } else {
+            p = lion(p, g, m, c);
+        }
+        p = store_master1<PT>(s, i, p, sr, idx);
+        store_moment1<MV>(s.m, i, m, sr, sr ? hash32(idx ^ s.seed_m) : 0u);
+        store_out1<OT>(s.out, i, p);
+    }
+}
+
+// ------------------------------------------------------------ FP8 moment kernel
+
+// 8 FP8 codes through byte accesses (buffers without 8-byte alignment).
+__device__ __forceinline__ u32x2 load_codes8(const uint8_t* q)
+{
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) w[k >> 2] |= (uint32_t)q[k] << (8 * (k & 3));
+    return u32x2{w[0], w[1]};
+}
+
+__device__ __forceinline__ void store_codes8(uint8_t* q, const uint32_t (&w)[2])
+{
+#pragma unroll
+    for (int k = 0; k < 8; ++k) q[k] = (uint8_t)(w[k >> 2] >> (8 * (k & 3)));
+}
+
+// Max over the 16 lanes of a block group (values are >= 0 and never NaN).
+__device__ __forceinline__ float group16_max(float x)
+{
+#pragma unroll
+    for (int d = 1; d < 16; d <<= 1) x = fmaxf(x, __shfl_xor(x, d, 16));
+    return x;
+}
+
+template <int ALGO, int PT, int GT, int OT>
+__global__ __launch_bounds__(kThreads) void k_update_fp8(Launch L)
+{
+    constexpr bool kLion = ALGO == ALGO_LION;
+    const int64_t tile = blockIdx.x;
+    const DevSeg& s = *find_segment(L, tile);
+    const int64_t n = s.n, n_main = s.n_main;
+    const int64_t lo = (tile - s.tile_begin) * kTile;
+    const int64_t hi = lo + kTile < n ? lo + kTile : n;
+    const bool sr = (s.flags & kSR) != 0;
+    const bool vec = (s.flags & kVec) != 0;
+    const Coef c = s.c;
+    const int lane = threadIdx.x & 15;
+    const int group = threadIdx.x >> 4;
+    uint8_t* const mq = static_cast<uint8_t*>(s.m);
+    uint8_t* const vq = static_cast<uint8_t*>(s.v);
+
+    // one 128-element block per 16-lane group; this lane holds elements e0 .. e0+7
+    for (int64_t b0 = lo + group * kFp8Block; b0 < hi; b0 += (kThreads / 16) * kFp8Block) {
+        const int64_t blk = b0 / kFp8Block;
+        const int64_t e0 = b0 + lane * 8;
+        const uint32_t idx = s.idx0 + (uint32_t)e0;
+        const bool full = vec && e0 + 8 <= n;
+        const float sm = s.m_scale[blk];
+        const float sv = kLion ? 0.0f : s.v_scale[blk];
+        // codes are stored padded to whole blocks, so all 8 of this lane's exist
+        const u32x2 cm = vec ? ld(reinterpret_cast<const u32x2*>(mq + e0)) : load_codes8(mq + e0);
+        u32x2 cv = {0u, 0u};
+        if constexpr (!kLion) cv = vec ? ld(reinterpret_cast<const u32x2*>(vq + e0)) : load_codes8(vq + e0);
+        float g[8], p[8], mt[8], vt[8];
+        if (full) {
+            load8<GT>(s.g, e0, g);
+            load_master8<PT>(s, e0, p);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const bool in = e0 + k < n;
+                g[k] = in ? load1<GT>(s.g, e0 + k) : 0.0f;
+                p[k] = in ? load_master1<PT>(s, e0 + k) : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t w = k < 4 ? cm.x : cm.y, wv = k < 4 ? cv.x : cv.y;
+            mt[k] = e4m3_decode((w >> (8 * (k & 3))) & 0xffu) * sm;
+            if constexpr (!kLion) {
+                const float u = e5m2_decode((wv >> (8 * (k & 3))) & 0xffu) * sv;
+                vt[k] = u * u;
+            }
+        }
+        // the update, FP32 moments in registers
+        const bool lane_fused = kLion || e0 + 8 <= n_main;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if constexpr (kLion) p[k] = lion(p[k], g[k], mt[k], c);
+            else p[k] = lane_fused ? adamw<true>(p[k], g[k], mt[k], vt[k], c)
+                                   : adamw_sel(p[k], g[k], mt[k], vt[k], c, e0 + k < n_main);
+        }
+        if (full) {
+            store_master8<PT>(s, e0, p, sr, idx);
+            store_out8<OT>(s.out, e0, p);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                if (e0 + k < n) {
+                    const float stored = store_master1<PT>(s, e0 + k, p[k], sr, idx + k);
+                    store_out1<OT>(s.out, e0 + k, stored);
+                }
+            }
+        }
+        // block maxima (NaN skipped), elements past the end count as zero
+        float am = 0.0f, au = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const bool in = e0 + k < n;
+            if (!in) { mt[k] = 0.0f; vt[k] = 0.0f; }
+            const float a = fabsf(mt[k]);
+            am = a > am ? a : am;
+            if constexpr (!kLion) {
+                const float u = __builtin_sqrtf(vt[k] > 0.0f ? vt[k] : 0.0f);
+                vt[k] = u;
+                au = u > au ? u : au;
+            }
+        }
+        am = group16_max(am);
+        const float scm = am > 0.0f ? am / 448.0f : 1.0f;
+        uint32_t qm[2] = {0u, 0u}, qv[2] = {0u, 0u};
+        float scu = 1.0f;
+        if constexpr (!kLion) {
+            au = group16_max(au);
+            scu = au > 0.0f ? au / 57344.0f : 1.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t ik = idx + k;
+            const bool in = e0 + k < n;   // padding codes are zero
+            const uint32_t a = e4m3_encode(mt[k] / scm, sr, sr ? hash32(ik ^ s.seed_m) : 0u);
+            qm[k >> 2] |= (in ? a : 0u) << (8 * (k & 3));
+            if constexpr (!kLion) {
+                const uint32_t b = e5m2_encode(vt[k] / scu, sr, sr ? hash32(ik ^ s.seed_v) : 0u);
+                qv[k >> 2] |= (in ? b : 0u) << (8 * (k & 3));
+            }
+        }
+        if (vec) {
+            st(reinterpret_cast<u32x2*>(mq + e0), u32x2{qm[0], qm[1]});
+            if constexpr (!kLion) st(reinterpret_cast<u32x2*>(vq + e0), u32x2{qv[0], qv[1]});
+        } else {
+            store_codes8(mq + e0, qm);
+            if constexpr (!kLion) store_codes8(vq + e0, qv);
+        }
+        if (lane == 0) {
+            s.m_scale[blk] = scm;
+            if constexpr (!kLion) s.v_scale[blk] = scu;
+        }
+    }
+}
+
+// ------------------------------------------------------------ kernel table
+
+using KernelFn = void (*)(Launch);
+
+// Index: ((((algo * 3 + mv) * 2 + pt) * 2 + gt) * 3 + ot), with
+// mv 0/1/2 = F32/BF16/FP8, pt 0/1 = F32/F24, gt 0/1 = F32/BF16, ot 0/1/2 = NONE/F32/BF16.
+constexpr int kNumKernels = 2 * 3 * 2 * 2 * 3;
+
+template <int ALGO, int MVI, int PTI, int GTI, int OTI>
+constexpr KernelFn pick()
+{
+    constexpr int PT = PTI ? DT_F24 : DT_F32;
+    constexpr int GT = GTI ? DT_BF16 : DT_F32;
+    constexpr int OT = OTI == 0 ? DT_NONE : OTI == 1 ? DT_F32 : DT_BF16;
+    if constexpr (MVI == 2) return &k_update_fp8<ALGO, PT, GT, OT>;
+    else return &k_update<ALGO, MVI ? DT_BF16 : DT_F32, PT, GT, OT>;
+}
+
+template <int I>
+constexpr KernelFn entry()
+{
+    constexpr int ot = I % 3, gt = (I / 3) % 2, pt = (I / 6) % 2, mv = (I / 12) % 3, algo = I / 36;
+    return pick<algo, mv, pt, gt, ot>();
+}
+
+template <int... I>
+constexpr auto make_table(std::integer_sequence<int, I...>)
+{
+    return std::array<KernelFn, sizeof...(I)>{entry<I>()...};
+}
+
+static const auto kKernels = make_table(std::make_integer_sequence<int, kNumKernels>{});
+
+inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
+{
+    const int mvi = mv == DT_F32 ? 0 : mv == DT_BF16 ? 1 : 2;
+    const int pti = pt == DT_F24 ? 1 : 0;
+    const int gti = gt == DT_BF16 ? 1 : 0;
+    const int oti = ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2;
+    return (((algo * 3 + mvi) * 2 + pti) * 2 + gti) * 3 + oti;
+}
+
+}  // namespace abh
+
+#include "abh_host.inc"

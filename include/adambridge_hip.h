@@ -1,0 +1,185 @@
+/*
+ * adambridge_hip.h -- C ABI of libadambridge_hip.so, the fused AdamW / Lion
+ * optimizer update for AMD Instinct MI355X (gfx950).
+ *
+ * Drop-in for the reference's native kernel library, adambridge/csrc/
+ * adambridge_kernels.c, as its ctypes binding (adambridge/native.py:273-435)
+ * uses it: the same entry-point names, argument meanings, struct layouts,
+ * dtype codes and negative error codes.  What changes:
+ *
+ *   - every buffer pointer in a segment (and in adambridge_fused_adamw) is a
+ *     device pointer in HBM of the current HIP device, not a host pointer;
+ *   - a "pool" is a launch queue bound to one device and one HIP stream, not
+ *     a host thread pool; work is enqueued on that stream and the call returns
+ *     once it is enqueued (adambridge_fused_adamw alone waits, as documented);
+ *   - the "SIMD level" selects which of the reference's host ISAs is
+ *     reproduced bit for bit (its vector bodies fuse multiply-adds, its scalar
+ *     tail does not; see adambridge_set_simd_level).
+ *
+ * All structs, scalars and pointers are plain C; no torch types cross this
+ * boundary.  Thread-safety: calls on different pools may run concurrently from
+ * different host threads; calls on one pool must not overlap.
+ */
+#ifndef ADAMBRIDGE_HIP_H
+#define ADAMBRIDGE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ADAMBRIDGE_API __attribute__((visibility("default")))
+
+/* ABI version of the reference this library is a drop-in for (kernels.c:71). */
+#define ADAMBRIDGE_ABI_VERSION 5
+
+/* Storage codes, kernels.c:73: DT_NONE 0, DT_F32 1, DT_BF16 2, DT_FP8 3, DT_F24 4.
+ * Algorithms, kernels.c:75: ALGO_ADAMW 0, ALGO_LION 1.
+ * SIMD levels reproduced, kernels.c:74: 0 scalar, 1 AVX2 (8 lanes), 2 AVX-512 (16 lanes). */
+enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, ADAMBRIDGE_DT_FP8 = 3,
+       ADAMBRIDGE_DT_F24 = 4 };
+enum { ADAMBRIDGE_ALGO_ADAMW = 0, ADAMBRIDGE_ALGO_LION = 1 };
+
+/* Error codes (kernels.c:1537-1553, 1582-1584, 1620-1621), plus the HIP-side ones. */
+enum {
+    ADAMBRIDGE_OK = 0,
+    ADAMBRIDGE_EBADN = -1,         /* negative n, NULL segment array */
+    ADAMBRIDGE_ENULL = -2,         /* a required buffer pointer is NULL */
+    ADAMBRIDGE_EGDTYPE = -3,
+    ADAMBRIDGE_EMVDTYPE = -4,
+    ADAMBRIDGE_EOUTDTYPE = -5,
+    ADAMBRIDGE_EOUTNULL = -6,
+    ADAMBRIDGE_ESCALES = -7,       /* FP8 moments without block scales */
+    ADAMBRIDGE_EGROUP = -8,        /* multi_step segment without a group */
+    ADAMBRIDGE_ETOOMANY = -9,
+    ADAMBRIDGE_ENOMEM = -10,
+    ADAMBRIDGE_EOFFSET = -11,      /* negative offset, or FP8 offset not a multiple of 128 */
+    ADAMBRIDGE_EALGO = -12,
+    ADAMBRIDGE_EPDTYPE = -13,
+    ADAMBRIDGE_EHIP = -20,         /* a HIP runtime call failed; see adambridge_last_error() */
+    ADAMBRIDGE_EDEVICE = -21       /* the pool belongs to another device than the current one */
+};
+
+/* Per-segment step coefficients: kernels.c:77-88 (40 bytes). */
+typedef struct adambridge_hparams {
+    float beta1;
+    float beta2;
+    float one_minus_beta1;
+    float one_minus_beta2;
+    float decay;         /* 1 - lr * weight_decay */
+    float step_size;     /* AdamW: lr / (1 - beta1^t); Lion: lr */
+    float inv_sqrt_bc2;  /* 1 / sqrt(1 - beta2^t) */
+    float eps;
+    uint32_t seed;       /* rounding stream of this (parameter, step) */
+    int32_t stochastic;  /* nonzero: stochastic rounding of BF16/FP8 moments and an FP24 master */
+} adambridge_hparams;
+
+/* A parameter group's hyperparameters: kernels.c:736-745 (56 bytes, host memory). */
+typedef struct adambridge_group {
+    double lr;
+    double beta1;
+    double beta2;
+    double eps;
+    double weight_decay;
+    uint64_t seed;
+    int32_t stochastic;
+    int32_t reserved;
+} adambridge_group;
+
+/* One tensor (or one chunk of one): kernels.c:747-769 (128 bytes).  The struct
+ * itself is host memory; p .. out are device pointers. */
+typedef struct adambridge_segment {
+    void* p;                 /* FP32 master, or the FP24 hi plane (uint16) when p_dtype is DT_F24 */
+    uint8_t* p_lo;           /* FP24 lo plane (one byte per element); NULL for FP32 */
+    const void* g;           /* gradient, g_dtype */
+    void* m;                 /* first moment, mv_dtype (FP8: E4M3 codes, padded to 128 per block) */
+    void* v;                 /* second moment (FP8: E5M2 codes of sqrt(v)); unused by Lion */
+    float* m_scale;          /* FP8 only: one scale per 128 elements */
+    float* v_scale;
+    void* out;               /* optional copy of the new master in out_dtype (the bf16 working weight) */
+    const adambridge_group* group;   /* multi_step only; host memory */
+    int64_t n;
+    int64_t step;            /* this update's step number (multi_step) */
+    uint64_t index;          /* parameter index: selects the rounding stream */
+    int64_t offset;          /* element offset of p[0] within its parameter (multiple of 128 for FP8) */
+    int32_t g_dtype;
+    int32_t mv_dtype;
+    int32_t out_dtype;
+    int32_t algorithm;
+    int32_t p_dtype;         /* DT_F32 (or 0) or DT_F24 */
+    int32_t reserved;
+} adambridge_segment;
+
+/* kernels.c:1493. */
+ADAMBRIDGE_API int adambridge_abi_version(void);
+
+/* kernels.c:1495-1510.  The level whose results are reproduced: its vector
+ * body (fused multiply-adds) covers the first n - n mod W elements of every
+ * segment and its scalar loop (separately rounded products and sums) the last
+ * n mod W, W = 16 at level 2, 8 at level 1; level 0 is the scalar loop for
+ * every element.  Lion and FP8 blocks follow the same rule as the reference.
+ * Detected level: 2.  set: <0 restores it; returns the level now active.
+ * Process-wide, read at enqueue time. */
+ADAMBRIDGE_API int adambridge_detected_simd_level(void);
+ADAMBRIDGE_API int adambridge_simd_level(void);
+ADAMBRIDGE_API int adambridge_set_simd_level(int level);
+
+/* kernels.c:1512-1514: layout checks for bindings. */
+ADAMBRIDGE_API int adambridge_hparams_size(void);
+ADAMBRIDGE_API int adambridge_group_size(void);
+ADAMBRIDGE_API int adambridge_segment_size(void);
+
+/* kernels.c:1518-1535.  One FP32-master AdamW update of n elements with FP32 or
+ * BF16 moments, on the calling thread's stream (adambridge_set_stream; the
+ * null stream by default).  Waits for completion before returning, like the
+ * reference's synchronous call. */
+ADAMBRIDGE_API int adambridge_fused_adamw(float* p, const void* g, int g_dtype, void* m, void* v, int mv_dtype,
+                                          void* out, int out_dtype, int64_t n, uint64_t offset,
+                                          const adambridge_hparams* hp);
+
+/* kernels.c:1427-1487.  A launch queue on the current HIP device, initially on
+ * the null stream.  nthreads, cpus and ncpus are accepted and ignored (the
+ * device schedules its own compute units).  NULL on failure.  pool_threads
+ * returns the device's compute-unit count; pool_set_spin is a no-op. */
+ADAMBRIDGE_API void* adambridge_pool_create(int32_t nthreads, const int32_t* cpus, int32_t ncpus);
+ADAMBRIDGE_API void adambridge_pool_destroy(void* pool);
+ADAMBRIDGE_API int32_t adambridge_pool_threads(void* pool);
+ADAMBRIDGE_API void adambridge_pool_set_spin(void* pool, int32_t spin);
+
+/* kernels.c:1611-1626.  Update every segment; coefficients from its group and
+ * step, computed on the host in double as the reference does.  Validates every
+ * segment before enqueueing anything (first bad segment's code).  pool NULL:
+ * the current device's default queue on the calling thread's stream.
+ * threads is ignored.  Asynchronous: ordered on the pool's stream. */
+ADAMBRIDGE_API int adambridge_multi_step(void* pool, adambridge_segment* const* segs, int32_t nsegs,
+                                         int32_t threads);
+
+/* kernels.c:1630-1641.  As multi_step with caller-supplied coefficients. */
+ADAMBRIDGE_API int adambridge_multi_apply(void* pool, adambridge_segment* const* segs,
+                                          const adambridge_hparams* hps, int32_t nsegs, int32_t threads);
+
+/* ---- HIP-specific entry points (no counterpart in the reference) ---------- */
+
+/* The HIP stream (a hipStream_t, e.g. torch.cuda.Stream.cuda_stream) on which
+ * the pool enqueues from now on.  Returns 0. */
+ADAMBRIDGE_API int adambridge_pool_set_stream(void* pool, void* stream);
+
+/* Block until the pool's stream has drained; returns ADAMBRIDGE_EHIP if a
+ * kernel of it failed. */
+ADAMBRIDGE_API int adambridge_pool_sync(void* pool);
+
+/* The calling thread's stream for pool == NULL calls and adambridge_fused_adamw. */
+ADAMBRIDGE_API int adambridge_set_stream(void* stream);
+
+/* Text of the calling thread's last HIP-side failure ("" if none). */
+ADAMBRIDGE_API const char* adambridge_last_error(void);
+
+/* Name of the device code this library carries, e.g. "hip/gfx950". */
+ADAMBRIDGE_API const char* adambridge_backend(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ADAMBRIDGE_HIP_H */
