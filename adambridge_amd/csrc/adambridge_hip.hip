@@ -2,7 +2,7 @@
 // and the C ABI declared in include/adambridge_hip.h.
 //
 // One launch updates every segment (tensor) of a call: the grid is a list of
-// tiles of kTile elements, each workgroup finds its segment by a binary search
+// tiles of L.tile elements, each workgroup finds its segment by a binary search
 // of the per-segment first-tile table (uniform, scalar loads), then streams its
 // tile once: reads the gradient, the master and the moments, updates them in
 // registers and writes the master, the moments and the bf16 working weight.
@@ -22,6 +22,7 @@
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -38,7 +39,10 @@
 namespace abh {
 
 constexpr int kThreads = 256;
-constexpr int64_t kTile = 8192;   // elements per workgroup (a multiple of kFp8Block and of 8 * kThreads)
+// Elements per workgroup: a launch parameter, a multiple of kTileQuantum (one pass of the FP8
+// kernel's 16 block groups, and of the two-element kernels' 256 lanes).  Larger tiles amortize
+// each workgroup's segment search; see the host's default.
+constexpr int64_t kTileQuantum = 2048;
 constexpr int kInline = 7;        // segments carried in the kernel arguments
 
 // Per-segment launch descriptor (device side), 144 bytes.
@@ -63,22 +67,30 @@ static_assert(sizeof(DevSeg) == 144, "DevSeg layout");
 constexpr uint32_t kVec = 1u, kSR = 2u;
 
 struct Launch {
-    const DevSeg* table;  // device table when nsegs > kInline
+    const DevSeg* table;     // device table when nsegs > kInline
+    const int64_t* starts;   // device: first tile of each segment (compact, for the search)
+    int64_t tile;            // elements per tile (multiple of kTileQuantum)
     int32_t nsegs;
     int32_t pad;
     DevSeg inl[kInline];
 };
-static_assert(sizeof(Launch) <= 1024 + 16, "kernel argument block");
+static_assert(sizeof(Launch) <= 1024 + 32, "kernel argument block");
 
 __device__ __forceinline__ const DevSeg* find_segment(const Launch& L, int64_t tile)
 {
-    const DevSeg* S = L.nsegs <= kInline ? L.inl : L.table;
     int lo = 0, hi = L.nsegs - 1;
+    if (L.nsegs <= kInline) {
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (L.inl[mid].tile_begin <= tile) lo = mid; else hi = mid - 1;
+        }
+        return L.inl + lo;
+    }
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
-        if (S[mid].tile_begin <= tile) lo = mid; else hi = mid - 1;
+        if (L.starts[mid] <= tile) lo = mid; else hi = mid - 1;
     }
-    return S + lo;
+    return L.table + lo;
 }
 
 // --------------------------------------------------------------- loads/stores
@@ -86,6 +98,7 @@ __device__ __forceinline__ const DevSeg* find_segment(const Launch& L, int64_t t
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 // Streaming accesses: every byte is touched once per step, so keep them out of the caches.
 template <typename T>
@@ -147,14 +160,14 @@ __device__ __forceinline__ void load_master8(const DevSeg& s, int64_t i, float (
 }
 
 // Rounds and stores 8 new master values; x becomes the values stored.
-template <int PT>
-__device__ __forceinline__ void store_master8(const DevSeg& s, int64_t i, float (&x)[8], bool sr, uint32_t idx)
+template <int PT, bool SR>
+__device__ __forceinline__ void store_master8(const DevSeg& s, int64_t i, float (&x)[8], uint32_t idx)
 {
     if constexpr (PT == DT_F24) {
         uint32_t hi[8], lo[2] = {0u, 0u};
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            const uint32_t b = f24_round(x[k], sr, sr ? hash32((idx + k) ^ s.seed_p) : 0u);
+            const uint32_t b = f24_round<SR>(x[k], SR ? hash32((idx + k) ^ s.seed_p) : 0u);
             x[k] = bitsf(b);
             hi[k] = b >> 16;
             lo[k >> 2] |= ((b >> 8) & 0xffu) << (8 * (k & 3));
@@ -166,14 +179,14 @@ __device__ __forceinline__ void store_master8(const DevSeg& s, int64_t i, float 
     }
 }
 
-template <int MV>
-__device__ __forceinline__ void store_moment8(void* base, int64_t i, const float (&x)[8], bool sr, uint32_t idx,
+template <int MV, bool SR>
+__device__ __forceinline__ void store_moment8(void* base, int64_t i, const float (&x)[8], uint32_t idx,
                                               uint32_t seed)
 {
     if constexpr (MV == DT_BF16) {
         uint32_t h[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) h[k] = bf16_store(x[k], sr, sr ? hash32((idx + k) ^ seed) : 0u);
+        for (int k = 0; k < 8; ++k) h[k] = bf16_store<SR>(x[k], SR ? hash32((idx + k) ^ seed) : 0u);
         store8_u16(base, i, h);
     } else {
         store8_f32(base, i, x);
@@ -193,6 +206,83 @@ __device__ __forceinline__ void store_out8(void* base, int64_t i, const float (&
     }
 }
 
+// ------------------------------------------------ two elements per lane
+//
+// The FP32/BF16-moment kernel gives each lane two consecutive elements: one
+// small access per buffer per lane.  Measured on MI355X this streams faster
+// than wider per-lane chunks (fewer bytes in flight per lane to distinct rows).
+
+template <int DT>
+__device__ __forceinline__ void load2(const void* base, int64_t i, float& x0, float& x1)
+{
+    if constexpr (DT == DT_BF16) {
+        const uint32_t w = ld(reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(base) + i));
+        x0 = bitsf(w << 16);
+        x1 = bitsf(w & 0xffff0000u);
+    } else {
+        const f32x2 w = ld(reinterpret_cast<const f32x2*>(static_cast<const float*>(base) + i));
+        x0 = w.x;
+        x1 = w.y;
+    }
+}
+
+__device__ __forceinline__ void store2_f32(void* base, int64_t i, float x0, float x1)
+{
+    st(reinterpret_cast<f32x2*>(static_cast<float*>(base) + i), f32x2{x0, x1});
+}
+
+__device__ __forceinline__ void store2_u16(void* base, int64_t i, uint32_t h0, uint32_t h1)
+{
+    st(reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(base) + i), h0 | (h1 << 16));
+}
+
+template <int PT>
+__device__ __forceinline__ void load_master2(const DevSeg& s, int64_t i, float& x0, float& x1)
+{
+    if constexpr (PT == DT_F24) {
+        const uint32_t h = ld(reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(s.p) + i));
+        const uint32_t l = ld(reinterpret_cast<const uint16_t*>(s.p_lo + i));
+        x0 = bitsf((h << 16) | ((l & 0xffu) << 8));
+        x1 = bitsf((h & 0xffff0000u) | (l & 0xff00u));
+    } else {
+        load2<DT_F32>(s.p, i, x0, x1);
+    }
+}
+
+// Rounds and stores two new master values; x0, x1 become the values stored.
+template <int PT, bool SR>
+__device__ __forceinline__ void store_master2(const DevSeg& s, int64_t i, float& x0, float& x1, uint32_t idx)
+{
+    if constexpr (PT == DT_F24) {
+        const uint32_t b0 = f24_round<SR>(x0, SR ? hash32(idx ^ s.seed_p) : 0u);
+        const uint32_t b1 = f24_round<SR>(x1, SR ? hash32((idx + 1) ^ s.seed_p) : 0u);
+        x0 = bitsf(b0);
+        x1 = bitsf(b1);
+        st(reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(s.p) + i), (b0 >> 16) | (b1 & 0xffff0000u));
+        st(reinterpret_cast<uint16_t*>(s.p_lo + i), (uint16_t)(((b0 >> 8) & 0xffu) | (b1 & 0xff00u)));
+    } else {
+        store2_f32(s.p, i, x0, x1);
+    }
+}
+
+template <int MV, bool SR>
+__device__ __forceinline__ void store_moment2(void* base, int64_t i, float x0, float x1, uint32_t idx, uint32_t seed)
+{
+    if constexpr (MV == DT_BF16) {
+        store2_u16(base, i, bf16_store<SR>(x0, SR ? hash32(idx ^ seed) : 0u),
+                   bf16_store<SR>(x1, SR ? hash32((idx + 1) ^ seed) : 0u));
+    } else {
+        store2_f32(base, i, x0, x1);
+    }
+}
+
+template <int OT>
+__device__ __forceinline__ void store_out2(void* base, int64_t i, float x0, float x1)
+{
+    if constexpr (OT == DT_BF16) store2_u16(base, i, bf16_rne(x0), bf16_rne(x1));
+    else if constexpr (OT == DT_F32) store2_f32(base, i, x0, x1);
+}
+
 // ------------------------------------------------------------ scalar access
 
 template <int DT>
@@ -210,11 +300,11 @@ __device__ __forceinline__ float load_master1(const DevSeg& s, int64_t i)
     else return static_cast<const float*>(s.p)[i];
 }
 
-template <int PT>
-__device__ __forceinline__ float store_master1(const DevSeg& s, int64_t i, float x, bool sr, uint32_t idx)
+template <int PT, bool SR>
+__device__ __forceinline__ float store_master1(const DevSeg& s, int64_t i, float x, uint32_t idx)
 {
     if constexpr (PT == DT_F24) {
-        const uint32_t b = f24_round(x, sr, sr ? hash32(idx ^ s.seed_p) : 0u);
+        const uint32_t b = f24_round<SR>(x, SR ? hash32(idx ^ s.seed_p) : 0u);
         static_cast<uint16_t*>(s.p)[i] = (uint16_t)(b >> 16);
         s.p_lo[i] = (uint8_t)(b >> 8);
         return bitsf(b);
@@ -224,10 +314,10 @@ __device__ __forceinline__ float store_master1(const DevSeg& s, int64_t i, float
     }
 }
 
-template <int MV>
-__device__ __forceinline__ void store_moment1(void* base, int64_t i, float x, bool sr, uint32_t r)
+template <int MV, bool SR>
+__device__ __forceinline__ void store_moment1(void* base, int64_t i, float x, uint32_t r)
 {
-    if constexpr (MV == DT_BF16) static_cast<uint16_t*>(base)[i] = (uint16_t)bf16_store(x, sr, r);
+    if constexpr (MV == DT_BF16) static_cast<uint16_t*>(base)[i] = (uint16_t)bf16_store<SR>(x, r);
     else static_cast<float*>(base)[i] = x;
 }
 
@@ -241,40 +331,40 @@ __device__ __forceinline__ void store_out1(void* base, int64_t i, float x)
 // ------------------------------------------------- FP32 / BF16 moment kernel
 
 // ALGO: AdamW or Lion; MV: moment storage (F32 / BF16); PT: master (F32 / F24);
-// GT: gradient (F32 / BF16); OT: working-weight output (NONE / F32 / BF16).
-template <int ALGO, int MV, int PT, int GT, int OT>
-__global__ __launch_bounds__(kThreads) void k_update(Launch L)
+// GT: gradient (F32 / BF16); OT: working-weight output (NONE / F32 / BF16);
+// SR: stochastic rounding of BF16 moments and an FP24 master.
+template <int ALGO, int MV, int PT, int GT, int OT, bool SR>
+__device__ __forceinline__ void update_tile(const DevSeg& s, int64_t tile, int64_t T)
 {
-    const int64_t tile = blockIdx.x;
-    const DevSeg& s = *find_segment(L, tile);
     const int64_t n = s.n, n_main = s.n_main;
-    const int64_t lo = (tile - s.tile_begin) * kTile;
-    const int64_t hi = lo + kTile < n ? lo + kTile : n;
-    const bool sr = (s.flags & kSR) != 0;
+    const int64_t lo = (tile - s.tile_begin) * T;
+    const int64_t hi = lo + T < n ? lo + T : n;
     const Coef c = s.c;
-    const int64_t nvec = (s.flags & kVec) ? (n_main & ~(int64_t)7) : 0;
+    const int64_t nvec = (s.flags & kVec) ? (n_main & ~(int64_t)1) : 0;
     int64_t vend = hi < nvec ? hi : nvec;
     if (vend < lo) vend = lo;
 
-    // whole groups of 8 elements, every one of them in the fused range
-    for (int64_t i = lo + threadIdx.x * 8; i < vend; i += kThreads * 8) {
+    // each workgroup streams one contiguous tile: pairs of elements, both in the fused range
+    for (int64_t i = lo + threadIdx.x * 2; i < vend; i += kThreads * 2) {
         const uint32_t idx = s.idx0 + (uint32_t)i;
-        float g[8], m[8], v[8], p[8];
-        load8<GT>(s.g, i, g);
-        load8<MV>(s.m, i, m);
-        if constexpr (ALGO == ALGO_ADAMW) load8<MV>(s.v, i, v);
-        load_master8<PT>(s, i, p);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            if constexpr (ALGO == ALGO_ADAMW) p[k] = adamw<true>(p[k], g[k], m[k], v[k], c);
-            else p[k] = lion(p[k], g[k], m[k], c);
+        float g0, g1, m0, m1, v0 = 0.0f, v1 = 0.0f, p0, p1;
+        load2<GT>(s.g, i, g0, g1);
+        load2<MV>(s.m, i, m0, m1);
+        if constexpr (ALGO == ALGO_ADAMW) load2<MV>(s.v, i, v0, v1);
+        load_master2<PT>(s, i, p0, p1);
+        if constexpr (ALGO == ALGO_ADAMW) {
+            p0 = adamw<true>(p0, g0, m0, v0, c);
+            p1 = adamw<true>(p1, g1, m1, v1, c);
+        } else {
+            p0 = lion(p0, g0, m0, c);
+            p1 = lion(p1, g1, m1, c);
         }
-        store_master8<PT>(s, i, p, sr, idx);
-        store_moment8<MV>(s.m, i, m, sr, idx, s.seed_m);
-        if constexpr (ALGO == ALGO_ADAMW) store_moment8<MV>(s.v, i, v, sr, idx, s.seed_v);
-        store_out8<OT>(s.out, i, p);
+        store_master2<PT, SR>(s, i, p0, p1, idx);
+        store_moment2<MV, SR>(s.m, i, m0, m1, idx, s.seed_m);
+        if constexpr (ALGO == ALGO_ADAMW) store_moment2<MV, SR>(s.v, i, v0, v1, idx, s.seed_v);
+        store_out2<OT>(s.out, i, p0, p1);
     }
-    // the rest one element per lane: misaligned buffers, ragged ends, the scalar tail
+    // the rest one element per lane: misaligned buffers, a ragged end, the scalar tail
     for (int64_t i = vend + threadIdx.x; i < hi; i += kThreads) {
         const uint32_t idx = s.idx0 + (uint32_t)i;
         const float g = load1<GT>(s.g, i);
@@ -283,14 +373,23 @@ __global__ __launch_bounds__(kThreads) void k_update(Launch L)
         if constexpr (ALGO == ALGO_ADAMW) {
             float v = load1<MV>(s.v, i);
             p = adamw_sel(p, g, m, v, c, i < n_main);
-            store_moment1<MV>(s.v, i, v, sr, sr ? hash32(idx ^ s.seed_v) : 0u);
+            store_moment1<MV, SR>(s.v, i, v, SR ? hash32(idx ^ s.seed_v) : 0u);
         } else {
             p = lion(p, g, m, c);
         }
-        p = store_master1<PT>(s, i, p, sr, idx);
-        store_moment1<MV>(s.m, i, m, sr, sr ? hash32(idx ^ s.seed_m) : 0u);
+        p = store_master1<PT, SR>(s, i, p, idx);
+        store_moment1<MV, SR>(s.m, i, m, SR ? hash32(idx ^ s.seed_m) : 0u);
         store_out1<OT>(s.out, i, p);
     }
+}
+
+template <int ALGO, int MV, int PT, int GT, int OT>
+__global__ __launch_bounds__(kThreads) void k_update(Launch L)
+{
+    const int64_t tile = blockIdx.x;
+    const DevSeg& s = *find_segment(L, tile);
+    if (s.flags & kSR) update_tile<ALGO, MV, PT, GT, OT, true>(s, tile, L.tile);
+    else update_tile<ALGO, MV, PT, GT, OT, false>(s, tile, L.tile);
 }
 
 // ------------------------------------------------------------ FP8 moment kernel
@@ -318,16 +417,11 @@ __device__ __forceinline__ float group16_max(float x)
     return x;
 }
 
-template <int ALGO, int PT, int GT, int OT>
-__global__ __launch_bounds__(kThreads) void k_update_fp8(Launch L)
+template <int ALGO, int PT, int GT, int OT, bool SR>
+__device__ __forceinline__ void update_tile_fp8(const DevSeg& s, int64_t tile, int64_t T)
 {
     constexpr bool kLion = ALGO == ALGO_LION;
-    const int64_t tile = blockIdx.x;
-    const DevSeg& s = *find_segment(L, tile);
     const int64_t n = s.n, n_main = s.n_main;
-    const int64_t lo = (tile - s.tile_begin) * kTile;
-    const int64_t hi = lo + kTile < n ? lo + kTile : n;
-    const bool sr = (s.flags & kSR) != 0;
     const bool vec = (s.flags & kVec) != 0;
     const Coef c = s.c;
     const int lane = threadIdx.x & 15;
@@ -335,6 +429,8 @@ __global__ __launch_bounds__(kThreads) void k_update_fp8(Launch L)
     uint8_t* const mq = static_cast<uint8_t*>(s.m);
     uint8_t* const vq = static_cast<uint8_t*>(s.v);
 
+    const int64_t lo = (tile - s.tile_begin) * T;
+    const int64_t hi = lo + T < n ? lo + T : n;
     // one 128-element block per 16-lane group; this lane holds elements e0 .. e0+7
     for (int64_t b0 = lo + group * kFp8Block; b0 < hi; b0 += (kThreads / 16) * kFp8Block) {
         const int64_t blk = b0 / kFp8Block;
@@ -377,13 +473,13 @@ __global__ __launch_bounds__(kThreads) void k_update_fp8(Launch L)
                                    : adamw_sel(p[k], g[k], mt[k], vt[k], c, e0 + k < n_main);
         }
         if (full) {
-            store_master8<PT>(s, e0, p, sr, idx);
+            store_master8<PT, SR>(s, e0, p, idx);
             store_out8<OT>(s.out, e0, p);
         } else {
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 if (e0 + k < n) {
-                    const float stored = store_master1<PT>(s, e0 + k, p[k], sr, idx + k);
+                    const float stored = store_master1<PT, SR>(s, e0 + k, p[k], idx + k);
                     store_out1<OT>(s.out, e0 + k, stored);
                 }
             }
@@ -414,10 +510,10 @@ __global__ __launch_bounds__(kThreads) void k_update_fp8(Launch L)
         for (int k = 0; k < 8; ++k) {
             const uint32_t ik = idx + k;
             const bool in = e0 + k < n;   // padding codes are zero
-            const uint32_t a = e4m3_encode(mt[k] / scm, sr, sr ? hash32(ik ^ s.seed_m) : 0u);
+            const uint32_t a = e4m3_encode<SR>(mt[k] / scm, SR ? hash32(ik ^ s.seed_m) : 0u);
             qm[k >> 2] |= (in ? a : 0u) << (8 * (k & 3));
             if constexpr (!kLion) {
-                const uint32_t b = e5m2_encode(vt[k] / scu, sr, sr ? hash32(ik ^ s.seed_v) : 0u);
+                const uint32_t b = e5m2_encode<SR>(vt[k] / scu, SR ? hash32(ik ^ s.seed_v) : 0u);
                 qv[k >> 2] |= (in ? b : 0u) << (8 * (k & 3));
             }
         }
@@ -433,6 +529,103 @@ __global__ __launch_bounds__(kThreads) void k_update_fp8(Launch L)
             if constexpr (!kLion) s.v_scale[blk] = scu;
         }
     }
+}
+
+template <int ALGO, int PT, int GT, int OT>
+__global__ __launch_bounds__(kThreads) void k_update_fp8(Launch L)
+{
+    const int64_t tile = blockIdx.x;
+    const DevSeg& s = *find_segment(L, tile);
+    if (s.flags & kSR) update_tile_fp8<ALGO, PT, GT, OT, true>(s, tile, L.tile);
+    else update_tile_fp8<ALGO, PT, GT, OT, false>(s, tile, L.tile);
+}
+
+// ------------------------------------------------- packed AdamW state kernel
+//
+// AdamW with an FP32 master and BF16 moments interleaved in HBM: for elements
+// 2k and 2k+1 of a segment, 16 bytes {p[2k], p[2k+1], m[2k] | m[2k+1] << 16,
+// v[2k] | v[2k+1] << 16}.  One 16-byte state access per lane instead of three
+// separate streams (master, m, v): fewer concurrent DRAM streams, measured
+// faster on MI355X.  s.p holds the state; s.p_lo the buffer that receives the
+// new state (the same pointer, or a second buffer when double-buffered).  The
+// arithmetic and rounding are those of the separate layout, element by element.
+
+__device__ __forceinline__ void adamw_pair_tail(const DevSeg& s, int64_t i, u32x4& x, float g0, float g1,
+                                                int nvalid, uint32_t idx, bool sr, int64_t n_main,
+                                                float& o0, float& o1)
+{
+    // slow path for a pair that holds a tail element or ends past n: element by element
+    float p[2] = {bitsf(x.x), bitsf(x.y)};
+    float m[2] = {bitsf(x.z << 16), bitsf(x.z & 0xffff0000u)};
+    float v[2] = {bitsf(x.w << 16), bitsf(x.w & 0xffff0000u)};
+    const float g[2] = {g0, g1};
+    uint32_t mh[2] = {x.z & 0xffffu, x.z >> 16}, vh[2] = {x.w & 0xffffu, x.w >> 16};
+    uint32_t pb[2] = {x.x, x.y};
+    for (int k = 0; k < nvalid; ++k) {
+        p[k] = adamw_sel(p[k], g[k], m[k], v[k], s.c, i + k < n_main);
+        pb[k] = fbits(p[k]);
+        mh[k] = sr ? bf16_store<true>(m[k], hash32((idx + k) ^ s.seed_m)) : bf16_store<false>(m[k], 0u);
+        vh[k] = sr ? bf16_store<true>(v[k], hash32((idx + k) ^ s.seed_v)) : bf16_store<false>(v[k], 0u);
+    }
+    x = u32x4{pb[0], pb[1], mh[0] | (mh[1] << 16), vh[0] | (vh[1] << 16)};
+    o0 = p[0];
+    o1 = p[1];
+}
+
+template <int GT, int OT, bool SR>
+__device__ __forceinline__ void update_tile_packed(const DevSeg& s, int64_t tile, int64_t T)
+{
+    const int64_t n = s.n, n_main = s.n_main;
+    const Coef c = s.c;
+    const u32x4* __restrict__ src = static_cast<const u32x4*>(s.p);
+    u32x4* __restrict__ dst = reinterpret_cast<u32x4*>(s.p_lo);
+    const bool vec = (s.flags & kVec) != 0;   // g and out allow 2-element access
+    const int64_t lo = (tile - s.tile_begin) * T;
+    const int64_t hi = lo + T < n ? lo + T : n;
+    for (int64_t i = lo + threadIdx.x * 2; i < hi; i += kThreads * 2) {
+        const int64_t pair = i >> 1;
+        const uint32_t idx = s.idx0 + (uint32_t)i;
+        u32x4 x = ld(src + pair);
+        const bool both = i + 2 <= n;
+        float g0 = 0.0f, g1 = 0.0f;
+        if (vec && both) load2<GT>(s.g, i, g0, g1);
+        else {
+            g0 = load1<GT>(s.g, i);
+            if (both) g1 = load1<GT>(s.g, i + 1);
+        }
+        float o0, o1;
+        if (i + 2 <= n_main) {
+            float p0 = bitsf(x.x), p1 = bitsf(x.y);
+            float m0 = bitsf(x.z << 16), m1 = bitsf(x.z & 0xffff0000u);
+            float v0 = bitsf(x.w << 16), v1 = bitsf(x.w & 0xffff0000u);
+            p0 = adamw<true>(p0, g0, m0, v0, c);
+            p1 = adamw<true>(p1, g1, m1, v1, c);
+            const uint32_t mw = bf16_store<SR>(m0, SR ? hash32(idx ^ s.seed_m) : 0u) |
+                                (bf16_store<SR>(m1, SR ? hash32((idx + 1) ^ s.seed_m) : 0u) << 16);
+            const uint32_t vw = bf16_store<SR>(v0, SR ? hash32(idx ^ s.seed_v) : 0u) |
+                                (bf16_store<SR>(v1, SR ? hash32((idx + 1) ^ s.seed_v) : 0u) << 16);
+            x = u32x4{fbits(p0), fbits(p1), mw, vw};
+            o0 = p0;
+            o1 = p1;
+        } else {
+            adamw_pair_tail(s, i, x, g0, g1, both ? 2 : 1, idx, SR, n_main, o0, o1);
+        }
+        st(dst + pair, x);
+        if (vec && both) store_out2<OT>(s.out, i, o0, o1);
+        else {
+            store_out1<OT>(s.out, i, o0);
+            if (both) store_out1<OT>(s.out, i + 1, o1);
+        }
+    }
+}
+
+template <int GT, int OT>
+__global__ __launch_bounds__(kThreads) void k_update_packed(Launch L)
+{
+    const int64_t tile = blockIdx.x;
+    const DevSeg& s = *find_segment(L, tile);
+    if (s.flags & kSR) update_tile_packed<GT, OT, true>(s, tile, L.tile);
+    else update_tile_packed<GT, OT, false>(s, tile, L.tile);
 }
 
 // ------------------------------------------------------------ kernel table
@@ -466,10 +659,34 @@ constexpr auto make_table(std::integer_sequence<int, I...>)
     return std::array<KernelFn, sizeof...(I)>{entry<I>()...};
 }
 
+// Packed-state kernels follow the table: index kNumKernels + gt * 3 + ot.
+constexpr int kNumPacked = 2 * 3;
+
+template <int I>
+constexpr KernelFn packed_entry()
+{
+    constexpr int ot = I % 3, gt = I / 3;
+    return &k_update_packed<gt ? DT_BF16 : DT_F32, ot == 0 ? DT_NONE : ot == 1 ? DT_F32 : DT_BF16>;
+}
+
+template <int... I>
+constexpr auto make_packed_table(std::integer_sequence<int, I...>)
+{
+    return std::array<KernelFn, sizeof...(I)>{packed_entry<I>()...};
+}
+
 static const auto kKernels = make_table(std::make_integer_sequence<int, kNumKernels>{});
+static const auto kPacked = make_packed_table(std::make_integer_sequence<int, kNumPacked>{});
+
+inline KernelFn kernel_at(int index)
+{
+    return index < kNumKernels ? kKernels[index] : kPacked[index - kNumKernels];
+}
 
 inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
 {
+    if (pt == DT_PACKED)
+        return kNumKernels + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
     const int mvi = mv == DT_F32 ? 0 : mv == DT_BF16 ? 1 : 2;
     const int pti = pt == DT_F24 ? 1 : 0;
     const int gti = gt == DT_BF16 ? 1 : 0;

@@ -38,7 +38,15 @@ extern "C" {
  * Algorithms, kernels.c:75: ALGO_ADAMW 0, ALGO_LION 1.
  * SIMD levels reproduced, kernels.c:74: 0 scalar, 1 AVX2 (8 lanes), 2 AVX-512 (16 lanes). */
 enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, ADAMBRIDGE_DT_FP8 = 3,
-       ADAMBRIDGE_DT_F24 = 4 };
+       ADAMBRIDGE_DT_F24 = 4, ADAMBRIDGE_DT_PACKED = 5 };
+
+/* ADAMBRIDGE_DT_PACKED (p_dtype; no counterpart in the reference): an HBM layout for
+ * AdamW with an FP32 master and BF16 moments (mv_dtype DT_BF16).  p points at 16-byte
+ * pairs: for elements 2k and 2k+1 of the segment, {p[2k], p[2k+1] (FP32),
+ * m[2k] | m[2k+1] << 16, v[2k] | v[2k+1] << 16 (BF16 bits)}, ceil(n/2) pairs, 16-byte
+ * aligned.  m and v are unused.  p_lo is NULL (update in place) or a second buffer of
+ * the same layout that receives the new state (double buffering).  Same arithmetic,
+ * rounding and rounding streams as the separate layout. */
 enum { ADAMBRIDGE_ALGO_ADAMW = 0, ADAMBRIDGE_ALGO_LION = 1 };
 
 /* Error codes (kernels.c:1537-1553, 1582-1584, 1620-1621), plus the HIP-side ones. */
@@ -57,6 +65,7 @@ enum {
     ADAMBRIDGE_EOFFSET = -11,      /* negative offset, or FP8 offset not a multiple of 128 */
     ADAMBRIDGE_EALGO = -12,
     ADAMBRIDGE_EPDTYPE = -13,
+    ADAMBRIDGE_EALIGN = -14,       /* a packed state buffer is not 16-byte aligned */
     ADAMBRIDGE_EHIP = -20,         /* a HIP runtime call failed; see adambridge_last_error() */
     ADAMBRIDGE_EDEVICE = -21       /* the pool belongs to another device than the current one */
 };
@@ -90,8 +99,10 @@ typedef struct adambridge_group {
 /* One tensor (or one chunk of one): kernels.c:747-769 (128 bytes).  The struct
  * itself is host memory; p .. out are device pointers. */
 typedef struct adambridge_segment {
-    void* p;                 /* FP32 master, or the FP24 hi plane (uint16) when p_dtype is DT_F24 */
-    uint8_t* p_lo;           /* FP24 lo plane (one byte per element); NULL for FP32 */
+    void* p;                 /* FP32 master, the FP24 hi plane (uint16) when p_dtype is DT_F24, or the
+                                packed state when p_dtype is DT_PACKED */
+    uint8_t* p_lo;           /* FP24 lo plane (one byte per element); NULL for FP32; DT_PACKED: the
+                                destination state (NULL: in place) */
     const void* g;           /* gradient, g_dtype */
     void* m;                 /* first moment, mv_dtype (FP8: E4M3 codes, padded to 128 per block) */
     void* v;                 /* second moment (FP8: E5M2 codes of sqrt(v)); unused by Lion */
@@ -107,7 +118,7 @@ typedef struct adambridge_segment {
     int32_t mv_dtype;
     int32_t out_dtype;
     int32_t algorithm;
-    int32_t p_dtype;         /* DT_F32 (or 0) or DT_F24 */
+    int32_t p_dtype;         /* DT_F32 (or 0), DT_F24, or DT_PACKED */
     int32_t reserved;
 } adambridge_segment;
 

@@ -102,3 +102,89 @@ def run_steps(case: O.Case, grads: list, runner, width: int) -> O.Case:
         state = runner([state], width)[0]
         state.step += 1
     return state
+
+
+def pack_state(case: O.Case) -> np.ndarray:
+    """Separate FP32 master + BF16 moments -> the interleaved layout (pairs x 4 uint32)."""
+    n = case.n
+    pairs = max(1, (n + 1) // 2)
+    out = np.zeros((pairs, 4), np.uint32)
+    p = np.zeros(2 * pairs, np.uint32)
+    p[:n] = case.arrays["p"].view(np.uint32)
+    m = np.zeros(2 * pairs, np.uint32)
+    m[:n] = case.arrays["m"]
+    v = np.zeros(2 * pairs, np.uint32)
+    v[:n] = case.arrays["v"]
+    out[:, 0], out[:, 1] = p[0::2], p[1::2]
+    out[:, 2] = m[0::2] | (m[1::2] << 16)
+    out[:, 3] = v[0::2] | (v[1::2] << 16)
+    return out
+
+
+def unpack_state(case: O.Case, state: np.ndarray) -> None:
+    """The interleaved layout -> the case's separate arrays (in place)."""
+    n = case.n
+    p = np.empty(2 * state.shape[0], np.uint32)
+    p[0::2], p[1::2] = state[:, 0], state[:, 1]
+    m = np.empty(2 * state.shape[0], np.uint32)
+    m[0::2], m[1::2] = state[:, 2] & 0xFFFF, state[:, 2] >> 16
+    v = np.empty(2 * state.shape[0], np.uint32)
+    v[0::2], v[1::2] = state[:, 3] & 0xFFFF, state[:, 3] >> 16
+    case.arrays["p"] = p[:n].view(np.float32).copy()
+    case.arrays["m"] = m[:n].astype(np.uint16)
+    case.arrays["v"] = v[:n].astype(np.uint16)
+
+
+def run_hip_packed(cases: list[O.Case], width: int = 16, double_buffer: bool = False,
+                   misalign_g: bool = False) -> list[O.Case]:
+    """Like run_hip for AdamW / FP32 master / BF16 moment cases, through the interleaved layout
+    (ADAMBRIDGE_DT_PACKED): pack on the host, one call, unpack the result."""
+    kernels = _hip.load()
+    work = [c.copy() for c in cases]
+    keep, segs = [], []
+    by_group = all(c.group is not None for c in work)
+    groups = []
+    for c in work:
+        assert c.algorithm == O.ADAMW and c.mv_dtype == O.DT_BF16 and c.p_dtype == O.DT_F32
+        state = torch.from_numpy(pack_state(c).view(np.int32)).cuda()
+        dst = torch.full_like(state, -1) if double_buffer else None
+        g = to_device(c.arrays["g"])
+        if misalign_g:
+            buf = torch.empty(g.numel() + 1, dtype=g.dtype, device=g.device)
+            buf[1:].copy_(g)
+            keep.append(buf)
+            g = buf[1:]
+        out = to_device(c.arrays["out"]) if "out" in c.arrays else None
+        keep += [state, dst, g, out]
+        grp = None
+        if by_group:
+            grp = _hip.Group(**{k: c.group[k] for k in ("lr", "beta1", "beta2", "eps", "weight_decay")},
+                             seed=c.group["seed"] & (2**64 - 1), stochastic=int(c.group["stochastic"]))
+        groups.append(grp)
+        segs.append(_hip.Segment(p=state.data_ptr(), p_lo=dst.data_ptr() if dst is not None else None,
+                                 g=g.data_ptr(), m=None, v=None, out=out.data_ptr() if out is not None else None,
+                                 group=ctypes.pointer(grp) if grp is not None else None, n=c.n, step=c.step,
+                                 index=c.index, offset=c.offset, g_dtype=c.g_dtype, mv_dtype=O.DT_BF16,
+                                 out_dtype=c.out_dtype, algorithm=0, p_dtype=_hip.DT_PACKED))
+    arr = kernels.segment_array([ctypes.pointer(s) for s in segs])
+    kernels.set_simd_level(WIDTH_LEVEL[width])
+    try:
+        kernels.set_stream(torch.cuda.current_stream())
+        if by_group:
+            kernels.multi_step(None, arr)
+        else:
+            hps = [_hip.HParams(**{k: c.hparams[k] for k, _ in _hip.HParams._fields_}) for c in work]
+            kernels.multi_apply(None, arr, hps)
+        torch.cuda.synchronize()
+    finally:
+        kernels.set_simd_level(None)
+    it = iter(keep)
+    for c in work:
+        if misalign_g:
+            next(it)
+        state, dst, g, out = next(it), next(it), next(it), next(it)
+        result = (dst if dst is not None else state).cpu().numpy().view(np.uint32)
+        unpack_state(c, result)
+        if out is not None:
+            c.arrays["out"] = from_device(out, c.arrays["out"])
+    return work

@@ -159,3 +159,68 @@ def test_rejects_bad_segments_before_touching_any():
     bad_dtype.g_dtype = 7
     with pytest.raises(RuntimeError, match=r"code -3"):
         run_hip([good, bad_dtype], 16)
+
+
+# ------------------------------------------------------ interleaved state layout
+
+from hip_cases import run_hip_packed  # noqa: E402
+
+
+@pytest.mark.parametrize("double_buffer", [False, True])
+def test_packed_layout_matches_oracle(double_buffer):
+    """ADAMBRIDGE_DT_PACKED (master + BF16 moments interleaved) gives the separate layout's bytes:
+    odd sizes, tails of every reproduced ISA, offsets, SR on/off, every grad/out dtype."""
+    rng = np.random.default_rng(21)
+    cases = []
+    for gt, ot, sr, n in itertools.product([O.DT_BF16, O.DT_F32], [O.DT_NONE, O.DT_F32, O.DT_BF16], [True, False],
+                                           [1, 2, 15, 16, 17, 33, 1000, 2048 + 77, 5001]):
+        cases.append(O.make_case(rng, n, mv_dtype=O.DT_BF16, p_dtype=O.DT_F32, g_dtype=gt, out_dtype=ot,
+                                 stochastic=sr, offset=int(rng.integers(0, 2**32)), index=int(rng.integers(0, 999)),
+                                 step=int(rng.integers(1, 30))))
+    for width in (16, 8, 0):
+        want = O.run_many(cases, "oracle", width)
+        got = run_hip_packed(cases, width, double_buffer=double_buffer)
+        for w, g in zip(want, got):
+            check(w, g)
+
+
+def test_packed_layout_misaligned_gradient_and_specials():
+    rng = np.random.default_rng(22)
+    cases = [O.make_case(rng, n, mv_dtype=O.DT_BF16, special=sp) for n in (999, 4096) for sp in (False, True)]
+    want = O.run_many(cases, "oracle", 16)
+    got = run_hip_packed(cases, 16, misalign_g=True)
+    for w, g, c in zip(want, got, cases):
+        bad = O.outputs_equal(w, g, nan_equiv=True)
+        assert not bad, bad
+
+
+def test_packed_layout_multi_step_groups():
+    rng = np.random.default_rng(23)
+    cases = [O.make_case(rng, 3000 + 7 * k, mv_dtype=O.DT_BF16, explicit=False, index=k, step=k + 2, seed=3)
+             for k in range(12)]
+    want = O.run_many(cases, "oracle", 16)
+    got = run_hip_packed(cases, 16)
+    for w, g in zip(want, got):
+        check(w, g)
+
+
+def test_packed_layout_rejects_bad_segments():
+    rng = np.random.default_rng(24)
+    lion = O.make_case(rng, 100, mv_dtype=O.DT_BF16)
+    lion.algorithm = O.LION
+    with pytest.raises(RuntimeError, match=r"code -12"):
+        run_hip_packed_unchecked(lion)
+
+
+def run_hip_packed_unchecked(case):
+    """One packed segment with whatever algorithm the case names (validation test)."""
+    import ctypes
+    from adambridge_amd import _hip
+    from hip_cases import pack_state, to_device
+    k = _hip.load()
+    state = torch.from_numpy(pack_state(case).view(np.int32)).cuda()
+    g = to_device(case.arrays["g"])
+    seg = _hip.Segment(p=state.data_ptr(), g=g.data_ptr(), n=case.n, step=1, mv_dtype=O.DT_BF16,
+                       g_dtype=case.g_dtype, out_dtype=0, algorithm=case.algorithm, p_dtype=_hip.DT_PACKED)
+    hp = _hip.HParams(**{kk: case.hparams[kk] for kk, _ in _hip.HParams._fields_})
+    k.multi_apply(None, k.segment_array([ctypes.pointer(seg)]), [hp])

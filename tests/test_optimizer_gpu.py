@@ -1,0 +1,812 @@
+"""AdamBridge / LionBridge on the GPU: the reference's behavioural suite
+(tests/test_optimizer.py, test_lion.py, test_master24.py, test_cuda.py) on
+parameters in HBM, plus end-to-end bit-exactness of the API path against the
+oracle (parameter index, step counting, lazy state and seeds included).
+"""
+
+import copy
+import ctypes
+import io
+
+import numpy as np
+import pytest
+import torch
+
+import adambridge_amd as ab
+from conftest import max_param_diff, tiny_mlp
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def train(model, opt, steps, seed=1, batch=16, hooks=False):
+    torch.manual_seed(seed)
+    losses = []
+    for _ in range(steps):
+        x = torch.randn(batch, 48, device=DEV, dtype=next(model.parameters()).dtype)
+        opt.zero_grad()
+        loss = model(x).float().pow(2).mean()
+        loss.backward()
+        if hooks:
+            opt.step_sync()
+        else:
+            opt.step()
+        losses.append(loss.item())
+    return losses
+
+
+class RefLion(torch.optim.Optimizer):
+    """Lion as published: p -= lr * (sign(b1 m + (1-b1) g) + wd p); m = b2 m + (1-b2) g."""
+
+    def __init__(self, params, lr=1e-4, betas=(0.9, 0.99), weight_decay=0.0):
+        super().__init__(params, dict(lr=lr, betas=betas, weight_decay=weight_decay))
+
+    @torch.no_grad()
+    def step(self):
+        for group in self.param_groups:
+            b1, b2 = group["betas"]
+            for p in group["params"]:
+                if p.grad is None:
+                    continue
+                m = self.state[p].setdefault("m", torch.zeros_like(p))
+                c = m * b1 + p.grad * (1 - b1)
+                p.mul_(1 - group["lr"] * group["weight_decay"]).add_(c.sign(), alpha=-group["lr"])
+                m.mul_(b2).add_(p.grad, alpha=1 - b2)
+
+
+class TinyLM(torch.nn.Module):
+    """Embedding + blocks + tied head (reference tests/test_cuda.py:15-31)."""
+
+    def __init__(self, vocab=97, dim=64, layers=4):
+        super().__init__()
+        self.emb = torch.nn.Embedding(vocab, dim)
+        self.blocks = torch.nn.ModuleList(
+            torch.nn.Sequential(torch.nn.LayerNorm(dim), torch.nn.Linear(dim, 4 * dim), torch.nn.GELU(),
+                                torch.nn.Linear(4 * dim, dim)) for _ in range(layers))
+        self.norm = torch.nn.LayerNorm(dim)
+
+    def forward(self, tokens):
+        h = self.emb(tokens)
+        for blk in self.blocks:
+            h = h + blk(h)
+        return self.norm(h) @ self.emb.weight.t()
+
+
+def lm_loss(model, seed):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    tokens = torch.randint(0, 97, (8, 33), device=DEV, generator=g)
+    logits = model(tokens[:, :-1])
+    return torch.nn.functional.cross_entropy(logits.float().reshape(-1, logits.shape[-1]), tokens[:, 1:].reshape(-1))
+
+
+# ------------------------------------------------------- against torch AdamW
+
+def test_matches_torch_adamw_with_groups_and_scheduler():
+    """reference test_optimizer.py:27-51, FP32 parameters on the GPU."""
+    ref_model = tiny_mlp(device=DEV)
+    model = copy.deepcopy(ref_model)
+
+    def groups(m):
+        return [{"params": [m[0].weight, m[3].weight], "weight_decay": 0.1},
+                {"params": [m[0].bias, m[2].weight, m[2].bias, m[3].bias], "weight_decay": 0.0, "lr": 3e-3}]
+
+    ref = torch.optim.AdamW(groups(ref_model), lr=1e-2, betas=(0.8, 0.99))
+    opt = ab.AdamBridge(groups(model), lr=1e-2, betas=(0.8, 0.99))
+    sched_ref = torch.optim.lr_scheduler.StepLR(ref, step_size=3, gamma=0.5)
+    sched = torch.optim.lr_scheduler.StepLR(opt, step_size=3, gamma=0.5)
+    torch.manual_seed(1)
+    for _ in range(10):
+        x = torch.randn(16, 48, device=DEV)
+        for m, o, s in ((ref_model, ref, sched_ref), (model, opt, sched)):
+            o.zero_grad()
+            m(x).pow(2).mean().backward()
+            o.step()
+            s.step()
+    assert max_param_diff(ref_model, model) < 1e-6
+    assert opt.backend == "hip/gfx950"
+    opt.close()
+
+
+def test_sync_step_with_clipping():
+    """clip_grad_norm_ before step() is seen: grads are read at step (reference test_cuda.py:273-287)."""
+    torch.manual_seed(0)
+    ref_model = TinyLM().to(DEV)
+    model = copy.deepcopy(ref_model)
+    ref = torch.optim.AdamW(ref_model.parameters(), lr=3e-3)
+    opt = ab.AdamBridge(model.parameters(), lr=3e-3)
+    for step in range(5):
+        for m, o in ((ref_model, ref), (model, opt)):
+            o.zero_grad()
+            lm_loss(m, step).backward()
+            torch.nn.utils.clip_grad_norm_(m.parameters(), 0.1)
+            o.step()
+    assert max_param_diff(ref_model, model) < 1e-5
+    opt.close()
+
+
+@pytest.mark.parametrize("overlap", [True, False])
+def test_async_hooks_match_torch_adamw(overlap):
+    """reference test_cuda.py:41-62."""
+    torch.manual_seed(0)
+    ref_model = TinyLM().to(DEV)
+    model = copy.deepcopy(ref_model)
+    ref = torch.optim.AdamW(ref_model.parameters(), lr=3e-3)
+    opt = ab.AdamBridge(model.parameters(), lr=3e-3, overlap_writeback=overlap).attach_hooks(model)
+    for step in range(8):
+        ref.zero_grad()
+        lm_loss(ref_model, step).backward()
+        ref.step()
+        opt.zero_grad()
+        lm_loss(model, step).backward()
+        assert all(p.grad is None for p in model.parameters() if p.numel() >= opt.small_param_threshold)
+        stats = opt.step_sync()
+        assert all(p.grad is None for p in model.parameters())
+        assert stats.num_updates == len(list(model.parameters()))
+    assert max_param_diff(ref_model, model) < 1e-5
+    opt.close()
+
+
+@pytest.mark.parametrize("threshold", [0, 2000, 10**9])
+def test_hooked_and_grouped_parameters_match_torch_adamw(threshold):
+    """reference test_cuda.py:65-83."""
+    torch.manual_seed(0)
+    ref_model = TinyLM().to(DEV)
+    model = copy.deepcopy(ref_model)
+    ref = torch.optim.AdamW(ref_model.parameters(), lr=3e-3)
+    opt = ab.AdamBridge(model.parameters(), lr=3e-3, small_param_threshold=threshold).attach_hooks(model)
+    for step in range(6):
+        ref.zero_grad()
+        lm_loss(ref_model, step).backward()
+        ref.step()
+        lm_loss(model, step).backward()
+        opt.step_sync()
+    assert max_param_diff(ref_model, model) < 1e-5
+    opt.close()
+
+
+def _stale_reference(model, steps, make_opt, warmup):
+    """Losses and final weights of an optimizer whose updates reach the model one step late after
+    ``warmup`` exact steps (reference test_cuda.py:129-152)."""
+    master = copy.deepcopy(model).float()
+    ref = make_opt(master.parameters())
+    snapshots = [[p.detach().clone() for p in master.parameters()]]
+    losses = []
+    for k in range(1, steps + 1):
+        lag = k - 1 if k <= warmup + 1 else k - 2
+        with torch.no_grad():
+            for p, w in zip(model.parameters(), snapshots[lag]):
+                p.copy_(w)
+        model.zero_grad()
+        loss = lm_loss(model, k)
+        loss.backward()
+        losses.append(loss.item())
+        for p, q in zip(master.parameters(), model.parameters()):
+            p.grad = q.grad.float()
+        ref.step()
+        snapshots.append([p.detach().clone() for p in master.parameters()])
+    return losses, snapshots[-1]
+
+
+@pytest.mark.parametrize("warmup", [0, 3])
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_delayed_updates_match_one_step_stale_adamw(warmup, precision):
+    """reference test_cuda.py:155-177."""
+    torch.manual_seed(0)
+    model = TinyLM().to(DEV)
+    want_losses, want = _stale_reference(copy.deepcopy(model), 10, lambda ps: torch.optim.AdamW(ps, lr=3e-3), warmup)
+    opt = ab.AdamBridge(model.parameters(), lr=3e-3, precision=precision, delay_updates=True,
+                        delay_warmup_steps=warmup, small_param_threshold=2000).attach_hooks(model)
+    assert any(s.small is not None for s in opt._ordered) and any(s.small is None for s in opt._ordered)
+    losses = []
+    for k in range(1, 11):
+        loss = lm_loss(model, k)
+        loss.backward()
+        opt.step_sync()
+        losses.append(loss.item())
+    opt.flush()
+    tol = 1e-4 if precision == "fp32" else 2e-2
+    assert max(abs(a - b) for a, b in zip(losses, want_losses)) < tol
+    assert max((p - w).abs().max().item() for p, w in zip(model.parameters(), want)) < (
+        1e-5 if precision == "fp32" else 1e-2)
+    opt.close()
+
+
+def test_delayed_updates_state_dict_close_and_unused_params():
+    """reference test_cuda.py:180-209."""
+    torch.manual_seed(0)
+    model = TinyLM().to(DEV)
+    opt = ab.AdamBridge(model.parameters(), lr=1e-2, delay_updates=True, small_param_threshold=0).attach_hooks(model)
+    head = model.blocks[-1][3].weight
+    for k in range(3):
+        lm_loss(model, k).backward()
+        opt.step_sync()
+    before = head.detach().clone()
+    head.requires_grad_(False)
+    lm_loss(model, 3).backward()
+    opt.step_sync()
+    torch.cuda.synchronize()
+    assert not torch.equal(head, before)
+    assert torch.equal(head.detach().reshape(-1), opt._slots[head].master.to_fp32())
+    head.requires_grad_(True)
+    lm_loss(model, 4).backward()
+    opt.step_sync()
+    opt.state_dict()
+    torch.cuda.synchronize()
+    for p, master in zip(model.parameters(), opt.master_params()):
+        assert torch.equal(p.detach().reshape(-1), master)
+    lm_loss(model, 5).backward()
+    opt.step_sync()
+    opt.close()
+    torch.cuda.synchronize()
+    for p, master in zip(model.parameters(), opt.master_params()):
+        assert torch.equal(p.detach().reshape(-1), master)
+
+
+@pytest.mark.parametrize("delay", [False, True])
+def test_lion_hooks_match_reference(delay):
+    """reference test_cuda.py:212-232."""
+    torch.manual_seed(0)
+    model = TinyLM().to(DEV)
+    want_losses, want = _stale_reference(copy.deepcopy(model), 6, lambda ps: RefLion(ps, lr=1e-3, weight_decay=0.1),
+                                         warmup=10**9 if not delay else 0)
+    opt = ab.LionBridge(model.parameters(), lr=1e-3, weight_decay=0.1, delay_updates=delay).attach_hooks(model)
+    losses = []
+    for k in range(1, 7):
+        loss = lm_loss(model, k)
+        loss.backward()
+        opt.step_sync()
+        losses.append(loss.item())
+    opt.flush()
+    assert max(abs(a - b) for a, b in zip(losses, want_losses)) < 1e-5
+    assert max((p - w).abs().max().item() for p, w in zip(model.parameters(), want)) < 1e-6
+    assert all(s.v is None for s in opt._ordered)
+    opt.close()
+
+
+def test_lion_matches_reference_with_groups():
+    """reference test_lion.py:46-60."""
+    ref_model = tiny_mlp(device=DEV)
+    model = copy.deepcopy(ref_model)
+
+    def groups(m):
+        return [{"params": [m[0].weight, m[3].weight], "weight_decay": 0.5},
+                {"params": [m[0].bias, m[2].weight, m[2].bias, m[3].bias], "lr": 3e-4}]
+
+    ref = RefLion(groups(ref_model), lr=1e-3, betas=(0.9, 0.99), weight_decay=0.0)
+    opt = ab.LionBridge(groups(model), lr=1e-3, betas=(0.9, 0.99))
+    train(ref_model, ref, 10)
+    train(model, opt, 10)
+    assert max_param_diff(ref_model, model) < 1e-6
+    n = sum(p.numel() for p in model.parameters())
+    assert opt.memory_report()["moments"] == 4 * n
+    assert opt.expected_bytes_per_param() == 8.0
+    sd = opt.state_dict()
+    assert sd["adambridge"]["algorithm"] == "lion"
+    assert all("exp_avg" in st and "exp_avg_sq" not in st for st in sd["state"].values())
+    opt.close()
+
+
+def test_lion_no_eps():
+    with pytest.raises(TypeError):
+        ab.LionBridge(tiny_mlp(device=DEV).parameters(), eps=1e-8)
+
+
+@pytest.mark.parametrize("window", [3, 2])
+def test_accumulation_steps_match_accumulated_adamw(window):
+    """reference test_lion.py:132-153 (AdamW with accumulation_steps)."""
+    ref_model = tiny_mlp(device=DEV)
+    model = copy.deepcopy(ref_model)
+    ref = torch.optim.AdamW(ref_model.parameters(), lr=1e-2)
+    opt = ab.AdamBridge(model.parameters(), lr=1e-2, accumulation_steps=3, small_param_threshold=0).attach_hooks(model)
+    torch.manual_seed(1)
+    for _ in range(4):
+        xs = [torch.randn(8, 48, device=DEV) for _ in range(window)]
+        ref.zero_grad()
+        for x in xs:
+            (ref_model(x).pow(2).mean() / window).backward()
+        ref.step()
+        for x in xs:
+            (model(x).pow(2).mean() / window).backward()
+        opt.step_sync()
+        opt.zero_grad()
+    assert max_param_diff(ref_model, model) < 1e-6
+    opt.close()
+
+
+def test_gradient_accumulation_with_no_sync():
+    """reference test_cuda.py:311-330."""
+    torch.manual_seed(0)
+    ref_model = TinyLM().to(DEV)
+    model = copy.deepcopy(ref_model)
+    ref = torch.optim.AdamW(ref_model.parameters(), lr=3e-3)
+    opt = ab.AdamBridge(model.parameters(), lr=3e-3).attach_hooks(model)
+    for step in range(3):
+        ref.zero_grad()
+        for micro in range(3):
+            (lm_loss(ref_model, 10 * step + micro) / 3).backward()
+        ref.step()
+        for micro in range(3):
+            if micro < 2:
+                with opt.no_sync():
+                    (lm_loss(model, 10 * step + micro) / 3).backward()
+            else:
+                (lm_loss(model, 10 * step + micro) / 3).backward()
+        opt.step_sync()
+    assert max_param_diff(ref_model, model) < 1e-5
+    opt.close()
+
+
+def test_bf16_params_keep_fp32_master():
+    """reference test_cuda.py:290-308: bf16 weights are the RNE of the stored master."""
+    torch.manual_seed(0)
+    model = TinyLM().to(DEV).to(torch.bfloat16)
+    opt = ab.AdamBridge(model.parameters(), lr=3e-3, precision="bf16").attach_hooks(model)
+    losses = []
+    for step in range(30):
+        loss = lm_loss(model, step % 4)
+        loss.backward()
+        opt.step_sync()
+        losses.append(loss.item())
+    assert losses[-1] < losses[0] - 0.5
+    for p, master in zip(model.parameters(), opt.master_params()):
+        assert p.dtype == torch.bfloat16 and master.dtype == torch.float32
+        assert torch.equal(p.reshape(-1), master.to(torch.bfloat16))
+    rep = opt.memory_report()
+    n = sum(p.numel() for p in model.parameters())
+    assert rep["master"] == 4 * n and rep["moments"] == 4 * n
+    opt.close()
+
+
+def test_weights_visible_to_next_forward_without_host_sync():
+    """reference test_cuda.py:333-348: step_sync orders the update on the current stream."""
+    torch.manual_seed(0)
+    model = tiny_mlp(device=DEV)
+    opt = ab.AdamBridge(model.parameters(), lr=0.5).attach_hooks(model)
+    x = torch.randn(4, 48, device=DEV)
+    model(x).sum().backward()
+    opt.step_sync()
+    after = [p.clone() for p in model.parameters()]
+    torch.cuda.synchronize()
+    for p, q in zip(model.parameters(), after):
+        assert torch.equal(p, q)
+    opt.close()
+
+
+def test_params_without_grad_are_skipped():
+    """reference test_optimizer.py:77-85."""
+    model = tiny_mlp(device=DEV)
+    frozen = model[0].weight.detach().clone()
+    model[0].weight.requires_grad_(False)
+    opt = ab.AdamBridge(model.parameters(), lr=1e-2)
+    train(model, opt, 2)
+    assert torch.equal(model[0].weight, frozen)
+    assert opt.master_params()[0] is None
+    opt.close()
+
+
+def test_weights_loaded_after_construction_are_respected():
+    """reference test_optimizer.py:141-150: lazy master."""
+    model = tiny_mlp(seed=0, device=DEV)
+    opt = ab.AdamBridge(model.parameters(), lr=0.0, weight_decay=0.0)
+    pretrained = tiny_mlp(seed=42, device=DEV)
+    model.load_state_dict(pretrained.state_dict())
+    train(model, opt, 1)
+    assert max_param_diff(model, pretrained) == 0
+    opt.close()
+
+
+@pytest.mark.parametrize("precision", ["fp32", "bf16", "fp8"])
+def test_state_dict_resume_is_exact(precision):
+    """reference test_optimizer.py:88-118 (bf16 parameters so the master is a separate buffer)."""
+    torch.manual_seed(0)
+    base = tiny_mlp(device=DEV, dtype=torch.bfloat16)
+    a = copy.deepcopy(base)
+    opt_a = ab.AdamBridge(a.parameters(), lr=1e-2, precision=precision, seed=7)
+    train(a, opt_a, 6, seed=3)
+    b = copy.deepcopy(base)
+    opt_b = ab.AdamBridge(b.parameters(), lr=1e-2, precision=precision, seed=7)
+    train(b, opt_b, 3, seed=3)
+    buf = io.BytesIO()
+    torch.save({"model": b.state_dict(), "opt": opt_b.state_dict()}, buf)
+    buf.seek(0)
+    ckpt = torch.load(buf, weights_only=True)
+    c = tiny_mlp(seed=123, device=DEV, dtype=torch.bfloat16)
+    opt_c = ab.AdamBridge(c.parameters(), lr=1e-2, precision=precision, seed=7)
+    c.load_state_dict(ckpt["model"])
+    opt_c.load_state_dict(ckpt["opt"])
+    torch.manual_seed(3)
+    for _ in range(3):
+        torch.randn(16, 48, device=DEV, dtype=torch.bfloat16)
+    for _ in range(3):
+        x = torch.randn(16, 48, device=DEV, dtype=torch.bfloat16)
+        opt_c.zero_grad()
+        c(x).float().pow(2).mean().backward()
+        opt_c.step()
+    assert max_param_diff(a, c) == 0
+    for x, y in zip(opt_a.master_params(), opt_c.master_params()):
+        assert torch.equal(x, y)
+    for o in (opt_a, opt_b, opt_c):
+        o.close()
+
+
+@pytest.mark.parametrize("prec", ["fp32", "fp8"])
+def test_load_torch_adamw_checkpoint(prec):
+    """reference test_optimizer.py:121-138."""
+    ref_model = tiny_mlp(device=DEV)
+    ref = torch.optim.AdamW(ref_model.parameters(), lr=1e-2)
+    train(ref_model, ref, 3)
+    model = copy.deepcopy(ref_model)
+    opt = ab.AdamBridge(model.parameters(), lr=1e-2, precision=prec)
+    opt.load_state_dict(ref.state_dict())
+    for slot, p in zip(opt._ordered, ref_model.parameters()):
+        assert slot.step == 3 and slot.m.precision == prec
+        m_ref = ref.state[p]["exp_avg"].reshape(-1)
+        tol = 1e-7 if prec == "fp32" else 0.07 * m_ref.abs().max().item()
+        assert (slot.m.to_fp32() - m_ref).abs().max().item() <= tol
+    train(ref_model, ref, 3, seed=5)
+    train(model, opt, 3, seed=5)
+    assert max_param_diff(ref_model, model) < (1e-6 if prec == "fp32" else 1e-2)
+    opt.close()
+
+
+@pytest.mark.parametrize("hooks", [False, True])
+def test_set_precision_mid_training(hooks):
+    """reference test_optimizer.py:153-166."""
+    model = tiny_mlp(device=DEV)
+    opt = ab.AdamBridge(model.parameters(), lr=1e-2)
+    if hooks:
+        opt.attach_hooks(model)
+    train(model, opt, 2, hooks=hooks)
+    m_before = [s.m.to_fp32() for s in opt._ordered]
+    opt.set_precision("bf16_moments")
+    for s, m in zip(opt._ordered, m_before):
+        assert s.m.precision == "bf16"
+        torch.testing.assert_close(s.m.to_fp32(), m, rtol=2**-8, atol=0)
+    train(model, opt, 2, hooks=hooks)
+    opt.close()
+
+
+@pytest.mark.parametrize("prec", ["bf16", "fp8"])
+def test_low_precision_moments_converge_like_fp32(prec):
+    """reference test_optimizer.py:169-191."""
+    torch.manual_seed(0)
+    w_true = torch.randn(64, 16, device=DEV)
+    x_all = torch.randn(2048, 64, device=DEV)
+    y_all = x_all @ w_true + 0.01 * torch.randn(2048, 16, device=DEV)
+
+    def run(precision):
+        torch.manual_seed(1)
+        lin = torch.nn.Linear(64, 16).to(DEV)
+        opt = ab.AdamBridge(lin.parameters(), lr=1e-2, weight_decay=0.0, precision=precision)
+        for _ in range(1200):
+            idx = torch.randint(0, 2048, (64,), device=DEV)
+            opt.zero_grad()
+            (lin(x_all[idx]) - y_all[idx]).pow(2).mean().backward()
+            opt.step()
+        opt.close()
+        return (lin(x_all) - y_all).pow(2).mean().item()
+
+    base, low = run("fp32"), run(prec)
+    assert base < 2e-4
+    assert low < 1.2 * base
+
+
+def test_double_backward_without_no_sync_raises():
+    """reference test_optimizer.py:194-202."""
+    model = tiny_mlp(device=DEV)
+    opt = ab.AdamBridge(model.parameters(), release_grads=False, small_param_threshold=0).attach_hooks(model)
+    x = torch.randn(4, 48, device=DEV)
+    model(x).sum().backward()
+    with pytest.raises(RuntimeError, match="no_sync"):
+        model(x).sum().backward()
+    opt.step_sync()
+    opt.close()
+
+
+def test_hooks_match_step():
+    """reference test_optimizer.py:205-214: same bytes whichever way the update is driven."""
+    a, b = tiny_mlp(device=DEV), tiny_mlp(device=DEV)
+    opt_a = ab.AdamBridge(a.parameters(), lr=1e-2)
+    opt_b = ab.AdamBridge(b.parameters(), lr=1e-2).attach_hooks(b)
+    train(a, opt_a, 4)
+    train(b, opt_b, 4, hooks=True)
+    assert max_param_diff(a, b) == 0
+    assert all(p.grad is None for p in b.parameters())
+    opt_a.close()
+    opt_b.close()
+
+
+def test_errors_surface_in_step():
+    """reference test_optimizer.py:217-224: a bad group fails the step with a RuntimeError."""
+    model = tiny_mlp(device=DEV)
+    opt = ab.AdamBridge(model.parameters())
+    model(torch.randn(2, 48, device=DEV)).sum().backward()
+    opt.param_groups[0]["betas"] = None
+    with pytest.raises(RuntimeError, match="update failed"):
+        opt.step()
+    opt.close()
+
+
+def test_cpu_parameters_are_refused():
+    model = tiny_mlp()
+    opt = ab.AdamBridge(model.parameters())
+    model(torch.randn(2, 48)).sum().backward()
+    with pytest.raises(RuntimeError, match="update failed"):
+        opt.step()
+    opt.close()
+
+
+# ------------------------------------------------------------------ FP24
+
+def _bf16_model(seed=0):
+    return tiny_mlp(seed, dtype=torch.bfloat16, device=DEV)
+
+
+def _same_grad_train(pairs, steps, hooks=False):
+    """Every optimizer gets the same gradients (reference test_master24.py:22-37)."""
+    g = torch.Generator().manual_seed(1)
+    for _ in range(steps):
+        grads = [(torch.randn(p.shape, generator=g) * 0.1).to(device=DEV, dtype=torch.bfloat16)
+                 for p in pairs[0][0].parameters()]
+        for model, opt in pairs:
+            sum((p * grad).sum() for p, grad in zip(model.parameters(), grads)).backward()
+            if hooks:
+                opt.step_sync()
+            else:
+                opt.step()
+                opt.zero_grad(set_to_none=True)
+
+
+@pytest.mark.parametrize("hooks", [False, True])
+@pytest.mark.parametrize("precision", ["fp32", "fp8"])
+def test_fp24_master_tracks_the_fp32_master(precision, hooks):
+    """reference test_master24.py:40-54 and 116-129."""
+    a, b = _bf16_model(), _bf16_model()
+    kw = dict(lr=1e-2, weight_decay=0.0, small_param_threshold=0, precision=precision)
+    opt_a, opt_b = ab.AdamBridge(a.parameters(), **kw), ab.AdamBridge(b.parameters(), master_precision="fp24", **kw)
+    if hooks:
+        opt_a.attach_hooks(a)
+        opt_b.attach_hooks(b)
+    assert opt_b.expected_bytes_per_param() == opt_a.expected_bytes_per_param() - 1
+    _same_grad_train([(a, opt_a), (b, opt_b)], 20, hooks=hooks)
+    for ma, mb in zip(opt_a.master_params(), opt_b.master_params()):
+        assert ((ma - mb).abs() <= ma.abs() * 1e-3 + 1e-5).all()
+    assert max_param_diff(a, b) <= 2**-7
+    n = sum(p.numel() for p in b.parameters())
+    assert opt_b.memory_report()["master"] == 3 * n
+    assert opt_a.memory_report()["master"] == 4 * n
+    opt_a.close()
+    opt_b.close()
+
+
+def test_fp24_checkpoints_round_trip_and_convert():
+    """reference test_master24.py:67-95."""
+    kw = dict(lr=1e-2, weight_decay=0.0, small_param_threshold=0, precision="bf16")
+    model = _bf16_model()
+    opt = ab.AdamBridge(model.parameters(), master_precision="fp24", **kw)
+    _same_grad_train([(model, opt)], 3)
+    sd = opt.state_dict()
+    assert sd["adambridge"]["master_precision"] == "fp24"
+    saved = sd["state"][0]["master"]
+    assert saved["precision"] == "fp24" and saved["hi"].dtype == torch.bfloat16 and saved["lo"].dtype == torch.uint8
+    masters = [m.clone() for m in opt.master_params()]
+
+    def loaded(master_precision, state):
+        other = ab.AdamBridge(_bf16_model(1).parameters(), master_precision=master_precision, **kw)
+        other.load_state_dict(state)
+        return other
+
+    same = loaded("fp24", sd)
+    as32 = loaded("fp32", sd)
+    back = loaded("fp24", as32.state_dict())
+    for other in (same, as32, back):
+        for x, y in zip(masters, other.master_params()):
+            assert torch.equal(x, y)
+        assert other._ordered[0].step == 3
+        other.close()
+    opt.close()
+
+
+def test_bad_checkpoints_are_rejected_whole():
+    """reference test_master24.py:98-113 and test_lion.py:117-121."""
+    kw = dict(lr=1e-2, small_param_threshold=0)
+    model = _bf16_model()
+    opt = ab.AdamBridge(model.parameters(), master_precision="fp24", **kw)
+    _same_grad_train([(model, opt)], 1)
+    sd = opt.state_dict()
+    n = sd["state"][0]["master"]["hi"].numel()
+    for bad_master in ({"precision": "fp24", "hi": torch.zeros(1, dtype=torch.bfloat16),
+                        "lo": torch.zeros(n, dtype=torch.uint8)},
+                       {"precision": "fp24", "hi": torch.zeros(n, dtype=torch.bfloat16),
+                        "lo": torch.zeros(n, dtype=torch.int8)},
+                       {"precision": "fp16", "hi": torch.zeros(n, dtype=torch.bfloat16)}):
+        bad = {**sd, "state": {**sd["state"], 0: {**sd["state"][0], "master": bad_master}}}
+        other = ab.AdamBridge(_bf16_model(1).parameters(), master_precision="fp24", **kw)
+        with pytest.raises(ValueError):
+            other.load_state_dict(bad)
+        other.load_state_dict(sd)
+        other.close()
+    opt.close()
+
+
+def test_adamw_refuses_a_lion_checkpoint():
+    model = _bf16_model()
+    lion = ab.LionBridge(model.parameters(), lr=1e-3)
+    train(model, lion, 2)
+    sd = lion.state_dict()
+    adam = ab.AdamBridge(_bf16_model().parameters())
+    with pytest.raises(ValueError, match="exp_avg_sq"):
+        adam.load_state_dict(sd)
+    lion.close()
+    adam.close()
+
+
+# ------------------------------------------- end to end against the oracle
+
+def _oracle_state_after(params_bf16, grads_seq, precision, master, lr, wd, betas, seed, lion=False):
+    """Run the same updates through the oracle's multi_step: the API must give the same bytes."""
+    mv = {"fp32": O.DT_F32, "bf16": O.DT_BF16, "fp8": O.DT_FP8}[precision]
+    cases = []
+    for k, p in enumerate(params_bf16):
+        n = p.numel()
+        x = p.detach().float().reshape(-1).cpu().numpy()
+        arrays = {}
+        if master == "fp24":
+            arrays["p"], arrays["p_lo"] = O.f24_planes(x)
+        else:
+            arrays["p"] = x.copy()
+        if mv == O.DT_FP8:
+            nb = -(-n // 128)
+            arrays["m"] = np.zeros(nb * 128, np.uint8)
+            arrays["m_scale"] = np.ones(nb, np.float32)
+            if not lion:
+                arrays["v"] = np.zeros(nb * 128, np.uint8)
+                arrays["v_scale"] = np.ones(nb, np.float32)
+        else:
+            dt = np.float32 if mv == O.DT_F32 else np.uint16
+            arrays["m"] = np.zeros(n, dt)
+            if not lion:
+                arrays["v"] = np.zeros(n, dt)
+        arrays["out"] = np.zeros(n, np.uint16)
+        cases.append(O.Case(n=n, algorithm=O.LION if lion else O.ADAMW, mv_dtype=mv,
+                            p_dtype=O.DT_F24 if master == "fp24" else O.DT_F32, g_dtype=O.DT_BF16,
+                            out_dtype=O.DT_BF16, offset=0, index=k, step=1, arrays=arrays,
+                            group={"lr": lr, "beta1": betas[0], "beta2": betas[1], "eps": 0.0 if lion else 1e-8,
+                                   "weight_decay": wd, "seed": seed, "stochastic": 1}))
+    for t, grads in enumerate(grads_seq):
+        for c, g in zip(cases, grads):
+            c.arrays["g"] = g.reshape(-1).cpu().view(torch.int16).numpy().view(np.uint16).copy()
+            c.step = t + 1
+        O.run_many(cases, "oracle", 16, in_place=True)
+    return cases
+
+
+@pytest.mark.parametrize("precision,master,lion", [("bf16", "fp32", False), ("fp32", "fp32", False),
+                                                   ("fp8", "fp24", False), ("bf16", "fp24", True),
+                                                   ("fp8", "fp32", True)])
+@pytest.mark.parametrize("hooks", [False, True])
+def test_api_updates_are_bit_exact_against_the_oracle(precision, master, lion, hooks):
+    """AdamBridge/LionBridge on bf16 parameters (sync step or per-parameter hooks plus a batched
+    small group) give the exact bytes of the reference kernel run on the same gradients with the
+    same parameter indices and step numbers."""
+    torch.manual_seed(0)
+    shapes = [(300, 257), (4099,), (64, 64), (17,), (1000, 130)]
+    params = [torch.nn.Parameter((torch.randn(s, device=DEV) * 0.02).to(torch.bfloat16)) for s in shapes]
+    init = [p.detach().clone() for p in params]
+    lr, wd, betas, seed = (1e-3, 0.1, (0.9, 0.99), 5) if lion else (2e-3, 0.01, (0.9, 0.999), 5)
+    cls = ab.LionBridge if lion else ab.AdamBridge
+    opt = cls(params, lr=lr, betas=betas, weight_decay=wd, precision=precision, master_precision=master, seed=seed,
+              small_param_threshold=5000)
+    g = torch.Generator(device=DEV).manual_seed(3)
+    grads_seq = [[(torch.randn(s, device=DEV, generator=g) * 1e-2).to(torch.bfloat16) for s in shapes]
+                 for _ in range(4)]
+    if hooks:
+        opt.attach_hooks()
+    for grads in grads_seq:
+        if hooks:
+            # autograd delivers the gradient: loss = sum(p * g) has d/dp = g exactly
+            sum((p * gr).float().sum() for p, gr in zip(params, grads)).backward()
+            opt.step_sync()
+        else:
+            for p, gr in zip(params, grads):
+                p.grad = gr.clone()
+            opt.step()
+    torch.cuda.synchronize()
+    want = _oracle_state_after(init, grads_seq, precision, master, lr, wd, betas, seed, lion)
+    for k, (p, c) in enumerate(zip(params, want)):
+        slot = opt._ordered[k]
+        assert slot.step == 4
+        got_p = p.detach().reshape(-1).cpu().view(torch.int16).numpy().view(np.uint16)
+        assert np.array_equal(got_p, c.arrays["out"]), f"param {k} weights"
+        m_data = (slot.m.q if hasattr(slot.m, "q") else slot.m.data).detach().cpu()
+        want_m = c.arrays["m"]
+        assert np.array_equal(m_data.view(torch.uint8).numpy().view(want_m.dtype).reshape(want_m.shape), want_m), \
+            f"param {k} m"
+        if master == "fp24":
+            hi, lo = slot.master.native_buffers
+            assert np.array_equal(hi.cpu().view(torch.int16).numpy().view(np.uint16), c.arrays["p"])
+            assert np.array_equal(lo.cpu().numpy(), c.arrays["p_lo"])
+        else:
+            assert np.array_equal(slot.master.data.cpu().numpy().view(np.uint32), c.arrays["p"].view(np.uint32))
+    opt.close()
+
+
+def test_multi_tensor_launch_count():
+    """step() updates every parameter in one kernel launch."""
+    model = TinyLM().to(DEV).to(torch.bfloat16)
+    opt = ab.AdamBridge(model.parameters(), lr=1e-3, precision="bf16")
+    log = []
+    opt._engine.launch_log = log
+    lm_loss(model, 0).backward()
+    opt.step()
+    torch.cuda.synchronize()
+    assert len(log) == 1 and log[0][2] == sum(p.numel() for p in model.parameters())
+    opt.close()
+
+
+@pytest.mark.parametrize("hooks", [False, True])
+def test_state_layouts_give_identical_bytes(hooks):
+    """The interleaved layout (default), the separate layout and the double-buffered interleaved
+    layout produce the same weights, masters and moments, step after step."""
+    results = []
+    for kw in (dict(state_layout="separate"), dict(), dict(double_buffer=True)):
+        torch.manual_seed(0)
+        model = TinyLM().to(DEV).to(torch.bfloat16)
+        opt = ab.AdamBridge(model.parameters(), lr=3e-3, precision="bf16", small_param_threshold=2000, **kw)
+        if hooks:
+            opt.attach_hooks(model)
+        assert any(s.packed is not None for s in opt._ordered) or "state_layout" in kw or not opt._ordered[0].initialized
+        for step in range(4):
+            lm_loss(model, step).backward()
+            if hooks:
+                opt.step_sync()
+            else:
+                opt.step()
+                opt.zero_grad()
+        if "state_layout" not in kw:
+            assert all(s.packed is not None for s in opt._ordered)
+        results.append(([p.detach().clone() for p in model.parameters()], [m.clone() for m in opt.master_params()],
+                        [s.m.to_fp32() for s in opt._ordered], [s.v.to_fp32() for s in opt._ordered]))
+        opt.close()
+    for other in results[1:]:
+        for xs, ys in zip(results[0], other):
+            assert all(torch.equal(x, y) for x, y in zip(xs, ys))
+
+
+def test_packed_state_checkpoint_and_set_precision():
+    """Checkpoints of the interleaved layout are the reference format and load into either layout;
+    set_precision leaves and re-enters the interleaved layout without changing values."""
+    torch.manual_seed(0)
+    model = TinyLM().to(DEV).to(torch.bfloat16)
+    opt = ab.AdamBridge(model.parameters(), lr=3e-3, precision="bf16")
+    for step in range(3):
+        lm_loss(model, step).backward()
+        opt.step()
+        opt.zero_grad()
+    sd = opt.state_dict()
+    st = sd["state"][0]
+    assert isinstance(st["master"], torch.Tensor) and st["master"].dtype == torch.float32
+    assert st["exp_avg"]["precision"] == "bf16" and st["exp_avg"]["data"].dtype == torch.bfloat16
+    masters = [m.clone() for m in opt.master_params()]
+    for layout in ("separate", "auto"):
+        other = ab.AdamBridge(TinyLM().to(DEV).to(torch.bfloat16).parameters(), lr=3e-3, precision="bf16",
+                              state_layout=layout)
+        other.load_state_dict(sd)
+        for x, y in zip(masters, other.master_params()):
+            assert torch.equal(x, y)
+        for a, b in zip(opt._ordered, other._ordered):
+            assert torch.equal(a.m.to_fp32(), b.m.to_fp32()) and torch.equal(a.v.to_fp32(), b.v.to_fp32())
+        other.close()
+    m_before = [s.m.to_fp32() for s in opt._ordered]
+    opt.set_precision("fp32")
+    assert all(s.packed is None for s in opt._ordered)
+    for s, m in zip(opt._ordered, m_before):
+        assert torch.equal(s.m.to_fp32(), m)
+    opt.set_precision("bf16")
+    assert all(s.packed is not None for s in opt._ordered)
+    for s, m in zip(opt._ordered, m_before):
+        assert torch.equal(s.m.to_fp32(), m)
+    for x, y in zip(masters, opt.master_params()):
+        assert torch.equal(x, y)
+    opt.close()
