@@ -6,8 +6,16 @@
 // of the per-segment first-tile table (uniform, scalar loads), then streams its
 // tile once: reads the gradient, the master and the moments, updates them in
 // registers and writes the master, the moments and the bf16 working weight.
-// 128-bit loads and stores, non-temporal, one pass: the bytes moved per
-// element are exactly the reference's minimum (benchmarks/bench_kernels.py:63-65).
+// Non-temporal global loads and stores, one pass: the bytes moved per element
+// are exactly the reference's minimum (benchmarks/bench_kernels.py:63-65).
+//
+// Tiles are small (1024 elements for the FP32/BF16-moment kernels) and handed
+// out XCD by XCD: the hardware deals consecutive workgroups round-robin to the
+// 8 XCDs, so workgroup b takes tile (b mod 8) * ceil(ntiles/8) + b / 8 and each
+// XCD sweeps one contiguous eighth of the launch.  The accesses in flight then
+// cover a few compact address windows, which HBM serves with far fewer row
+// switches than the scattered windows of large per-workgroup tiles (measured on
+// MI355X: a 1:1 read/write stream goes from 5.4 to 6.5 TB/s).
 //
 // FP8 moments are handled 128-element block by block: 16 lanes x 8 elements
 // per block, the two block maxima reduced with cross-lane shuffles, codes and
@@ -39,11 +47,16 @@
 namespace abh {
 
 constexpr int kThreads = 256;
-// Elements per workgroup: a launch parameter, a multiple of kTileQuantum (one pass of the FP8
-// kernel's 16 block groups, and of the two-element kernels' 256 lanes).  Larger tiles amortize
-// each workgroup's segment search; see the host's default.
-constexpr int64_t kTileQuantum = 2048;
+// Elements per workgroup: a launch parameter, a multiple of the kernel family's quantum -- one
+// pass of the 256 lanes (two elements each) of the FP32/BF16-moment kernels, or of the 16 block
+// groups (128 elements each) of the FP8 kernel.
+constexpr int64_t kPairQuantum = 2 * kThreads;
+constexpr int64_t kFp8Quantum = (kThreads / 16) * kFp8Block;
 constexpr int kInline = 7;        // segments carried in the kernel arguments
+
+// Address spaces: buffers are global memory, descriptors are read-only and uniform (scalar loads).
+#define ABH_GLOBAL __attribute__((address_space(1)))
+#define ABH_CONST __attribute__((address_space(4)))
 
 // Per-segment launch descriptor (device side), 144 bytes.
 struct DevSeg {
@@ -69,28 +82,55 @@ constexpr uint32_t kVec = 1u, kSR = 2u;
 struct Launch {
     const DevSeg* table;     // device table when nsegs > kInline
     const int64_t* starts;   // device: first tile of each segment (compact, for the search)
-    int64_t tile;            // elements per tile (multiple of kTileQuantum)
+    int64_t tile;            // elements per tile (multiple of the kernel family's quantum)
+    int64_t ntiles;          // tiles of the launch; the grid is ntiles rounded up to a multiple of 8
     int32_t nsegs;
     int32_t pad;
     DevSeg inl[kInline];
 };
-static_assert(sizeof(Launch) <= 1024 + 32, "kernel argument block");
+static_assert(sizeof(Launch) <= 1024 + 64, "kernel argument block");
 
-__device__ __forceinline__ const DevSeg* find_segment(const Launch& L, int64_t tile)
+constexpr int kXcds = 8;
+
+// The tile of this workgroup (XCD-contiguous order, see the file comment); >= L.ntiles for the
+// few workgroups that round the grid up to a multiple of 8.
+__device__ __forceinline__ int64_t block_tile(const Launch& L)
+{
+    const int64_t b = blockIdx.x;
+    const int64_t per = (L.ntiles + kXcds - 1) / kXcds;
+    return (b % kXcds) * per + b / kXcds;
+}
+
+// A descriptor copied word by word out of the constant address space (scalar loads).
+__device__ __forceinline__ DevSeg load_desc(const ABH_CONST DevSeg* p)
+{
+    constexpr int kWords = sizeof(DevSeg) / 8;
+    union { DevSeg s; uint64_t w[kWords]; } u;
+    const ABH_CONST uint64_t* q = (const ABH_CONST uint64_t*)p;
+#pragma unroll
+    for (int k = 0; k < kWords; ++k) u.w[k] = q[k];
+    return u.s;
+}
+
+// The descriptor of the segment holding `tile`: binary search of the first-tile table, all
+// through scalar loads (uniform address, constant address space), result in scalar registers.
+__device__ __forceinline__ DevSeg find_segment(const Launch& L, int64_t tile)
 {
     int lo = 0, hi = L.nsegs - 1;
     if (L.nsegs <= kInline) {
+        const ABH_CONST DevSeg* inl = (const ABH_CONST DevSeg*)&L.inl[0];
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
-            if (L.inl[mid].tile_begin <= tile) lo = mid; else hi = mid - 1;
+            if (inl[mid].tile_begin <= tile) lo = mid; else hi = mid - 1;
         }
-        return L.inl + lo;
+        return load_desc(inl + lo);
     }
+    const ABH_CONST int64_t* starts = (const ABH_CONST int64_t*)L.starts;
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
-        if (L.starts[mid] <= tile) lo = mid; else hi = mid - 1;
+        if (starts[mid] <= tile) lo = mid; else hi = mid - 1;
     }
-    return L.table + lo;
+    return load_desc((const ABH_CONST DevSeg*)L.table + lo);
 }
 
 // --------------------------------------------------------------- loads/stores
@@ -101,10 +141,11 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 // Streaming accesses: every byte is touched once per step, so keep them out of the caches.
+// The casts make them global_load / global_store (not flat): the buffers are device memory.
 template <typename T>
-__device__ __forceinline__ T ld(const T* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ T ld(const T* p) { return __builtin_nontemporal_load((const ABH_GLOBAL T*)p); }
 template <typename T>
-__device__ __forceinline__ void st(T* p, T v) { __builtin_nontemporal_store(v, p); }
+__device__ __forceinline__ void st(T* p, T v) { __builtin_nontemporal_store(v, (ABH_GLOBAL T*)p); }
 
 // 8 consecutive values as FP32, from BF16 bits or FP32, 16-byte aligned.
 template <int DT>
@@ -288,16 +329,16 @@ __device__ __forceinline__ void store_out2(void* base, int64_t i, float x0, floa
 template <int DT>
 __device__ __forceinline__ float load1(const void* base, int64_t i)
 {
-    if constexpr (DT == DT_BF16) return bitsf((uint32_t)static_cast<const uint16_t*>(base)[i] << 16);
-    else return static_cast<const float*>(base)[i];
+    if constexpr (DT == DT_BF16) return bitsf((uint32_t)ld(static_cast<const uint16_t*>(base) + i) << 16);
+    else return ld(static_cast<const float*>(base) + i);
 }
 
 template <int PT>
 __device__ __forceinline__ float load_master1(const DevSeg& s, int64_t i)
 {
     if constexpr (PT == DT_F24)
-        return bitsf(((uint32_t)static_cast<const uint16_t*>(s.p)[i] << 16) | ((uint32_t)s.p_lo[i] << 8));
-    else return static_cast<const float*>(s.p)[i];
+        return bitsf(((uint32_t)ld(static_cast<const uint16_t*>(s.p) + i) << 16) | ((uint32_t)ld(s.p_lo + i) << 8));
+    else return ld(static_cast<const float*>(s.p) + i);
 }
 
 template <int PT, bool SR>
@@ -305,11 +346,11 @@ __device__ __forceinline__ float store_master1(const DevSeg& s, int64_t i, float
 {
     if constexpr (PT == DT_F24) {
         const uint32_t b = f24_round<SR>(x, SR ? hash32(idx ^ s.seed_p) : 0u);
-        static_cast<uint16_t*>(s.p)[i] = (uint16_t)(b >> 16);
-        s.p_lo[i] = (uint8_t)(b >> 8);
+        st(static_cast<uint16_t*>(s.p) + i, (uint16_t)(b >> 16));
+        st(s.p_lo + i, (uint8_t)(b >> 8));
         return bitsf(b);
     } else {
-        static_cast<float*>(s.p)[i] = x;
+        st(static_cast<float*>(s.p) + i, x);
         return x;
     }
 }
@@ -317,15 +358,15 @@ __device__ __forceinline__ float store_master1(const DevSeg& s, int64_t i, float
 template <int MV, bool SR>
 __device__ __forceinline__ void store_moment1(void* base, int64_t i, float x, uint32_t r)
 {
-    if constexpr (MV == DT_BF16) static_cast<uint16_t*>(base)[i] = (uint16_t)bf16_store<SR>(x, r);
-    else static_cast<float*>(base)[i] = x;
+    if constexpr (MV == DT_BF16) st(static_cast<uint16_t*>(base) + i, (uint16_t)bf16_store<SR>(x, r));
+    else st(static_cast<float*>(base) + i, x);
 }
 
 template <int OT>
 __device__ __forceinline__ void store_out1(void* base, int64_t i, float x)
 {
-    if constexpr (OT == DT_BF16) static_cast<uint16_t*>(base)[i] = (uint16_t)bf16_rne(x);
-    else if constexpr (OT == DT_F32) static_cast<float*>(base)[i] = x;
+    if constexpr (OT == DT_BF16) st(static_cast<uint16_t*>(base) + i, (uint16_t)bf16_rne(x));
+    else if constexpr (OT == DT_F32) st(static_cast<float*>(base) + i, x);
 }
 
 // ------------------------------------------------- FP32 / BF16 moment kernel
@@ -386,8 +427,9 @@ __device__ __forceinline__ void update_tile(const DevSeg& s, int64_t tile, int64
 template <int ALGO, int MV, int PT, int GT, int OT>
 __global__ __launch_bounds__(kThreads) void k_update(Launch L)
 {
-    const int64_t tile = blockIdx.x;
-    const DevSeg& s = *find_segment(L, tile);
+    const int64_t tile = block_tile(L);
+    if (tile >= L.ntiles) return;
+    const DevSeg s = find_segment(L, tile);
     if (s.flags & kSR) update_tile<ALGO, MV, PT, GT, OT, true>(s, tile, L.tile);
     else update_tile<ALGO, MV, PT, GT, OT, false>(s, tile, L.tile);
 }
@@ -399,14 +441,14 @@ __device__ __forceinline__ u32x2 load_codes8(const uint8_t* q)
 {
     uint32_t w[2] = {0u, 0u};
 #pragma unroll
-    for (int k = 0; k < 8; ++k) w[k >> 2] |= (uint32_t)q[k] << (8 * (k & 3));
+    for (int k = 0; k < 8; ++k) w[k >> 2] |= (uint32_t)ld(q + k) << (8 * (k & 3));
     return u32x2{w[0], w[1]};
 }
 
 __device__ __forceinline__ void store_codes8(uint8_t* q, const uint32_t (&w)[2])
 {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) q[k] = (uint8_t)(w[k >> 2] >> (8 * (k & 3)));
+    for (int k = 0; k < 8; ++k) st(q + k, (uint8_t)(w[k >> 2] >> (8 * (k & 3))));
 }
 
 // Max over the 16 lanes of a block group (values are >= 0 and never NaN).
@@ -437,8 +479,8 @@ __device__ __forceinline__ void update_tile_fp8(const DevSeg& s, int64_t tile, i
         const int64_t e0 = b0 + lane * 8;
         const uint32_t idx = s.idx0 + (uint32_t)e0;
         const bool full = vec && e0 + 8 <= n;
-        const float sm = s.m_scale[blk];
-        const float sv = kLion ? 0.0f : s.v_scale[blk];
+        const float sm = ld(s.m_scale + blk);
+        const float sv = kLion ? 0.0f : ld(s.v_scale + blk);
         // codes are stored padded to whole blocks, so all 8 of this lane's exist
         const u32x2 cm = vec ? ld(reinterpret_cast<const u32x2*>(mq + e0)) : load_codes8(mq + e0);
         u32x2 cv = {0u, 0u};
@@ -525,8 +567,8 @@ __device__ __forceinline__ void update_tile_fp8(const DevSeg& s, int64_t tile, i
             if constexpr (!kLion) store_codes8(vq + e0, qv);
         }
         if (lane == 0) {
-            s.m_scale[blk] = scm;
-            if constexpr (!kLion) s.v_scale[blk] = scu;
+            st(s.m_scale + blk, scm);
+            if constexpr (!kLion) st(s.v_scale + blk, scu);
         }
     }
 }
@@ -534,8 +576,9 @@ __device__ __forceinline__ void update_tile_fp8(const DevSeg& s, int64_t tile, i
 template <int ALGO, int PT, int GT, int OT>
 __global__ __launch_bounds__(kThreads) void k_update_fp8(Launch L)
 {
-    const int64_t tile = blockIdx.x;
-    const DevSeg& s = *find_segment(L, tile);
+    const int64_t tile = block_tile(L);
+    if (tile >= L.ntiles) return;
+    const DevSeg s = find_segment(L, tile);
     if (s.flags & kSR) update_tile_fp8<ALGO, PT, GT, OT, true>(s, tile, L.tile);
     else update_tile_fp8<ALGO, PT, GT, OT, false>(s, tile, L.tile);
 }
@@ -622,8 +665,9 @@ __device__ __forceinline__ void update_tile_packed(const DevSeg& s, int64_t tile
 template <int GT, int OT>
 __global__ __launch_bounds__(kThreads) void k_update_packed(Launch L)
 {
-    const int64_t tile = blockIdx.x;
-    const DevSeg& s = *find_segment(L, tile);
+    const int64_t tile = block_tile(L);
+    if (tile >= L.ntiles) return;
+    const DevSeg s = find_segment(L, tile);
     if (s.flags & kSR) update_tile_packed<GT, OT, true>(s, tile, L.tile);
     else update_tile_packed<GT, OT, false>(s, tile, L.tile);
 }
@@ -677,6 +721,12 @@ constexpr auto make_packed_table(std::integer_sequence<int, I...>)
 
 static const auto kKernels = make_table(std::make_integer_sequence<int, kNumKernels>{});
 static const auto kPacked = make_packed_table(std::make_integer_sequence<int, kNumPacked>{});
+
+// Kernel family of a table index: the FP8 block kernel, or a two-element-per-lane kernel.
+inline bool kernel_is_fp8(int index)
+{
+    return index < kNumKernels && (index / 12) % 3 == 2;
+}
 
 inline KernelFn kernel_at(int index)
 {
