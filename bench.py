@@ -41,6 +41,9 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "params updated/sec and achieved HBM GB/s (% roofline), AdamW bf16 moments @7B"
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of the update kernel, measured with rocprofv3 FETCH_SIZE + WRITE_SIZE, each
+# scaled by its reading for a copy of known size (profiles/k_update_packed_c3p_hbm_traffic.md).
+MEASURED_TRAFFIC = {"c3p": 134.764e9}
 
 
 # ------------------------------------------------------------ parameter lists
@@ -152,19 +155,36 @@ def gpu_bench(cfg: dict, steps: int, warmup: int, layout: str = "auto", double_b
     return stats
 
 
+def calibrate_copy(nbytes: int) -> None:
+    """Three copies of ``nbytes`` between two device buffers: under rocprofv3 --pmc, the copy kernel's
+    FETCH_SIZE and WRITE_SIZE readings against ``nbytes`` give the counters' scale factors."""
+    import torch
+
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"[bench] calibration: 3 copies of {nbytes} bytes", file=sys.stderr, flush=True)
+    del src, dst
+    torch.cuda.empty_cache()
+
+
 # ----------------------------------------------------------------- CPU side
 
-def cpu_bench(cfg: dict, budget_params: int, steps: int) -> dict | None:
-    """The reference's native kernel (oracle/_ref) over the first tensors of the same list, up to
-    ``budget_params`` parameters, on this host's CPU share; None when the library is absent."""
+def cpu_bench(cfg: dict, budget_params: int, steps: int) -> dict:
+    """The reference's native kernel (oracle/_ref, compiled from its C source) over the first tensors
+    of the same list, up to ``budget_params`` parameters, on this host's CPU share.  Where that
+    library was not built (no reference tree at build time), the oracle's C restatement of the same
+    algorithm (oracle/liboracle.so, OpenMP) is timed instead and reported as kind "port"."""
     import ctypes
 
     import numpy as np
     from oracle import oracle as O
 
-    if not O.reference_available():
-        return None
-    lib = O.load_reference()
+    use_ref = O.reference_available()
+    lib = O.load_reference() if use_ref else O.load_oracle()
     try:
         cores = len(os.sched_getaffinity(0))
     except AttributeError:
@@ -205,16 +225,23 @@ def cpu_bench(cfg: dict, budget_params: int, steps: int) -> dict | None:
                         mv_dtype=mv_dt, out_dtype=O.DT_BF16, algorithm=1 if lion else 0, p_dtype=O.DT_F32)
         segs.append(seg)
     arr = (ctypes.POINTER(O.Segment) * len(segs))(*[ctypes.pointer(s) for s in segs])
-    lib.adambridge_set_simd_level(-1)
-    level = lib.adambridge_simd_level()
-    pool = lib.adambridge_pool_create(threads, None, 0)
+    if use_ref:
+        lib.adambridge_set_simd_level(-1)
+        level = lib.adambridge_simd_level()
+        pool = lib.adambridge_pool_create(threads, None, 0)
+        run = lambda: lib.adambridge_multi_step(pool, arr, len(segs), threads)  # noqa: E731
+        what = f"reference native kernel (oracle/_ref, compiled from adambridge_kernels.c, SIMD level {level})"
+    else:
+        pool = None
+        run = lambda: lib.abo_multi_step(arr, len(segs), 16, threads)  # noqa: E731
+        what = "oracle C restatement of the reference kernel (oracle/liboracle.so, scalar C, OpenMP)"
     try:
         def one(step):
             for s in segs:
                 s.step = step
-            rc = lib.adambridge_multi_step(pool, arr, len(segs), threads)
+            rc = run()
             if rc:
-                raise RuntimeError(f"reference multi_step returned {rc}")
+                raise RuntimeError(f"CPU multi_step returned {rc}")
         one(1)
         times = []
         for k in range(steps):
@@ -222,14 +249,14 @@ def cpu_bench(cfg: dict, budget_params: int, steps: int) -> dict | None:
             one(k + 2)
             times.append(time.perf_counter() - t0)
     finally:
-        lib.adambridge_pool_destroy(pool)
+        if pool:
+            lib.adambridge_pool_destroy(pool)
     times.sort()
     med = times[len(times) // 2]
     bpp = min_bytes(cfg["precision"], cfg["algo"])
-    return dict(value=total / med, unit="params/s", cores=threads, kind="reference",
-                sample=(f"reference native kernel (oracle/_ref, compiled from adambridge_kernels.c, "
-                        f"SIMD level {level}) on the first {len(shapes)} tensors of the same list "
-                        f"({total:,} params), median of {steps} steps after 1 warm-up, {threads} threads"),
+    return dict(value=total / med, unit="params/s", cores=threads, kind="reference" if use_ref else "port",
+                sample=(f"{what} on the first {len(shapes)} tensors of the same list ({total:,} params), "
+                        f"median of {steps} steps after 1 warm-up, {threads} threads"),
                 ms_per_step=med * 1e3, gbs=total * bpp / med / 1e9)
 
 
@@ -241,14 +268,18 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c3p", choices=sorted(CONFIGS))
-    ap.add_argument("--cpu-params", type=int, default=1 << 29, help="CPU baseline sample size (parameters)")
-    ap.add_argument("--cpu-steps", type=int, default=5)
+    ap.add_argument("--cpu-params", type=int, default=1 << 30, help="CPU baseline sample size (parameters)")
+    ap.add_argument("--cpu-steps", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--layout", default="auto", choices=["auto", "packed", "separate"],
                     help="optimizer state layout in HBM (AdamBridge state_layout)")
     ap.add_argument("--double-buffer", action="store_true", help="AdamBridge double_buffer=True")
     ap.add_argument("--traffic", type=float, default=None,
-                    help="HBM bytes per launch measured by rocprofv3 (FETCH_SIZE+WRITE_SIZE, scaled)")
+                    help="HBM bytes per launch measured by rocprofv3 (FETCH_SIZE+WRITE_SIZE, scaled); "
+                         "default: the figure measured for this configuration, when there is one")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
+                    help="first run 3 device-to-device copies of BYTES bytes (a known-size kernel that "
+                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -257,6 +288,8 @@ def main() -> int:
     if args.steps < 1 or args.warmup < 0:
         ap.error("--steps must be >= 1 and --warmup >= 0")
     cfg = CONFIGS[args.config]
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy)
     print(f"[bench] config {args.config}: {cfg['desc']}; warmup {args.warmup}, steps {args.steps}",
           file=sys.stderr, flush=True)
     g = gpu_bench(cfg, args.steps, args.warmup, args.layout, args.double_buffer)
@@ -285,7 +318,8 @@ def main() -> int:
                    "state_layout": g["layout"], "state_bytes": g["state_bytes"],
                    "wall_gbs": g["params"] * g["bytes_per_param"] / (ms_per_step / 1e3) / 1e9},
         "roofline": {"bound": "hbm", "achieved": g["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": g["achieved_gbs"] / HBM_PEAK_GBS, "traffic": args.traffic,
+                     "frac": g["achieved_gbs"] / HBM_PEAK_GBS,
+                     "traffic": args.traffic if args.traffic is not None else MEASURED_TRAFFIC.get(args.config),
                      "kernel_ms": g["kernel_ms"]},
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
     }
