@@ -451,6 +451,31 @@ __device__ __forceinline__ void store_codes8(uint8_t* q, const uint32_t (&w)[2])
     for (int k = 0; k < 8; ++k) st(q + k, (uint8_t)(w[k >> 2] >> (8 * (k & 3))));
 }
 
+// The 8 codes of a lane (two words, byte k & 3 of word k >> 2) as FP32.
+template <bool E5M2>
+__device__ __forceinline__ void decode_codes(const u32x2 w, float (&x)[8])
+{
+    if constexpr (E5M2) {
+        x[0] = e5m2_decode<0>(w.x); x[1] = e5m2_decode<1>(w.x); x[2] = e5m2_decode<2>(w.x); x[3] = e5m2_decode<3>(w.x);
+        x[4] = e5m2_decode<0>(w.y); x[5] = e5m2_decode<1>(w.y); x[6] = e5m2_decode<2>(w.y); x[7] = e5m2_decode<3>(w.y);
+    } else {
+        x[0] = e4m3_decode<0>(w.x); x[1] = e4m3_decode<1>(w.x); x[2] = e4m3_decode<2>(w.x); x[3] = e4m3_decode<3>(w.x);
+        x[4] = e4m3_decode<0>(w.y); x[5] = e4m3_decode<1>(w.y); x[6] = e4m3_decode<2>(w.y); x[7] = e4m3_decode<3>(w.y);
+    }
+}
+
+// x[k] / scale in place for a lane's 8 elements of one block (see block_div).
+__device__ __forceinline__ void block_quotients(float (&x)[8], const BlockDiv& d)
+{
+    if (d.fast) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[k] = block_quot_fast(x[k], d);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[k] = x[k] / d.s;
+    }
+}
+
 // Max over the 16 lanes of a block group (values are >= 0 and never NaN).
 __device__ __forceinline__ float group16_max(float x)
 {
@@ -497,22 +522,28 @@ __device__ __forceinline__ void update_tile_fp8(const DevSeg& s, int64_t tile, i
                 p[k] = in ? load_master1<PT>(s, e0 + k) : 0.0f;
             }
         }
+        {
+            float d[8];
+            decode_codes<false>(cm, d);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const uint32_t w = k < 4 ? cm.x : cm.y, wv = k < 4 ? cv.x : cv.y;
-            mt[k] = e4m3_decode((w >> (8 * (k & 3))) & 0xffu) * sm;
+            for (int k = 0; k < 8; ++k) mt[k] = d[k] * sm;
             if constexpr (!kLion) {
-                const float u = e5m2_decode((wv >> (8 * (k & 3))) & 0xffu) * sv;
-                vt[k] = u * u;
+                decode_codes<true>(cv, d);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const float u = d[k] * sv;
+                    vt[k] = u * u;
+                }
             }
         }
-        // the update, FP32 moments in registers
+        // the update, FP32 moments in registers; sq = sqrt(new v), reused for the v code below
         const bool lane_fused = kLion || e0 + 8 <= n_main;
+        float sq[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             if constexpr (kLion) p[k] = lion(p[k], g[k], mt[k], c);
-            else p[k] = lane_fused ? adamw<true>(p[k], g[k], mt[k], vt[k], c)
-                                   : adamw_sel(p[k], g[k], mt[k], vt[k], c, e0 + k < n_main);
+            else p[k] = lane_fused ? adamw<true>(p[k], g[k], mt[k], vt[k], c, sq[k])
+                                   : adamw_sel(p[k], g[k], mt[k], vt[k], c, e0 + k < n_main, sq[k]);
         }
         if (full) {
             store_master8<PT, SR>(s, e0, p, idx);
@@ -526,7 +557,8 @@ __device__ __forceinline__ void update_tile_fp8(const DevSeg& s, int64_t tile, i
                 }
             }
         }
-        // block maxima (NaN skipped), elements past the end count as zero
+        // block maxima (NaN skipped), elements past the end count as zero; v is stored as
+        // sqrt(max(v, 0)), which is sq wherever v > 0 (same correctly rounded root)
         float am = 0.0f, au = 0.0f;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
@@ -535,7 +567,7 @@ __device__ __forceinline__ void update_tile_fp8(const DevSeg& s, int64_t tile, i
             const float a = fabsf(mt[k]);
             am = a > am ? a : am;
             if constexpr (!kLion) {
-                const float u = __builtin_sqrtf(vt[k] > 0.0f ? vt[k] : 0.0f);
+                const float u = vt[k] > 0.0f ? sq[k] : 0.0f;
                 vt[k] = u;
                 au = u > au ? u : au;
             }
@@ -548,14 +580,16 @@ __device__ __forceinline__ void update_tile_fp8(const DevSeg& s, int64_t tile, i
             au = group16_max(au);
             scu = au > 0.0f ? au / 57344.0f : 1.0f;
         }
+        block_quotients(mt, block_div(scm, am));
+        if constexpr (!kLion) block_quotients(vt, block_div(scu, au));
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const uint32_t ik = idx + k;
             const bool in = e0 + k < n;   // padding codes are zero
-            const uint32_t a = e4m3_encode<SR>(mt[k] / scm, SR ? hash32(ik ^ s.seed_m) : 0u);
+            const uint32_t a = e4m3_encode<SR>(mt[k], SR ? hash32(ik ^ s.seed_m) : 0u);
             qm[k >> 2] |= (in ? a : 0u) << (8 * (k & 3));
             if constexpr (!kLion) {
-                const uint32_t b = e5m2_encode<SR>(vt[k] / scu, SR ? hash32(ik ^ s.seed_v) : 0u);
+                const uint32_t b = e5m2_encode<SR>(vt[k], SR ? hash32(ik ^ s.seed_v) : 0u);
                 qv[k >> 2] |= (in ? b : 0u) << (8 * (k & 3));
             }
         }
