@@ -171,6 +171,115 @@ def calibrate_copy(nbytes: int) -> None:
     torch.cuda.empty_cache()
 
 
+# ------------------------------------------------------- hooked pipeline (c5)
+
+PIPELINE = dict(layers=24, hidden=2048, inter=8192, batch=8, seq=512, lr=1e-4, wd=0.01)
+
+
+def pipeline_model(device):
+    """24 x [Linear(2048 -> 8192) + GELU + Linear(8192 -> 2048)] with a residual, bf16: 805,552,128
+    parameters (48 weight matrices with a hook each, 48 biases batched at step_sync)."""
+    import torch
+
+    class Block(torch.nn.Module):
+        def __init__(self, h, i):
+            super().__init__()
+            self.up = torch.nn.Linear(h, i)
+            self.down = torch.nn.Linear(i, h)
+
+        def forward(self, x):
+            return x + self.down(torch.nn.functional.gelu(self.up(x)))
+
+    torch.manual_seed(0)
+    c = PIPELINE
+    return torch.nn.Sequential(*[Block(c["hidden"], c["inter"]) for _ in range(c["layers"])]).to(
+        device=device, dtype=torch.bfloat16)
+
+
+def pipeline_bench(steps: int, warmup: int) -> dict:
+    """Training-step wall time of the c5 stack with: no optimizer (the floor), torch's fused AdamW,
+    AdamBridge.step() after backward, attach_hooks + step_sync, and attach_hooks + delay_updates;
+    plus, for the hooked runs, the GPU time of the updates and the exposed tail (last gradient ready
+    -> last update done), from the side stream's events."""
+    import statistics
+
+    import torch
+    import adambridge_amd as ab
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    c = PIPELINE
+    gen = torch.Generator(device=device).manual_seed(0)
+    x = torch.randn(c["batch"] * c["seq"], c["hidden"], generator=gen, device=device, dtype=torch.bfloat16)
+    target = torch.randn(x.shape, generator=gen, device=device, dtype=torch.bfloat16)
+
+    def loss_of(model):
+        return torch.nn.functional.mse_loss(model(x).float(), target.float())
+
+    def timed(step, stats_of=None):
+        times, upd, tail, bwd = [], [], [], []
+        for i in range(warmup + steps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            st = step()
+            torch.cuda.synchronize()
+            if i >= warmup:
+                times.append(time.perf_counter() - t0)
+                if st is not None:
+                    upd.append(st.gpu_update or 0.0)
+                    tail.append(st.exposed_tail or 0.0)
+                    bwd.append(st.gpu_backward or 0.0)
+        out = dict(step_ms=statistics.median(times) * 1e3)
+        if upd:
+            out.update(gpu_update_ms=statistics.median(upd) * 1e3, exposed_tail_ms=statistics.median(tail) * 1e3,
+                       gpu_backward_ms=statistics.median(bwd) * 1e3)
+        return out
+
+    results = {}
+    model = pipeline_model(device)
+    n = sum(p.numel() for p in model.parameters())
+
+    def floor():
+        loss_of(model).backward()
+        for p in model.parameters():
+            p.grad = None
+    results["fwd+bwd only"] = timed(floor)
+
+    opt = torch.optim.AdamW(model.parameters(), lr=c["lr"], weight_decay=c["wd"], fused=True)
+
+    def torch_step():
+        loss_of(model).backward()
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+    results["torch.optim.AdamW(fused=True), bf16 state, no master"] = timed(torch_step)
+    del opt
+    torch.cuda.empty_cache()
+
+    for name, hooks, delay in (("AdamBridge bf16 step()", False, False),
+                               ("AdamBridge bf16 attach_hooks + step_sync", True, False),
+                               ("AdamBridge bf16 attach_hooks + delay_updates", True, True)):
+        model = pipeline_model(device)
+        opt = ab.AdamBridge(model.parameters(), lr=c["lr"], weight_decay=c["wd"], precision="bf16",
+                            delay_updates=delay)
+        opt._engine.timing = hooks
+        if hooks:
+            opt.attach_hooks(model)
+
+            def step():
+                loss_of(model).backward()
+                return opt.step_sync()
+        else:
+            def step():
+                loss_of(model).backward()
+                opt.step()
+                opt.zero_grad(set_to_none=True)
+        results[name] = timed(step)
+        opt.close()
+        del opt, model
+        torch.cuda.empty_cache()
+    return dict(params=n, results=results)
+
+
 # ----------------------------------------------------------------- CPU side
 
 def cpu_bench(cfg: dict, budget_params: int, steps: int) -> dict:
@@ -267,7 +376,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c3p", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="c3p", choices=sorted(CONFIGS) + ["c5"],
+                    help="c5: the hooked training pipeline (prints its own JSON line)")
     ap.add_argument("--cpu-params", type=int, default=1 << 30, help="CPU baseline sample size (parameters)")
     ap.add_argument("--cpu-steps", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -287,6 +397,8 @@ def main() -> int:
         return 2
     if args.steps < 1 or args.warmup < 0:
         ap.error("--steps must be >= 1 and --warmup >= 0")
+    if args.config == "c5":
+        return main_pipeline(args)
     cfg = CONFIGS[args.config]
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)
@@ -322,6 +434,26 @@ def main() -> int:
                      "traffic": args.traffic if args.traffic is not None else MEASURED_TRAFFIC.get(args.config),
                      "kernel_ms": g["kernel_ms"]},
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def main_pipeline(args) -> int:
+    c = PIPELINE
+    print(f"[bench] c5: {c['layers']}-layer bf16 MLP {c['hidden']}->{c['inter']}->{c['hidden']}, "
+          f"{c['batch']}x{c['seq']} tokens; warmup {args.warmup}, steps {args.steps}", file=sys.stderr, flush=True)
+    r = pipeline_bench(args.steps, args.warmup)
+    for name, v in r["results"].items():
+        print(f"[bench] {name:<48} " + ", ".join(f"{k} {x:.2f}" for k, x in v.items()), file=sys.stderr, flush=True)
+    hooked = r["results"]["AdamBridge bf16 attach_hooks + step_sync"]
+    line = {
+        "metric": "training step wall time, 24-layer bf16 MLP, hooked bf16-moment AdamW (c5)",
+        "value": hooked["step_ms"], "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": hooked["step_ms"], "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 model, f32 update", "data": "synthetic (N(0,1) tokens and targets, seed 0)",
+        "config": {"workload": "c5 hooked pipeline", "params": r["params"], "tokens": c["batch"] * c["seq"],
+                   "bytes_per_param": 20, "runs": r["results"]},
     }
     print(json.dumps(line), flush=True)
     return 0
