@@ -1,0 +1,148 @@
+"""Parity at the benchmark configurations' full sizes (GPU).
+
+Each test builds one BASELINE configuration's whole parameter list on the GPU (up to the 7B
+Llama list, 291 tensors), runs warm-up steps through ``AdamBridge.step()`` -- one multi-tensor
+launch per step -- and then checks one more step two ways:
+
+* sampled windows, bit for bit: before the step, windows of the optimizer state, gradient and
+  master are copied out (the first, a middle and the last 128-aligned elements of several
+  tensors, and every tensor's first elements); the oracle updates each window as a segment of
+  its own with the parameter's index, the step number and the window's element offset -- the
+  rounding stream is keyed by (parameter, step, element index), so a window reproduces exactly
+  what the whole-tensor launch must write there;
+* every element: the bf16 working weight written by the step equals the round-to-nearest-even
+  bf16 of the stored master (kernels.c:108-112 applied to the value actually stored).
+"""
+
+from __future__ import annotations
+
+import math
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+ROOT = Path(__file__).resolve().parents[1]
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+import bench  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+WINDOW = 4096
+
+
+def _u16(t: torch.Tensor) -> np.ndarray:
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _u8(t: torch.Tensor) -> np.ndarray:
+    return t.detach().contiguous().view(torch.uint8).cpu().numpy()
+
+
+def snapshot(opt, slot, lo: int, hi: int) -> dict:
+    """The slot's state, gradient and master over elements [lo, hi) as the oracle's arrays."""
+    a: dict[str, np.ndarray] = {}
+    if slot.packed is not None:   # interleaved FP32 master + BF16 moments, 16 bytes per pair
+        assert lo % 2 == 0
+        rows = slot.packed.current[lo // 2: (hi + 1) // 2].cpu().numpy().view(np.uint32)
+        p = np.empty(2 * rows.shape[0], np.uint32)
+        p[0::2], p[1::2] = rows[:, 0], rows[:, 1]
+        m = np.empty_like(p)
+        m[0::2], m[1::2] = rows[:, 2] & 0xFFFF, rows[:, 2] >> 16
+        v = np.empty_like(p)
+        v[0::2], v[1::2] = rows[:, 3] & 0xFFFF, rows[:, 3] >> 16
+        n = hi - lo
+        a["p"] = p[:n].view(np.float32).copy()
+        a["m"] = m[:n].astype(np.uint16)
+        a["v"] = v[:n].astype(np.uint16)
+    else:
+        master = slot.master
+        if master.precision == "fp24":
+            a["p"], a["p_lo"] = _u16(master.hi[lo:hi]), _u8(master.lo[lo:hi])
+        else:
+            a["p"] = master.data[lo:hi].detach().cpu().numpy().copy()
+        for key, store in (("m", slot.m), ("v", slot.v)):
+            if store is None:
+                continue
+            if store.precision == "fp8":
+                assert lo % 128 == 0
+                b0, b1 = lo // 128, math.ceil(hi / 128)
+                a[key] = _u8(store.q[b0 * 128: b1 * 128])
+                a[key + "_scale"] = store.scale[b0:b1].cpu().numpy().copy()
+            elif store.precision == "bf16":
+                a[key] = _u16(store.data[lo:hi])
+            else:
+                a[key] = store.data[lo:hi].detach().cpu().numpy().copy()
+    g = slot.param.grad.reshape(-1)[lo:hi]
+    a["g"] = _u16(g) if g.dtype == torch.bfloat16 else g.float().cpu().numpy()
+    a["out"] = np.zeros(hi - lo, np.uint16)
+    return a
+
+
+def windows(numel: int) -> list[tuple[int, int]]:
+    if numel <= 3 * WINDOW:
+        return [(0, numel)]
+    mid = (numel // 2) // 128 * 128
+    last = (numel - WINDOW) // 128 * 128
+    return [(0, WINDOW), (mid, mid + WINDOW), (last, numel)]
+
+
+def run_config(name: str, warm: int = 2, tensors: int = 6) -> None:
+    cfg = bench.CONFIGS[name]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    opt, params = bench.build(cfg, dev)
+    try:
+        for _ in range(warm):
+            opt.step()
+        torch.cuda.synchronize()
+        lion = cfg["algo"] == "lion"
+        mv = {"fp32": O.DT_F32, "bf16": O.DT_BF16, "fp8": O.DT_FP8}[cfg["precision"]]
+        # the largest tensors (first, middle, last windows) and the first window of every tensor
+        by_size = sorted(opt._ordered, key=lambda s: -s.numel)[:tensors]
+        picks = []
+        for slot in opt._ordered:
+            for lo, hi in (windows(slot.numel) if slot in by_size else [(0, min(slot.numel, 256))]):
+                picks.append((slot, lo, hi))
+        group = opt.param_groups[0]
+        cases = []
+        for slot, lo, hi in picks:
+            arrays = snapshot(opt, slot, lo, hi)
+            case = O.Case(n=hi - lo, algorithm=O.LION if lion else O.ADAMW, mv_dtype=mv,
+                          p_dtype=O.DT_F24 if "p_lo" in arrays else O.DT_F32, g_dtype=O.DT_BF16,
+                          out_dtype=O.DT_BF16, offset=lo, index=slot.index, step=slot.step + 1, arrays=arrays)
+            case.group = {"lr": group["lr"], "beta1": group["betas"][0], "beta2": group["betas"][1],
+                          "eps": group["eps"], "weight_decay": group["weight_decay"], "seed": 0, "stochastic": 1}
+            cases.append(case)
+        want = O.run_many(cases, "oracle", 16, threads=O.threads_default())
+        opt.step()
+        torch.cuda.synchronize()
+        for (slot, lo, hi), w, before in zip(picks, want, cases):
+            # the step moves the master (every window has nonzero gradients), so equality below
+            # compares two updates, not two copies of the old state
+            assert not np.array_equal(before.arrays["p"].view(np.uint8), w.arrays["p"].view(np.uint8))
+            got = snapshot(opt, slot, lo, hi)
+            got["out"] = _u16(slot.param.detach().reshape(-1)[lo:hi])
+            for key in ("p", "p_lo", "m", "v", "m_scale", "v_scale", "out"):
+                if key in w.arrays:
+                    assert np.array_equal(w.arrays[key].view(np.uint8), got[key].view(np.uint8)), \
+                        f"{name}: parameter {slot.index} elements [{lo}, {hi}): {key} differs"
+        # every element: working weight == bf16 RNE of the stored master
+        for slot in opt._ordered:
+            master = slot.master.to_fp32() if slot.packed is None else slot.packed.get("p")
+            assert torch.equal(slot.param.detach().reshape(-1), master.to(torch.bfloat16)), \
+                f"{name}: parameter {slot.index}: bf16 weight != RNE(master)"
+    finally:
+        opt.close()
+        del opt, params
+        torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("name", ["c3p", "c3", "c4", "c2", "c1"])
+def test_full_size_config_sampled_parity(name):
+    run_config(name)
