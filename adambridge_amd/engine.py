@@ -347,6 +347,7 @@ class UpdateEngine:
         this update."""
         by_dev: dict[torch.device, list[int]] = {}
         for i, slot in enumerate(slots):
+            self._check_param(slot.param)   # before any device context: CPU tensors get this error
             by_dev.setdefault(slot.param.device, []).append(i)
         for dev, idx in by_dev.items():
             self._update_device(dev, [slots[i] for i in idx], [grads[i] for i in idx], hooked)

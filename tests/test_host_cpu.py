@@ -1,0 +1,301 @@
+"""Host logic on the CPU: storage formats, torch-side encoders, argument and checkpoint validation.
+
+The torch-side encoders (``adambridge_amd.precision``) re-encode moments off the step path:
+initial state, ``set_precision()`` and loading a checkpoint of another precision.  Here they are
+pinned bit for bit against the oracle's encoders (oracle/abh_oracle.c, which the golden vectors
+pin to the reference kernel) on finite inputs, and against the formats' behaviour the reference's
+own suite checks (reference tests/test_precision.py:8-160).  Optimizer construction and
+checkpoint validation need no device and run here too.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+import adambridge_amd as ab
+from adambridge_amd import precision as P
+
+
+# ------------------------------------------------------------ names and sizes
+
+def test_precision_aliases_and_bytes_per_param():
+    assert P.canonical_precision("BF16_Moments") == "bf16"
+    assert P.canonical_precision("fp8_moments") == "fp8"
+    assert P.canonical_precision("float32") == "fp32"
+    for bad in ("int4", "fp16", None):
+        with pytest.raises(ValueError):
+            P.canonical_precision(bad)
+    assert P.canonical_master_precision("FP24") == "fp24"
+    with pytest.raises(ValueError):
+        P.canonical_master_precision("bf16")
+    # master + two moments (precision.py:103-108): 4+8, 4+4, 4+2*(1+4/128); FP24 one byte less
+    assert P.bytes_per_param("fp32") == 12
+    assert P.bytes_per_param("bf16") == 8
+    assert P.bytes_per_param("fp8") == pytest.approx(6.0625)
+    assert P.bytes_per_param("fp8", master="fp24") == pytest.approx(5.0625)
+    assert P.bytes_per_param("bf16", moments=1, master="fp24") == 5
+
+
+# ------------------------------------------------- rounding streams and codecs
+
+def test_random_bits_is_the_kernels_counter_hash():
+    lib = O.load_oracle()
+    for offset in (0, 12345, (1 << 31) - 100, (1 << 32) + 7):
+        bits = P.random_bits(offset, 200, seed=0xDEADBEEF).numpy().view(np.uint32)
+        want = [lib.abo_hash32(((offset + i) & 0xFFFFFFFF) ^ 0xDEADBEEF) for i in range(200)]
+        assert bits.tolist() == want, offset
+    seed = 0x1234567
+    assert P.moment_seed(seed, "m") == seed
+    assert P.moment_seed(seed, "v") == lib.abo_hash32(seed ^ 0xA511E9B3)
+    assert P.moment_seed(seed, "p") == lib.abo_hash32(seed ^ 0x6C8E9CF5)
+
+
+def _finite_samples(n, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(n, generator=g) * torch.exp2(torch.randint(-30, 30, (n,), generator=g).float())
+    x[::97] = 0.0
+    x[1::97] = -0.0
+    x[2::97] = 1e-41   # subnormal
+    return x
+
+
+def test_bf16_stochastic_rounding_matches_the_kernels():
+    """(bits + (hash & 0xffff)) >> 16, kernels.c:120-126."""
+    lib = O.load_oracle()
+    x = _finite_samples(20000, 1)
+    seed, offset = 0x9E37, 5000
+    got = P.round_to_bf16_stochastic(x.clone(), seed, offset).view(torch.int16).numpy().view(np.uint16)
+    b = x.numpy().view(np.uint32).astype(np.uint64)
+    r = np.array([lib.abo_hash32((offset + i) ^ seed) for i in range(x.numel())], np.uint64)
+    want = (((b + (r & 0xFFFF)) & 0xFFFFFFFF) >> 16).astype(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_fp24_nearest_matches_the_kernels_and_brute_force():
+    lib = O.load_oracle()
+    x = _finite_samples(20000, 2)
+    got = P.round_to_fp24_nearest_(x.clone()).numpy().view(np.uint32)
+    want = np.array([lib.abo_f24_round(int(b), 0, 0) for b in x.numpy().view(np.uint32)], np.uint32)
+    assert np.array_equal(got, want)
+    # nearest of the two 24-bit neighbours, ties to even
+    b = x.numpy().view(np.uint32).astype(np.int64)
+    down = b & ~0xFF
+    up = down + 0x100
+    xv = x.double().numpy()
+    dd = np.abs(xv - down.astype(np.uint32).view(np.float32).astype(np.float64))
+    du = np.abs(up.astype(np.uint32).view(np.float32).astype(np.float64) - xv)
+    pick = np.where(dd < du, down, np.where(du < dd, up, np.where(down & 0x100, up, down))).astype(np.uint32)
+    assert np.array_equal(got, pick)
+    nan = P.round_to_fp24_nearest_(torch.tensor([float("nan"), -float("inf")]))
+    assert nan[0].isnan() and nan[1] == -float("inf")
+
+
+def test_fp24_stochastic_rounding_is_unbiased():
+    x = torch.full((100_000,), 1.0 + 2 ** -17)   # a quarter of the way between two FP24 values
+    y = P.round_to_fp24_stochastic(x.clone(), seed=3)
+    assert set(y.unique().tolist()) == {1.0, 1.0 + 2 ** -15}
+    assert y.mean().item() == pytest.approx(1.0 + 2 ** -17, abs=0.01 * 2 ** -15)
+
+
+@pytest.mark.parametrize("role", ["m", "v"])
+@pytest.mark.parametrize("stochastic", [False, True])
+def test_fp8_store_encodes_like_the_kernels_block_path(role, stochastic):
+    """Per 128-block: scale = absmax / format max (1 for an all-zero block), codes = the encoder of
+    value / scale, v in the sqrt domain (kernels.c:1049-1057, 857-876)."""
+    lib = O.load_oracle()
+    n = 128 * 20 + 37
+    g = torch.Generator().manual_seed(4 + stochastic)
+    x = torch.randn(n, generator=g) * torch.exp2(torch.randint(-12, 4, (n,), generator=g).float())
+    x[128:256] = 0.0   # an all-zero block
+    if role == "v":
+        x = x.square()
+    seed, offset = 0xABC, 128 * 3
+    store = P.FP8Store(n, role)
+    store.write(0, n, x.clone(), seed=seed if stochastic else None)
+    # the store's block offset is its own element index (0); re-derive with that offset
+    del offset
+    codes = store.q.view(torch.uint8).numpy()
+    scales = store.scale.numpy()
+    vals = np.sqrt(np.maximum(x.numpy(), 0)) if role == "v" else x.numpy()
+    fmax = 448.0 if role == "m" else 57344.0
+    r = 0 if role == "m" else 1
+    for blk in range(-(-n // 128)):
+        lo, hi = blk * 128, min(blk * 128 + 128, n)
+        am = np.float32(np.max(np.abs(vals[lo:hi])))
+        sc = np.float32(am / np.float32(fmax)) if am > 0 else np.float32(1.0)
+        assert scales[blk].view(np.uint32) == sc.view(np.uint32), blk
+        for i in range(lo, hi):
+            q = np.float32(vals[i]) / sc
+            rb = lib.abo_hash32(i ^ seed) if stochastic else 0
+            assert codes[i] == lib.abo_fp8_encode(float(q), int(stochastic), rb, r), (blk, i)
+        assert not codes[hi: blk * 128 + 128].any()
+
+
+def test_fp8_decode_matches_the_kernels_table():
+    for role, dtype in ((0, torch.float8_e4m3fn), (1, torch.float8_e5m2)):
+        table = O.fp8_decode_table(role)
+        got = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(dtype).float().numpy()
+        same = (table.view(np.uint32) == got.view(np.uint32)) | (np.isnan(table) & np.isnan(got))
+        assert same.all()
+
+
+def test_fp8_store_chunked_writes_equal_whole():
+    n = 1000
+    x = torch.randn(n, generator=torch.Generator().manual_seed(5))
+    whole = P.make_store("fp8", n, "m")
+    whole.write(0, n, x.clone(), seed=77)
+    parts = P.make_store("fp8", n, "m")
+    for lo in range(0, n, 256):
+        hi = min(lo + 256, n)
+        parts.write(lo, hi, x[lo:hi].clone(), seed=77)
+    assert torch.equal(whole.q.view(torch.uint8), parts.q.view(torch.uint8))
+    assert torch.equal(whole.scale, parts.scale)
+
+
+@pytest.mark.parametrize("prec", ["bf16", "fp8"])
+def test_ema_stalls_under_nearest_but_not_under_stochastic_rounding(prec):
+    """v <- 0.999 v + 0.001 g^2 cannot leave its starting value under round-to-nearest when each
+    increment is below half an ulp; stochastic rounding tracks the exact EMA on average."""
+    lib = O.load_oracle()
+    n = 4096
+    init = torch.ones(n)
+    init[::128] = 4.0   # one larger element per block, so FP8 scaling cannot make 1.0 exact
+    target = torch.full((n,), 1.5)
+    target[::128] = 4.0
+    tracked = torch.ones(n, dtype=torch.bool)
+    tracked[::128] = False
+    out = {}
+    for sr in (False, True):
+        store = P.make_store(prec, n, "v", init=init)
+        for step in range(1, 401):
+            v = store.to_fp32()
+            v.mul_(0.999).add_(target, alpha=0.001)
+            seed = P.moment_seed(lib.abo_step_seed(0, 0, step), "v") if sr else None
+            store.write(0, n, v, seed=seed)
+        out[sr] = store.to_fp32()[tracked].mean().item()
+    exact = 1.5 - 0.5 * 0.999 ** 400
+    assert out[False] == pytest.approx(1.0, abs=1e-6)
+    assert out[True] == pytest.approx(exact, rel=0.01 if prec == "bf16" else 0.03)
+
+
+@pytest.mark.parametrize("prec", ["fp32", "bf16", "fp8"])
+@pytest.mark.parametrize("role", ["m", "v"])
+def test_store_round_trip_and_state_dict(prec, role):
+    n = 1000
+    x = torch.randn(n, generator=torch.Generator().manual_seed(6)) * 1e-3
+    if role == "v":
+        x = x.abs()
+    store = P.make_store(prec, n, role, init=x)
+    tol = {"fp32": 0.0, "bf16": 2 ** -8, "fp8": 0.25}[prec]
+    assert (store.to_fp32() - x).abs().max().item() <= tol * x.abs().max().item()
+    clone = P.store_from_state_dict(store.state_dict(), n, role)
+    assert torch.equal(clone.to_fp32(), store.to_fp32())
+
+
+def test_store_from_state_dict_rejects_bad_stores():
+    n = 300
+    good = P.make_store("fp8", n, "m", init=torch.randn(n)).state_dict()
+    with pytest.raises(ValueError):
+        P.store_from_state_dict({"precision": "int4", "data": torch.zeros(n)}, n, "m")
+    with pytest.raises(ValueError):
+        P.store_from_state_dict({"precision": "bf16", "data": torch.zeros(n + 1, dtype=torch.bfloat16)}, n, "m")
+    with pytest.raises(ValueError):
+        P.store_from_state_dict({**good, "role": "w"}, n, "m")
+    with pytest.raises(ValueError):
+        P.store_from_state_dict({**good, "block": 0}, n, "m")
+    with pytest.raises(ValueError):
+        P.store_from_state_dict({**good, "scale": good["scale"][:-1]}, n, "m")
+    with pytest.raises(ValueError):
+        P.check_master_state({"precision": "fp24", "hi": torch.zeros(n, dtype=torch.bfloat16),
+                              "lo": torch.zeros(n, dtype=torch.int8)}, n, "master")
+
+
+def test_fp24_master_store_round_trip():
+    n = 1000
+    x = torch.randn(n) * 3
+    store = P.make_master("fp24", n, init=x)
+    y = store.to_fp32()
+    assert store.nbytes == 3 * n
+    assert ((y - x).abs() <= x.abs() * 2 ** -16).all()
+    assert (y.view(torch.int32) & 0xFF == 0).all()
+    clone = P.FP24Store(n)
+    P.load_master_(clone, store.state_dict())
+    assert torch.equal(clone.to_fp32(), y)
+
+
+# ------------------------------------------------------- optimizer, host side
+
+def _params():
+    return [torch.nn.Parameter(torch.zeros(10)), torch.nn.Parameter(torch.zeros(3, 3))]
+
+
+@pytest.mark.parametrize("kwargs", [dict(lr=-1.0), dict(eps=-1.0), dict(betas=(1.0, 0.9)), dict(betas=(0.9, -0.1)),
+                                    dict(weight_decay=-0.1), dict(chunk_size=100), dict(precision="int4"),
+                                    dict(master_precision="fp16"), dict(accumulation_steps=0),
+                                    dict(delay_warmup_steps=-1), dict(gpu_state_budget=-5), dict(backend="torch"),
+                                    dict(backend="cuda"), dict(state_layout="rows")])
+def test_constructor_validates_like_the_reference(kwargs):
+    with pytest.raises(ValueError):
+        ab.AdamBridge(_params(), **kwargs)
+
+
+def test_lion_has_no_eps_and_its_own_defaults():
+    with pytest.raises(TypeError):
+        ab.LionBridge(_params(), eps=1e-8)
+    opt = ab.LionBridge(_params())
+    g = opt.param_groups[0]
+    assert g["lr"] == 1e-4 and g["betas"] == (0.9, 0.99) and g["weight_decay"] == 0.0
+    assert opt.expected_bytes_per_param() == 8
+    assert ab.AdamBridge(_params(), precision="fp8").expected_bytes_per_param() == pytest.approx(6.0625)
+    assert ab.OptiComputeAdamW is ab.AdamBridge
+
+
+def test_host_only_knobs_are_accepted():
+    opt = ab.AdamBridge(_params(), numa_aware=False, num_threads=3, chunk_size=256, transfer_buffer_mb=64,
+                        gpu_state_budget="auto", autotune=ab.AutoTuneConfig(), precision="BF16")
+    assert opt.precision == "bf16"
+    assert opt.autotune_log and opt.tune_threads() == {}
+    assert opt.memory_report()["total"] == 0   # lazy state: nothing allocated before the first update
+
+
+def test_cpu_parameters_are_refused_at_the_first_update():
+    p = torch.nn.Parameter(torch.ones(4))
+    opt = ab.AdamBridge([p])
+    p.grad = torch.ones(4)
+    with pytest.raises(RuntimeError, match="GPU"):
+        opt.step()
+
+
+def test_fresh_state_dict_and_checkpoint_validation():
+    params = _params()
+    opt = ab.AdamBridge(params, precision="fp8")
+    sd = opt.state_dict()
+    assert sd["state"] == {}
+    assert sd["adambridge"] == {"precision": "fp8", "master_precision": "fp32", "format": 1, "algorithm": "adamw"}
+    bad = {"state": {0: {"step": 1, "master": torch.zeros(11), "exp_avg": torch.zeros(10),
+                         "exp_avg_sq": torch.zeros(10)}}, "param_groups": sd["param_groups"]}
+    with pytest.raises(ValueError, match="11 elements"):
+        opt.load_state_dict(bad)
+    lion_ckpt = {"state": {0: {"step": 1, "master": torch.zeros(10), "exp_avg": torch.zeros(10)}},
+                 "param_groups": sd["param_groups"]}
+    with pytest.raises(ValueError, match="exp_avg_sq"):
+        opt.load_state_dict(lion_ckpt)
+    out_of_range = {"state": {5: {"step": 1, "exp_avg": torch.zeros(10), "exp_avg_sq": torch.zeros(10)}},
+                    "param_groups": sd["param_groups"]}
+    with pytest.raises(ValueError, match="parameters"):
+        opt.load_state_dict(out_of_range)
+    assert opt.state_dict()["state"] == {}   # nothing was loaded
+
+
+def test_segment_struct_mirrors_match_the_library():
+    from adambridge_amd import _hip
+    lib = _hip.open_library()
+    assert ctypes.sizeof(_hip.Segment) == lib.adambridge_segment_size() == ctypes.sizeof(O.Segment)
+    assert ctypes.sizeof(_hip.HParams) == lib.adambridge_hparams_size() == ctypes.sizeof(O.HParams)
+    assert ctypes.sizeof(_hip.Group) == lib.adambridge_group_size() == ctypes.sizeof(O.Group)
