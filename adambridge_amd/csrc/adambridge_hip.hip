@@ -484,126 +484,157 @@ __device__ __forceinline__ float group16_max(float x)
     return x;
 }
 
+// FP8 block scale: absmax / format max, 1 for an all-zero block (kernels.c:1049-1057), correctly
+// rounded.  The division by the constant multiplies by its correctly rounded reciprocal and
+// applies one residual correction, which yields the correctly rounded quotient for every absmax
+// >= 2^-100 (checked exhaustively over all floats, for both 448 and 57344); smaller ones divide.
+template <bool E5M2>
+__device__ __forceinline__ float block_scale(float amax)
+{
+    constexpr float kMax = E5M2 ? 57344.0f : 448.0f;
+    constexpr float kInv = E5M2 ? 0x1.24924ap-16f : 0x1.24924ap-9f;   // RN(1 / kMax)
+    if (!(amax > 0.0f)) return 1.0f;
+    if (amax < 0x1p-100f) return amax / kMax;
+    const float q = amax * kInv;
+    const float r = __builtin_fmaf(-q, kMax, amax);
+    return (r < 0.0f || r > 0.0f) ? __builtin_fmaf(r, kInv, q) : q;   // r zero or NaN (inf): q
+}
+
+// One 128-element block, 16 lanes x 8 elements (this lane: e0 .. e0 + 7): decode both moments,
+// update, store master and output, block maxima by shuffles within the 16 lanes, scales, codes.
+// FULL: the whole block lies inside the segment, takes the fused form and allows vector access --
+// straight-line code.  FULL is the same for the 16 lanes of a block, so the shuffles below always
+// run with the whole group active.
+template <int ALGO, int PT, int GT, int OT, bool SR, bool FULL>
+__device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_t b0, int lane)
+{
+    constexpr bool kLion = ALGO == ALGO_LION;
+    const int64_t n = s.n, n_main = s.n_main;
+    const bool vec = FULL || (s.flags & kVec) != 0;
+    uint8_t* const mq = static_cast<uint8_t*>(s.m);
+    uint8_t* const vq = static_cast<uint8_t*>(s.v);
+    const int64_t blk = b0 / kFp8Block;
+    const int64_t e0 = b0 + lane * 8;
+    const uint32_t idx = s.idx0 + (uint32_t)e0;
+    const bool full = FULL || (vec && e0 + 8 <= n);
+    const float sm = ld(s.m_scale + blk);
+    const float sv = kLion ? 0.0f : ld(s.v_scale + blk);
+    // codes are stored padded to whole blocks, so all 8 of this lane's exist
+    const u32x2 cm = vec ? ld(reinterpret_cast<const u32x2*>(mq + e0)) : load_codes8(mq + e0);
+    u32x2 cv = {0u, 0u};
+    if constexpr (!kLion) cv = vec ? ld(reinterpret_cast<const u32x2*>(vq + e0)) : load_codes8(vq + e0);
+    float g[8], p[8], mt[8], vt[8];
+    if (full) {
+        load8<GT>(s.g, e0, g);
+        load_master8<PT>(s, e0, p);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const bool in = e0 + k < n;
+            g[k] = in ? load1<GT>(s.g, e0 + k) : 0.0f;
+            p[k] = in ? load_master1<PT>(s, e0 + k) : 0.0f;
+        }
+    }
+    {
+        float d[8];
+        decode_codes<false>(cm, d);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) mt[k] = d[k] * sm;
+        if constexpr (!kLion) {
+            decode_codes<true>(cv, d);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float u = d[k] * sv;
+                vt[k] = u * u;
+            }
+        }
+    }
+    // the update, FP32 moments in registers; sq = sqrt(new v), reused for the v code below
+    float sq[8];
+    const bool lane_fused = FULL || kLion || e0 + 8 <= n_main;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        if constexpr (kLion) p[k] = lion(p[k], g[k], mt[k], c);
+        else if constexpr (FULL) p[k] = adamw<true>(p[k], g[k], mt[k], vt[k], c, sq[k]);
+        else p[k] = lane_fused ? adamw<true>(p[k], g[k], mt[k], vt[k], c, sq[k])
+                               : adamw_sel(p[k], g[k], mt[k], vt[k], c, e0 + k < n_main, sq[k]);
+    }
+    if (full) {
+        store_master8<PT, SR>(s, e0, p, idx);
+        store_out8<OT>(s.out, e0, p);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if (e0 + k < n) {
+                const float stored = store_master1<PT, SR>(s, e0 + k, p[k], idx + k);
+                store_out1<OT>(s.out, e0 + k, stored);
+            }
+        }
+    }
+    // block maxima (NaN skipped), elements past the end count as zero; v is stored as
+    // sqrt(max(v, 0)), which is sq wherever v > 0 (same correctly rounded root)
+    float am = 0.0f, au = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        if (!FULL && e0 + k >= n) { mt[k] = 0.0f; vt[k] = 0.0f; }
+        const float a = fabsf(mt[k]);
+        am = a > am ? a : am;
+        if constexpr (!kLion) {
+            const float u = vt[k] > 0.0f ? sq[k] : 0.0f;
+            vt[k] = u;
+            au = u > au ? u : au;
+        }
+    }
+    am = group16_max(am);
+    const float scm = block_scale<false>(am);
+    float scu = 1.0f;
+    if constexpr (!kLion) {
+        au = group16_max(au);
+        scu = block_scale<true>(au);
+    }
+    block_quotients(mt, block_div(scm, am));
+    if constexpr (!kLion) block_quotients(vt, block_div(scu, au));
+    uint32_t qm[2] = {0u, 0u}, qv[2] = {0u, 0u};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t ik = idx + k;
+        const bool in = FULL || e0 + k < n;   // padding codes are zero
+        const uint32_t a = e4m3_encode<SR>(mt[k], SR ? hash32(ik ^ s.seed_m) : 0u);
+        qm[k >> 2] |= (in ? a : 0u) << (8 * (k & 3));
+        if constexpr (!kLion) {
+            const uint32_t b = e5m2_encode<SR>(vt[k], SR ? hash32(ik ^ s.seed_v) : 0u);
+            qv[k >> 2] |= (in ? b : 0u) << (8 * (k & 3));
+        }
+    }
+    if (vec) {
+        st(reinterpret_cast<u32x2*>(mq + e0), u32x2{qm[0], qm[1]});
+        if constexpr (!kLion) st(reinterpret_cast<u32x2*>(vq + e0), u32x2{qv[0], qv[1]});
+    } else {
+        store_codes8(mq + e0, qm);
+        if constexpr (!kLion) store_codes8(vq + e0, qv);
+    }
+    if (lane == 0) {
+        st(s.m_scale + blk, scm);
+        if constexpr (!kLion) st(s.v_scale + blk, scu);
+    }
+}
+
 template <int ALGO, int PT, int GT, int OT, bool SR>
 __device__ __forceinline__ void update_tile_fp8(const DevSeg& s, int64_t tile, int64_t T)
 {
     constexpr bool kLion = ALGO == ALGO_LION;
-    const int64_t n = s.n, n_main = s.n_main;
-    const bool vec = (s.flags & kVec) != 0;
     const Coef c = s.c;
     const int lane = threadIdx.x & 15;
     const int group = threadIdx.x >> 4;
-    uint8_t* const mq = static_cast<uint8_t*>(s.m);
-    uint8_t* const vq = static_cast<uint8_t*>(s.v);
-
+    const bool vec = (s.flags & kVec) != 0;
+    // blocks wholly in the fused range (AdamW's scalar tail, if any, is the segment's last n mod W)
+    const int64_t full_end = kLion ? s.n : s.n_main;
     const int64_t lo = (tile - s.tile_begin) * T;
-    const int64_t hi = lo + T < n ? lo + T : n;
-    // one 128-element block per 16-lane group; this lane holds elements e0 .. e0+7
+    const int64_t hi = lo + T < s.n ? lo + T : s.n;
+    // one 128-element block per 16-lane group
     for (int64_t b0 = lo + group * kFp8Block; b0 < hi; b0 += (kThreads / 16) * kFp8Block) {
-        const int64_t blk = b0 / kFp8Block;
-        const int64_t e0 = b0 + lane * 8;
-        const uint32_t idx = s.idx0 + (uint32_t)e0;
-        const bool full = vec && e0 + 8 <= n;
-        const float sm = ld(s.m_scale + blk);
-        const float sv = kLion ? 0.0f : ld(s.v_scale + blk);
-        // codes are stored padded to whole blocks, so all 8 of this lane's exist
-        const u32x2 cm = vec ? ld(reinterpret_cast<const u32x2*>(mq + e0)) : load_codes8(mq + e0);
-        u32x2 cv = {0u, 0u};
-        if constexpr (!kLion) cv = vec ? ld(reinterpret_cast<const u32x2*>(vq + e0)) : load_codes8(vq + e0);
-        float g[8], p[8], mt[8], vt[8];
-        if (full) {
-            load8<GT>(s.g, e0, g);
-            load_master8<PT>(s, e0, p);
-        } else {
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const bool in = e0 + k < n;
-                g[k] = in ? load1<GT>(s.g, e0 + k) : 0.0f;
-                p[k] = in ? load_master1<PT>(s, e0 + k) : 0.0f;
-            }
-        }
-        {
-            float d[8];
-            decode_codes<false>(cm, d);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) mt[k] = d[k] * sm;
-            if constexpr (!kLion) {
-                decode_codes<true>(cv, d);
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const float u = d[k] * sv;
-                    vt[k] = u * u;
-                }
-            }
-        }
-        // the update, FP32 moments in registers; sq = sqrt(new v), reused for the v code below
-        const bool lane_fused = kLion || e0 + 8 <= n_main;
-        float sq[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            if constexpr (kLion) p[k] = lion(p[k], g[k], mt[k], c);
-            else p[k] = lane_fused ? adamw<true>(p[k], g[k], mt[k], vt[k], c, sq[k])
-                                   : adamw_sel(p[k], g[k], mt[k], vt[k], c, e0 + k < n_main, sq[k]);
-        }
-        if (full) {
-            store_master8<PT, SR>(s, e0, p, idx);
-            store_out8<OT>(s.out, e0, p);
-        } else {
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                if (e0 + k < n) {
-                    const float stored = store_master1<PT, SR>(s, e0 + k, p[k], idx + k);
-                    store_out1<OT>(s.out, e0 + k, stored);
-                }
-            }
-        }
-        // block maxima (NaN skipped), elements past the end count as zero; v is stored as
-        // sqrt(max(v, 0)), which is sq wherever v > 0 (same correctly rounded root)
-        float am = 0.0f, au = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const bool in = e0 + k < n;
-            if (!in) { mt[k] = 0.0f; vt[k] = 0.0f; }
-            const float a = fabsf(mt[k]);
-            am = a > am ? a : am;
-            if constexpr (!kLion) {
-                const float u = vt[k] > 0.0f ? sq[k] : 0.0f;
-                vt[k] = u;
-                au = u > au ? u : au;
-            }
-        }
-        am = group16_max(am);
-        const float scm = am > 0.0f ? am / 448.0f : 1.0f;
-        uint32_t qm[2] = {0u, 0u}, qv[2] = {0u, 0u};
-        float scu = 1.0f;
-        if constexpr (!kLion) {
-            au = group16_max(au);
-            scu = au > 0.0f ? au / 57344.0f : 1.0f;
-        }
-        block_quotients(mt, block_div(scm, am));
-        if constexpr (!kLion) block_quotients(vt, block_div(scu, au));
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const uint32_t ik = idx + k;
-            const bool in = e0 + k < n;   // padding codes are zero
-            const uint32_t a = e4m3_encode<SR>(mt[k], SR ? hash32(ik ^ s.seed_m) : 0u);
-            qm[k >> 2] |= (in ? a : 0u) << (8 * (k & 3));
-            if constexpr (!kLion) {
-                const uint32_t b = e5m2_encode<SR>(vt[k], SR ? hash32(ik ^ s.seed_v) : 0u);
-                qv[k >> 2] |= (in ? b : 0u) << (8 * (k & 3));
-            }
-        }
-        if (vec) {
-            st(reinterpret_cast<u32x2*>(mq + e0), u32x2{qm[0], qm[1]});
-            if constexpr (!kLion) st(reinterpret_cast<u32x2*>(vq + e0), u32x2{qv[0], qv[1]});
-        } else {
-            store_codes8(mq + e0, qm);
-            if constexpr (!kLion) store_codes8(vq + e0, qv);
-        }
-        if (lane == 0) {
-            st(s.m_scale + blk, scm);
-            if constexpr (!kLion) st(s.v_scale + blk, scu);
-        }
+        if (vec && b0 + kFp8Block <= full_end) fp8_block<ALGO, PT, GT, OT, SR, true>(s, c, b0, lane);
+        else fp8_block<ALGO, PT, GT, OT, SR, false>(s, c, b0, lane);
     }
 }
 
