@@ -57,7 +57,7 @@ class ParamSlot:
     """Device-side optimizer state of one parameter (reference ParamSlot, engine.py:257-293)."""
 
     __slots__ = ("index", "param", "group", "numel", "step", "master", "out", "out_view", "m", "v", "submitted",
-                 "seg", "small", "done_ev", "in_place", "pending_grad", "packed")
+                 "seg", "seg_ptr", "seg_group", "small", "done_ev", "in_place", "pending_grad", "packed")
 
     def __init__(self, index: int, param: torch.Tensor, group: dict):
         self.index = index
@@ -72,6 +72,8 @@ class ParamSlot:
         self.v: MomentStore | None = None        # None for Lion
         self.submitted = False
         self.seg: _hip.Segment | None = None     # cached kernel descriptor of the buffers above
+        self.seg_ptr = None                      # ctypes pointer to seg
+        self.seg_group: _hip.Group | None = None   # the group struct seg.group points at
         self.small: SmallGroup | None = None
         self.done_ev: torch.cuda.Event | None = None   # the last update of this slot has run
         self.in_place = False                    # master is the FP32 parameter itself
@@ -202,6 +204,7 @@ class UpdateEngine:
             slot.out = torch.empty(slot.numel, dtype=p.dtype, device=dev) if needs_out else None
             slot.out_view = slot.out.view(p.shape) if slot.out is not None else None
         slot.seg = None
+        slot.seg_ptr = None
 
     def _packable(self, slot: ParamSlot) -> bool:
         """The interleaved layout serves AdamW with an FP32 master (a buffer of its own) and BF16 moments."""
@@ -215,12 +218,12 @@ class UpdateEngine:
         slot.m = PackedMoment(packed, "m")
         slot.v = PackedMoment(packed, "v")
         slot.seg = None
+        slot.seg_ptr = None
 
     def _ensure_out(self, slot: ParamSlot) -> None:
         if slot.out is None and not slot.in_place:
             slot.out = torch.empty(slot.numel, dtype=slot.param.dtype, device=slot.param.device)
             slot.out_view = slot.out.view(slot.param.shape)
-            slot.seg = None
 
     def convert_moments(self, slot: ParamSlot, precision: str) -> None:
         """Re-encode a slot's moments in another precision (between steps); the engine's
@@ -236,6 +239,7 @@ class UpdateEngine:
             if self._packable(slot):
                 self._pack(slot)
         slot.seg = None
+        slot.seg_ptr = None
 
     def _pack(self, slot: ParamSlot) -> None:
         """Move an FP32 master and BF16 moments (separate stores) into the interleaved layout."""
@@ -256,6 +260,7 @@ class UpdateEngine:
             slot.packed = None
         slot.m, slot.v = m, v
         slot.seg = None
+        slot.seg_ptr = None
 
     # ------------------------------------------------------------ descriptors
 
@@ -276,24 +281,15 @@ class UpdateEngine:
         g.stochastic = int(self.stochastic)
         return g
 
-    def _segment(self, slot: ParamSlot, grad: torch.Tensor, out: torch.Tensor | None) -> _hip.Segment:
-        seg = slot.seg
-        if seg is None and slot.packed is not None:
-            seg = _hip.Segment()
+    def _new_segment(self, slot: ParamSlot) -> _hip.Segment:
+        """The slot's descriptor: its state buffers, size, index and formats (fixed until the state
+        is replaced); the per-update fields are filled by :meth:`_segment`."""
+        seg = _hip.Segment()
+        if slot.packed is not None:
             seg.p_dtype = _hip.DT_PACKED
             seg.m = seg.v = seg.m_scale = seg.v_scale = seg.p_lo = None
-            seg.n = slot.numel
-            seg.index = slot.index
-            seg.offset = 0
             seg.mv_dtype = _hip.DT_BF16
-            seg.algorithm = _hip.ALGORITHMS[self.algorithm]
-            slot.seg = seg
-        if slot.packed is not None:   # the buffers alternate when double-buffered
-            seg.p = slot.packed.current.data_ptr()
-            other = slot.packed.other
-            seg.p_lo = other.data_ptr() if other is not None else None
-        if seg is None:
-            seg = _hip.Segment()
+        else:
             p_hi, p_lo = slot.master.native_buffers
             seg.p = p_hi.data_ptr()
             seg.p_lo = p_lo.data_ptr() if p_lo is not None else None
@@ -305,34 +301,55 @@ class UpdateEngine:
                 v_data, v_scale = slot.v.native_buffers
                 seg.v = v_data.data_ptr()
                 seg.v_scale = v_scale.data_ptr() if v_scale is not None else None
-            seg.n = slot.numel
-            seg.index = slot.index
-            seg.offset = 0
             seg.mv_dtype = _hip.MOMENT_CODES[slot.m.precision]
-            seg.algorithm = _hip.ALGORITHMS[self.algorithm]
-            slot.seg = seg
-        if grad.dtype not in (torch.float32, torch.bfloat16):
-            raise TypeError(f"gradients must be float32 or bfloat16, got {grad.dtype}")
+        seg.n = slot.numel
+        seg.index = slot.index
+        seg.offset = 0
+        seg.algorithm = _hip.ALGORITHMS[self.algorithm]
+        slot.seg = seg
+        slot.seg_ptr = ctypes.pointer(seg)
+        slot.seg_group = None
+        return seg
+
+    def _segment(self, slot: ParamSlot, grad: torch.Tensor, out_ptr: int | None, out_dtype: torch.dtype | None,
+                 group: _hip.Group):
+        """Pointer to the slot's descriptor, filled in for this update: gradient, output, step, group."""
+        seg = slot.seg
+        if seg is None:
+            seg = self._new_segment(slot)
+        if slot.packed is not None:   # the buffers alternate when double-buffered
+            seg.p = slot.packed.current.data_ptr()
+            other = slot.packed.other
+            seg.p_lo = other.data_ptr() if other is not None else None
+        dt = grad.dtype
+        if dt is torch.bfloat16:
+            seg.g_dtype = _hip.DT_BF16
+        elif dt is torch.float32:
+            seg.g_dtype = _hip.DT_F32
+        else:
+            raise TypeError(f"gradients must be float32 or bfloat16, got {dt}")
         seg.g = grad.data_ptr()
-        seg.g_dtype = _hip.DT_F32 if grad.dtype == torch.float32 else _hip.DT_BF16
-        if out is None:
+        if out_ptr is None:
             seg.out = None
             seg.out_dtype = _hip.DT_NONE
         else:
-            seg.out = out.data_ptr()
-            seg.out_dtype = _hip.DT_F32 if out.dtype == torch.float32 else _hip.DT_BF16
+            seg.out = out_ptr
+            seg.out_dtype = _hip.DT_F32 if out_dtype is torch.float32 else _hip.DT_BF16
         seg.step = slot.step
-        seg.group = ctypes.pointer(self._group_struct(slot.group))
-        return seg
+        if slot.seg_group is not group:
+            seg.group = ctypes.pointer(group)
+            slot.seg_group = group
+        return slot.seg_ptr
 
-    def _target(self, slot: ParamSlot, hooked: bool) -> torch.Tensor | None:
-        """Where the kernel writes the new working weight."""
+    def _target(self, slot: ParamSlot, hooked: bool) -> tuple[int | None, torch.dtype | None]:
+        """Where the kernel writes the new working weight: (device address, dtype), or (None, None)."""
         if slot.in_place:
-            return None                     # the master is the parameter
-        if self.delay or (hooked and not self.overlap_writeback) or not slot.param.is_contiguous():
+            return None, None                   # the master is the parameter
+        p = slot.param
+        if self.delay or (hooked and not self.overlap_writeback) or not p.is_contiguous():
             self._ensure_out(slot)
-            return slot.out
-        return slot.param.data.view(-1)
+            return slot.out.data_ptr(), slot.out.dtype
+        return p.data_ptr(), p.dtype
 
     # ------------------------------------------------------------ submission
 
@@ -347,7 +364,8 @@ class UpdateEngine:
         this update."""
         by_dev: dict[torch.device, list[int]] = {}
         for i, slot in enumerate(slots):
-            self._check_param(slot.param)   # before any device context: CPU tensors get this error
+            if not slot.initialized:
+                self._check_param(slot.param)   # before any device context: CPU tensors get this error
             by_dev.setdefault(slot.param.device, []).append(i)
         for dev, idx in by_dev.items():
             self._update_device(dev, [slots[i] for i in idx], [grads[i] for i in idx], hooked)
@@ -380,14 +398,23 @@ class UpdateEngine:
                     st.side.wait_event(written)
             grads = [g if g.is_contiguous() else g.contiguous() for g in grads]
             segs = []
-            for slot, g in zip(slots, grads):
-                if g.numel() != slot.numel:
-                    raise ValueError(f"gradient of parameter {slot.index} has {g.numel()} elements, "
-                                     f"expected {slot.numel}")
-                if g.device != dev:
-                    raise ValueError(f"gradient of parameter {slot.index} is on {g.device}, parameter on {dev}")
-                slot.step += 1
-                segs.append(ctypes.pointer(self._segment(slot, g, self._target(slot, hooked))))
+            structs: dict[int, _hip.Group] = {}   # each group's hyperparameters, read once per launch
+            try:
+                for slot, g in zip(slots, grads):
+                    if g.numel() != slot.numel:
+                        raise ValueError(f"gradient of parameter {slot.index} has {g.numel()} elements, "
+                                         f"expected {slot.numel}")
+                    if g.device != dev:
+                        raise ValueError(f"gradient of parameter {slot.index} is on {g.device}, parameter on {dev}")
+                    gs = structs.get(id(slot.group))
+                    if gs is None:
+                        gs = structs[id(slot.group)] = self._group_struct(slot.group)
+                    slot.step += 1
+                    segs.append(self._segment(slot, g, *self._target(slot, hooked), gs))
+            except BaseException:
+                for slot in slots[:len(segs)]:
+                    slot.step -= 1
+                raise
             timed = self.timing or self.launch_log is not None
             start = None
             if timed:
