@@ -160,8 +160,12 @@ __device__ __forceinline__ void load8(const void* base, int64_t i, float (&x)[8]
             x[2 * k + 1] = bitsf(u[k] & 0xffff0000u);
         }
     } else {
+        // Two 16-byte loads per lane at a 32-byte lane stride: each load covers half of every cache
+        // line it touches.  Ordinary (cached) loads let the second find the line the first brought
+        // into L2; non-temporal ones fetched most lines twice (measured: 1.39x the FP8 kernel's
+        // algorithmic reads, 8% slower).
         const f32x4* q = reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + i);
-        const f32x4 a = ld(q), b = ld(q + 1);
+        const f32x4 a = *(const ABH_GLOBAL f32x4*)q, b = *(const ABH_GLOBAL f32x4*)(q + 1);
         x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
         x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
     }

@@ -42,8 +42,8 @@ sys.path.insert(0, str(ROOT))
 METRIC = "params updated/sec and achieved HBM GB/s (% roofline), AdamW bf16 moments @7B"
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the update kernel, measured with rocprofv3 FETCH_SIZE + WRITE_SIZE, each
-# scaled by its reading for a copy of known size (profiles/k_update_packed_c3p_hbm_traffic.md).
-MEASURED_TRAFFIC = {"c3p": 134.764e9}
+# scaled by its reading for a copy of known size (profiles/*_hbm_traffic.md).
+MEASURED_TRAFFIC = {"c3p": 134.764e9, "c1": 469.84e6, "c2": 9.8808e9, "c3": 110.48e9, "c4": 24.6996e9}
 
 
 # ------------------------------------------------------------ parameter lists
@@ -412,7 +412,8 @@ def main() -> int:
               file=sys.stderr, flush=True)
     ms_per_step = g["wall"] / args.steps * 1e3
     line = {
-        "metric": METRIC,
+        "metric": METRIC if args.config == "c3p" else
+        f"params updated/sec and achieved HBM GB/s (% roofline), {cfg['desc']} ({args.config})",
         "value": g["params"] * args.steps / g["wall"],
         "unit": "params/s",
         "n_gpus": 1,
