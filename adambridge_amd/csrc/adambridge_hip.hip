@@ -468,12 +468,17 @@ __device__ __forceinline__ void decode_codes(const u32x2 w, float (&x)[8])
     }
 }
 
-// x[k] / scale in place for a lane's 8 elements of one block (see block_div).
+// x[k] / scale in place for a lane's 8 elements of one block (see block_div).  NONNEG: the
+// values are the sqrt-domain v (never -0 or NaN).
+template <bool NONNEG>
 __device__ __forceinline__ void block_quotients(float (&x)[8], const BlockDiv& d)
 {
-    if (d.fast) {
+    if (d.fast && d.pre == 1.0f) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) x[k] = block_quot_fast(x[k], d);
+        for (int k = 0; k < 8; ++k) x[k] = block_quot_fast<false, NONNEG>(x[k], d);
+    } else if (d.fast) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[k] = block_quot_fast<true, NONNEG>(x[k], d);
     } else {
 #pragma unroll
         for (int k = 0; k < 8; ++k) x[k] = x[k] / d.s;
@@ -596,8 +601,8 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
         au = group16_max(au);
         scu = block_scale<true>(au);
     }
-    block_quotients(mt, block_div(scm, am));
-    if constexpr (!kLion) block_quotients(vt, block_div(scu, au));
+    block_quotients<false>(mt, block_div(scm, am));
+    if constexpr (!kLion) block_quotients<true>(vt, block_div(scu, au));
     uint32_t qm[2] = {0u, 0u}, qv[2] = {0u, 0u};
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
