@@ -8,6 +8,7 @@ of parameters per launch.  The public API mirrors the reference package
 
 from . import precision
 from .engine import StepStats
+from .losses import causal_lm_loss
 from .optimizer import AdamBridge, AutoTuneConfig, LionBridge, OptiComputeAdamW
 from .precision import bytes_per_param
 
@@ -20,6 +21,7 @@ __all__ = [
     "AutoTuneConfig",
     "StepStats",
     "bytes_per_param",
+    "causal_lm_loss",
     "precision",
     "__version__",
 ]
