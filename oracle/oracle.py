@@ -186,7 +186,33 @@ def _addr(a: np.ndarray | None) -> int | None:
     return a.ctypes.data
 
 
+def check_sizes(case: Case) -> None:
+    """Raise unless every buffer the segment's kernels will touch holds its n elements (FP8 codes:
+    whole 128-element blocks, one scale per block).  Run before any implementation -- the C oracle,
+    the compiled reference or a GPU launch -- is handed the case."""
+    a, n = case.arrays, case.n
+    nb = -(-n // FP8_BLOCK)
+    lion = case.algorithm == LION
+    need = {"p": n, "g": n}
+    if case.p_dtype == DT_F24:
+        need["p_lo"] = n
+    if case.out_dtype != DT_NONE:
+        need["out"] = n
+    for key in ("m",) + (() if lion else ("v",)):
+        if case.mv_dtype == DT_FP8:
+            need[key] = nb * FP8_BLOCK
+            need[key + "_scale"] = nb
+        else:
+            need[key] = n
+    for key, count in need.items():
+        arr = a.get(key)
+        if arr is None or arr.size < count:
+            raise ValueError(f"case buffer {key!r} holds {None if arr is None else arr.size} elements, "
+                             f"the segment needs {count}")
+
+
 def segment_for(case: Case, group: Group | None = None) -> Segment:
+    check_sizes(case)
     a = case.arrays
     return Segment(p=_addr(a.get("p")), p_lo=_addr(a.get("p_lo")), g=_addr(a.get("g")), m=_addr(a.get("m")),
                    v=_addr(a.get("v")), m_scale=_addr(a.get("m_scale")), v_scale=_addr(a.get("v_scale")),

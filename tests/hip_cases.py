@@ -48,6 +48,8 @@ def run_hip(cases: list[O.Case], width: int = 16, pool: int | None = None,
     ``tensors_hook(i, tensors)`` may replace device tensors before the call (misalignment tests)."""
     kernels = _hip.load()
     work = [c.copy() for c in cases]
+    for c in work:
+        O.check_sizes(c)   # every buffer covers what the launch will touch, before anything runs
     dev = [{k: to_device(a) for k, a in c.arrays.items()} for c in work]
     if tensors_hook is not None:
         for i, t in enumerate(dev):
@@ -146,6 +148,7 @@ def run_hip_packed(cases: list[O.Case], width: int = 16, double_buffer: bool = F
     groups = []
     for c in work:
         assert c.algorithm == O.ADAMW and c.mv_dtype == O.DT_BF16 and c.p_dtype == O.DT_F32
+        O.check_sizes(c)
         state = torch.from_numpy(pack_state(c).view(np.int32)).cuda()
         dst = torch.full_like(state, -1) if double_buffer else None
         g = to_device(c.arrays["g"])

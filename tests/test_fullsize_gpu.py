@@ -92,11 +92,13 @@ def windows(numel: int) -> list[tuple[int, int]]:
     return [(0, WINDOW), (mid, mid + WINDOW), (last, numel)]
 
 
-def run_config(name: str, warm: int = 2, tensors: int = 6) -> None:
-    cfg = bench.CONFIGS[name]
+def run_config(name: str, warm: int = 2, tensors: int = 6, cfg: dict | None = None,
+               windows_of=None) -> None:
+    cfg = cfg or bench.CONFIGS[name]
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     opt, params = bench.build(cfg, dev)
+    windows_of = windows_of or windows
     try:
         for _ in range(warm):
             opt.step()
@@ -107,7 +109,8 @@ def run_config(name: str, warm: int = 2, tensors: int = 6) -> None:
         by_size = sorted(opt._ordered, key=lambda s: -s.numel)[:tensors]
         picks = []
         for slot in opt._ordered:
-            for lo, hi in (windows(slot.numel) if slot in by_size else [(0, min(slot.numel, 256))]):
+            for lo, hi in (windows_of(slot.numel) if slot in by_size else [(0, min(slot.numel, 256))]):
+                assert 0 <= lo < hi <= slot.numel, (slot.index, lo, hi, slot.numel)
                 picks.append((slot, lo, hi))
         group = opt.param_groups[0]
         cases = []
@@ -146,3 +149,19 @@ def run_config(name: str, warm: int = 2, tensors: int = 6) -> None:
 @pytest.mark.parametrize("name", ["c3p", "c3", "c4", "c2", "c1"])
 def test_full_size_config_sampled_parity(name):
     run_config(name)
+
+
+# one tensor past 2^31 elements: 64-bit element indices, and the rounding stream's 32-bit element
+# index wrapping (kernels.c:100-106, idx = uint32(i)); every window lies inside it
+BIG = (1 << 31) + 3 * WINDOW + 1152
+
+
+def _big_windows(numel):
+    around = (1 << 31) - 2048
+    return [(0, WINDOW), (around, around + WINDOW), ((numel - WINDOW) // 128 * 128, numel)]
+
+
+@pytest.mark.parametrize("precision", ["bf16", "fp8"])
+def test_tensor_beyond_2_31_elements(precision):
+    cfg = dict(bench.CONFIGS["c3p"], shapes=lambda: [("big", (BIG,)), ("norm", (4096,))], precision=precision)
+    run_config(f"2^31+ {precision}", warm=1, tensors=1, cfg=cfg, windows_of=_big_windows)
