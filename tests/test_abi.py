@@ -65,3 +65,86 @@ def test_library_is_built_for_gfx950():
 @pytest.mark.parametrize("sym", ["hipMalloc", "hipHostMalloc"])
 def test_links_the_hip_runtime(sym):
     assert sym.encode() in _hip.LIB_PATH.read_bytes()
+
+
+# ------------------------------------------- argument validation, on the host
+
+import ctypes  # noqa: E402
+
+import numpy as np  # noqa: E402
+
+from oracle import oracle as O  # noqa: E402
+
+
+def _segment_variants():
+    """(description, segment mutation, expected code) -- kernels.c:1537-1553 in order; every
+    segment is invalid, so no call below reaches the device."""
+    def m(**kw):
+        return kw
+    return [
+        ("negative n", m(n=-1), -1),
+        ("unknown algorithm", m(algorithm=5), -12),
+        ("unknown master format", m(p_dtype=7), -13),
+        ("no master", m(p=None), -2),
+        ("no gradient", m(g=None), -2),
+        ("no first moment", m(m=None), -2),
+        ("AdamW without v", m(v=None), -2),
+        ("FP24 master without its low plane", m(p_dtype=O.DT_F24, p_lo=None), -2),
+        ("gradient dtype", m(g_dtype=O.DT_FP8), -3),
+        ("moment dtype", m(mv_dtype=O.DT_F24), -4),
+        ("output dtype", m(out_dtype=O.DT_FP8), -5),
+        ("output missing", m(out=None), -6),
+        ("FP8 without scales", m(mv_dtype=O.DT_FP8, m_scale=None), -7),
+        ("negative offset", m(offset=-128), -11),
+        ("FP8 offset not a block multiple", m(mv_dtype=O.DT_FP8, offset=64), -11),
+    ]
+
+
+@pytest.mark.parametrize("desc,mut,code", _segment_variants(), ids=[v[0] for v in _segment_variants()])
+def test_validation_codes_match_the_reference(desc, mut, code):
+    lib = _hip.HipKernels()._lib
+    oracle = O.load_oracle()
+    rng = np.random.default_rng(3)
+    case = O.make_case(rng, 1000, mv_dtype=O.DT_FP8, explicit=False)
+    group = O.group_struct(case.group)
+    hp = O.HParams(0.9, 0.999, 0.1, 0.001, 1.0, 1e-3, 1.0, 1e-8, 7, 1)
+    for need_group in (False, True):
+        seg = O.segment_for(case, group)
+        for k, val in mut.items():
+            setattr(seg, k, val)
+        good = O.segment_for(case, group)   # a valid segment first: validation covers every segment
+        arr = (ctypes.POINTER(O.Segment) * 2)(ctypes.pointer(good), ctypes.pointer(seg))
+        codes = {"oracle": oracle.abo_check_segment(ctypes.byref(seg), int(need_group))}
+        hps = (_hip.HParams * 2)(*[_hip.HParams(*[getattr(hp, f) for f, _ in O.HParams._fields_])] * 2)
+        harr = ctypes.cast(arr, ctypes.POINTER(ctypes.POINTER(_hip.Segment)))
+        codes["hip"] = (lib.adambridge_multi_step(None, harr, 2, 0) if need_group
+                        else lib.adambridge_multi_apply(None, harr, hps, 2, 0))
+        if O.reference_available():
+            ref = O.load_reference()
+            rhps = (O.HParams * 2)(hp, hp)
+            codes["reference"] = (ref.adambridge_multi_step(None, arr, 2, 1) if need_group
+                                  else ref.adambridge_multi_apply(None, arr, rhps, 2, 1))
+        assert set(codes.values()) == {code}, (desc, need_group, codes)
+    # a valid segment without a group: multi_step refuses it (-8)
+    seg = O.segment_for(case, None)
+    arr = (ctypes.POINTER(_hip.Segment) * 1)(ctypes.cast(ctypes.pointer(seg), ctypes.POINTER(_hip.Segment)))
+    assert lib.adambridge_multi_step(None, arr, 1, 0) == -8
+
+
+def test_fused_adamw_argument_codes():
+    """kernels.c:1518-1535: the same checks and codes; none reaches the device."""
+    lib = _hip.HipKernels()._lib
+    hp = _hip.HParams(0.9, 0.999, 0.1, 0.001, 1.0, 1e-3, 1.0, 1e-8, 7, 1)
+    buf = (ctypes.c_float * 16)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    F32, BF16, FP8 = _hip.DT_F32, _hip.DT_BF16, _hip.DT_FP8
+    call = lib.adambridge_fused_adamw
+    assert call(p, p, BF16, p, p, BF16, p, BF16, -1, 0, ctypes.byref(hp)) == -1
+    assert call(p, p, BF16, p, p, BF16, p, BF16, 8, 0, None) == -1
+    assert call(p, p, BF16, p, p, BF16, p, BF16, 0, 0, ctypes.byref(hp)) == 0   # nothing to do
+    assert call(None, p, BF16, p, p, BF16, p, BF16, 8, 0, ctypes.byref(hp)) == -2
+    assert call(p, p, BF16, p, None, BF16, p, BF16, 8, 0, ctypes.byref(hp)) == -2
+    assert call(p, p, FP8, p, p, BF16, p, BF16, 8, 0, ctypes.byref(hp)) == -3
+    assert call(p, p, F32, p, p, FP8, p, BF16, 8, 0, ctypes.byref(hp)) == -4
+    assert call(p, p, F32, p, p, F32, p, FP8, 8, 0, ctypes.byref(hp)) == -5
+    assert call(p, p, F32, p, p, F32, None, BF16, 8, 0, ctypes.byref(hp)) == -6

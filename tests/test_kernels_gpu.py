@@ -224,3 +224,99 @@ def run_hip_packed_unchecked(case):
                        g_dtype=case.g_dtype, out_dtype=0, algorithm=case.algorithm, p_dtype=_hip.DT_PACKED)
     hp = _hip.HParams(**{kk: case.hparams[kk] for kk, _ in _hip.HParams._fields_})
     k.multi_apply(None, k.segment_array([ctypes.pointer(seg)]), [hp])
+
+
+# ------------------------------------------------ fused_adamw, pools, streams
+
+@pytest.mark.parametrize("mv", [O.DT_F32, O.DT_BF16])
+@pytest.mark.parametrize("gt", [O.DT_BF16, O.DT_F32])
+@pytest.mark.parametrize("ot", [O.DT_NONE, O.DT_F32, O.DT_BF16])
+def test_fused_adamw_updates_a_subrange_like_the_oracle(mv, gt, ot):
+    """adambridge_fused_adamw (kernels.c:1518-1535) through HipKernels.fused_adamw: elements
+    [lo, hi) of flat tensors, rounding streams at offset lo, the rest untouched."""
+    from adambridge_amd import _hip
+    from hip_cases import to_device, from_device
+    k = _hip.load()
+    rng = np.random.default_rng(40 + mv * 10 + gt * 3 + ot)
+    n, lo, hi = 10007, 384, 10007 - 5
+    whole = O.make_case(rng, n, mv_dtype=mv, g_dtype=gt, out_dtype=ot, stochastic=True)
+    dev = {key: to_device(a) for key, a in whole.arrays.items()}
+    as_t = lambda key, dt: dev[key].view(dt)  # noqa: E731
+    f32, bf16 = torch.float32, torch.bfloat16
+    mdt = f32 if mv == O.DT_F32 else bf16
+    out = None if ot == O.DT_NONE else as_t("out", f32 if ot == O.DT_F32 else bf16)
+    hp = _hip.HParams(**{f: whole.hparams[f] for f, _ in _hip.HParams._fields_})
+    k.fused_adamw(as_t("p", f32), as_t("g", f32 if gt == O.DT_F32 else bf16), as_t("m", mdt), as_t("v", mdt),
+                  out, hp, lo, hi)
+    part = whole.copy()
+    part.n, part.offset = hi - lo, lo
+    part.arrays = {key: a[lo:hi].copy() for key, a in whole.arrays.items()}
+    want = O.run(part, "oracle", 16)
+    for key, a in whole.arrays.items():
+        got = from_device(dev[key], a)
+        assert np.array_equal(got[:lo].view(np.uint8), a[:lo].view(np.uint8)), key
+        assert np.array_equal(got[hi:].view(np.uint8), a[hi:].view(np.uint8)), key
+        assert np.array_equal(got[lo:hi].view(np.uint8), want.arrays[key].view(np.uint8)), key
+
+
+def test_fused_adamw_python_checks():
+    from adambridge_amd import _hip
+    k = _hip.load()
+    hp = _hip.HParams(0.9, 0.999, 0.1, 0.001, 1.0, 1e-3, 1.0, 1e-8, 7, 1)
+    t = lambda n, dt=torch.float32: torch.zeros(n, dtype=dt, device="cuda")  # noqa: E731
+    with pytest.raises(ValueError):
+        k.fused_adamw(t(8), t(7), t(8), t(8), None, hp, 0, 8)
+    with pytest.raises(TypeError):
+        k.fused_adamw(t(8, torch.bfloat16), t(8), t(8), t(8), None, hp, 0, 8)
+    with pytest.raises(TypeError):
+        k.fused_adamw(t(8), t(8), t(8), t(8, torch.bfloat16), None, hp, 0, 8)
+    with pytest.raises(IndexError):
+        k.fused_adamw(t(8), t(8), t(8), t(8), None, hp, 4, 9)
+    with pytest.raises(ValueError):
+        k.fused_adamw(t(8), torch.zeros(8), t(8), t(8), None, hp, 0, 8)
+
+
+def test_pools_on_two_streams_from_two_threads():
+    """Two launch queues bound to two streams, driven from two host threads at once (the GIL is
+    released in the C calls): each gets the oracle's bytes; pool_threads reports the CUs."""
+    import ctypes
+    import threading
+    from adambridge_amd import _hip
+    from hip_cases import hip_segment, to_device, from_device
+    k = _hip.load()
+    rng = np.random.default_rng(50)
+    sets = [[O.make_case(rng, int(rng.integers(1000, 300000)), mv_dtype=MVS[(i + j) % 3], index=10 * i + j,
+                         offset=128 * j) for j in range(9)] for i in range(2)]
+    want = [O.run_many(cs, "oracle", 16) for cs in sets]
+    pools = [k.create_pool() for _ in range(2)]
+    streams = [torch.cuda.Stream() for _ in range(2)]
+    try:
+        assert k.pool_threads(pools[0]) == torch.cuda.get_device_properties(0).multi_processor_count
+        dev = [[{key: to_device(a) for key, a in c.arrays.items()} for c in cs] for cs in sets]
+        torch.cuda.synchronize()
+        errors = []
+
+        def work(i):
+            try:
+                k.set_pool_stream(pools[i], streams[i])
+                segs = [hip_segment(c, t, None) for c, t in zip(sets[i], dev[i])]
+                hps = [_hip.HParams(**{f: c.hparams[f] for f, _ in _hip.HParams._fields_}) for c in sets[i]]
+                k.multi_apply(pools[i], k.segment_array([ctypes.pointer(s) for s in segs]), hps)
+                k.pool_sync(pools[i])
+            except Exception as exc:  # noqa: BLE001 -- reported by the main thread
+                errors.append(exc)
+
+        threads = [threading.Thread(target=work, args=(i,)) for i in range(2)]
+        for th in threads:
+            th.start()
+        for th in threads:
+            th.join()
+        assert not errors, errors
+        for i in range(2):
+            for c, t, w in zip(sets[i], dev[i], want[i]):
+                got = c.copy()
+                got.arrays = {key: from_device(t[key], a) for key, a in c.arrays.items()}
+                check(w, got)
+    finally:
+        for p in pools:
+            k.destroy_pool(p)
