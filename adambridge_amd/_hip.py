@@ -69,6 +69,7 @@ EXPORTS = (
     "adambridge_fused_adamw", "adambridge_pool_create", "adambridge_pool_destroy", "adambridge_pool_threads",
     "adambridge_pool_set_spin", "adambridge_multi_step", "adambridge_multi_apply", "adambridge_pool_set_stream",
     "adambridge_pool_sync", "adambridge_set_stream", "adambridge_last_error", "adambridge_backend",
+    "adambridge_check_conversions",
 )
 
 
@@ -100,6 +101,7 @@ def open_library(path: Path = LIB_PATH) -> ctypes.CDLL:
         "adambridge_set_stream": (ctypes.c_int, [vp]),
         "adambridge_last_error": (ctypes.c_char_p, []),
         "adambridge_backend": (ctypes.c_char_p, []),
+        "adambridge_check_conversions": (ctypes.c_int, [ctypes.c_uint32, ctypes.POINTER(u64), i32]),
     }
     for name in EXPORTS:
         fn = getattr(lib, name)
@@ -125,6 +127,19 @@ class HipKernels:
     @property
     def backend(self) -> str:
         return self._lib.adambridge_backend().decode()
+
+    CONVERSION_CHECKS = ("stochastic E4M3", "stochastic E5M2", "nearest-even E4M3", "nearest-even E5M2",
+                         "nearest-even BF16")
+
+    def check_conversions(self, seed: int = 0) -> dict[str, int]:
+        """Differing results between the current device's conversion instructions and the
+        reference's rounding rules over every FP32 input in the ranges the kernels use them
+        (adambridge_check_conversions); all zero on a conforming device."""
+        out = (ctypes.c_uint64 * len(self.CONVERSION_CHECKS))()
+        rc = self._lib.adambridge_check_conversions(seed & 0xFFFFFFFF, out, len(out))
+        if rc < 0:
+            raise RuntimeError(f"adambridge_check_conversions: {rc} {self._lib.adambridge_last_error().decode()}")
+        return dict(zip(self.CONVERSION_CHECKS, (int(x) for x in out)))
 
     @property
     def simd_level(self) -> str:

@@ -242,10 +242,9 @@ template <int OT>
 __device__ __forceinline__ void store_out8(void* base, int64_t i, const float (&x)[8])
 {
     if constexpr (OT == DT_BF16) {
-        uint32_t h[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) h[k] = bf16_rne(x[k]);
-        store8_u16(base, i, h);
+        const u32x4 w = {bf16x2_rne(x[0], x[1]), bf16x2_rne(x[2], x[3]), bf16x2_rne(x[4], x[5]),
+                         bf16x2_rne(x[6], x[7])};
+        st(reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + i), w);
     } else if constexpr (OT == DT_F32) {
         store8_f32(base, i, x);
     }
@@ -324,7 +323,7 @@ __device__ __forceinline__ void store_moment2(void* base, int64_t i, float x0, f
 template <int OT>
 __device__ __forceinline__ void store_out2(void* base, int64_t i, float x0, float x1)
 {
-    if constexpr (OT == DT_BF16) store2_u16(base, i, bf16_rne(x0), bf16_rne(x1));
+    if constexpr (OT == DT_BF16) st(reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(base) + i), bf16x2_rne(x0, x1));
     else if constexpr (OT == DT_F32) store2_f32(base, i, x0, x1);
 }
 
@@ -493,6 +492,37 @@ __device__ __forceinline__ float group16_max(float x)
     return x;
 }
 
+// A lane's 8 codes (two words, byte k & 3 of word k >> 2) through gfx950's conversion
+// instructions.  Returns false if some value lies outside the range where those give
+// fp8_encode's code (fp8_hw_range); the words are then to be recomputed in software.
+// idx % 8 == 0: FP8 segments start at multiples of 128 elements and a lane's group at a
+// multiple of 8, so the 8 rounding streams share one hash head.
+template <bool E5M2, bool SR>
+__device__ __forceinline__ bool hw_codes8(const float (&x)[8], uint32_t idx, uint32_t seed, uint32_t (&q)[2])
+{
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) ok &= fp8_hw_range<E5M2, SR>(x[k]);   // no short circuit: no branches
+    if constexpr (SR) {
+        const uint32_t head = hash32_head(idx ^ seed);
+        uint32_t r[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) r[k] = hash32_tail(head ^ (uint32_t)k);
+        uint32_t w = fp8_hw_sr<E5M2, 0>(x[0], r[0], 0u);
+        w = fp8_hw_sr<E5M2, 1>(x[1], r[1], w);
+        w = fp8_hw_sr<E5M2, 2>(x[2], r[2], w);
+        q[0] = fp8_hw_sr<E5M2, 3>(x[3], r[3], w);
+        w = fp8_hw_sr<E5M2, 0>(x[4], r[4], 0u);
+        w = fp8_hw_sr<E5M2, 1>(x[5], r[5], w);
+        w = fp8_hw_sr<E5M2, 2>(x[6], r[6], w);
+        q[1] = fp8_hw_sr<E5M2, 3>(x[7], r[7], w);
+    } else {
+        q[0] = fp8_hw_rne2<E5M2, true>(x[2], x[3], fp8_hw_rne2<E5M2, false>(x[0], x[1], 0u));
+        q[1] = fp8_hw_rne2<E5M2, true>(x[6], x[7], fp8_hw_rne2<E5M2, false>(x[4], x[5], 0u));
+    }
+    return ok;
+}
+
 // FP8 block scale: absmax / format max, 1 for an all-zero block (kernels.c:1049-1057), correctly
 // rounded.  The division by the constant multiplies by its correctly rounded reciprocal and
 // applies one residual correction, which yields the correctly rounded quotient for every absmax
@@ -603,15 +633,30 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     }
     block_quotients<false>(mt, block_div(scm, am));
     if constexpr (!kLion) block_quotients<true>(vt, block_div(scu, au));
+    // codes: full blocks through the conversion instructions; a lane holding a value outside
+    // their exact range (rare: zeros, values below the smallest normal after scaling, NaN) and
+    // partial blocks take the integer encoder
     uint32_t qm[2] = {0u, 0u}, qv[2] = {0u, 0u};
+    bool soft_m = true, soft_v = !kLion;
+    if constexpr (FULL) {
+        soft_m = !hw_codes8<false, SR>(mt, idx, s.seed_m, qm);
+        if constexpr (!kLion) soft_v = !hw_codes8<true, SR>(vt, idx, s.seed_v, qv);
+    }
+    if (soft_m) {
+        qm[0] = qm[1] = 0u;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const uint32_t ik = idx + k;
-        const bool in = FULL || e0 + k < n;   // padding codes are zero
-        const uint32_t a = e4m3_encode<SR>(mt[k], SR ? hash32(ik ^ s.seed_m) : 0u);
-        qm[k >> 2] |= (in ? a : 0u) << (8 * (k & 3));
-        if constexpr (!kLion) {
-            const uint32_t b = e5m2_encode<SR>(vt[k], SR ? hash32(ik ^ s.seed_v) : 0u);
+        for (int k = 0; k < 8; ++k) {
+            const bool in = FULL || e0 + k < n;   // padding codes are zero
+            const uint32_t a = e4m3_encode<SR>(mt[k], SR ? hash32((idx + k) ^ s.seed_m) : 0u);
+            qm[k >> 2] |= (in ? a : 0u) << (8 * (k & 3));
+        }
+    }
+    if (soft_v) {
+        qv[0] = qv[1] = 0u;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const bool in = FULL || e0 + k < n;
+            const uint32_t b = e5m2_encode<SR>(vt[k], SR ? hash32((idx + k) ^ s.seed_v) : 0u);
             qv[k >> 2] |= (in ? b : 0u) << (8 * (k & 3));
         }
     }
@@ -816,6 +861,56 @@ inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
     const int gti = gt == DT_BF16 ? 1 : 0;
     const int oti = ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2;
     return (((algo * 3 + mvi) * 2 + pti) * 2 + gti) * 3 + oti;
+}
+
+// ------------------------------------------------------ conversion self-check
+
+// Every FP32 bit pattern through the conversion instructions the kernels use, compared with the
+// integer forms of the reference's rules (fp8_encode, bf16_rne_soft) in the ranges where the
+// kernels use the instructions.  counts[c] accumulates the differing results of check c:
+// 0 stochastic E4M3, 1 stochastic E5M2, 2 nearest-even E4M3, 3 nearest-even E5M2, 4 BF16.
+// The random bits of input x are hash32(x ^ seed); every byte / half-word position is exercised.
+constexpr int kConvChecks = 5;
+
+template <bool E5M2>
+__device__ __forceinline__ uint32_t sr_code_at(float x, uint32_t r, uint32_t pos)
+{
+    switch (pos) {
+    case 0: return fp8_hw_sr<E5M2, 0>(x, r, 0u) & 0xffu;
+    case 1: return (fp8_hw_sr<E5M2, 1>(x, r, 0u) >> 8) & 0xffu;
+    case 2: return (fp8_hw_sr<E5M2, 2>(x, r, 0u) >> 16) & 0xffu;
+    default: return fp8_hw_sr<E5M2, 3>(x, r, 0u) >> 24;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_check_conversions(unsigned long long* counts, uint32_t seed)
+{
+    unsigned long long c[kConvChecks] = {0ull, 0ull, 0ull, 0ull, 0ull};
+    const uint64_t stride = (uint64_t)gridDim.x * kThreads;
+    for (uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x; i < (1ull << 32); i += stride) {
+        const uint32_t u = (uint32_t)i;
+        const float x = bitsf(u);
+        const uint32_t r = hash32(u ^ seed);
+        const uint32_t pos = (u >> 7) & 3u;
+        if (fp8_hw_range<false, true>(x) && sr_code_at<false>(x, r, pos) != fp8_encode<3, 7, true>(x, r)) ++c[0];
+        if (fp8_hw_range<true, true>(x) && sr_code_at<true>(x, r, pos) != fp8_encode<2, 15, true>(x, r)) ++c[1];
+        if (fp8_hw_range<false, false>(x)) {
+            const uint32_t w = fp8_hw_rne2<false, true>(x, -x, fp8_hw_rne2<false, false>(-x, x, 0u));
+            const uint32_t a = fp8_encode<3, 7, false>(x, 0u), b = fp8_encode<3, 7, false>(-x, 0u);
+            if (w != (b | (a << 8) | (a << 16) | (b << 24))) ++c[2];
+        }
+        if (fp8_hw_range<true, false>(x)) {
+            const uint32_t w = fp8_hw_rne2<true, true>(x, -x, fp8_hw_rne2<true, false>(-x, x, 0u));
+            const uint32_t a = fp8_encode<2, 15, false>(x, 0u), b = fp8_encode<2, 15, false>(-x, 0u);
+            if (w != (b | (a << 8) | (a << 16) | (b << 24))) ++c[3];
+        }
+        const uint32_t h = bf16x2_rne(x, bitsf(u ^ 0x80000000u));
+        if (h != (bf16_rne_soft(x) | (bf16_rne_soft(bitsf(u ^ 0x80000000u)) << 16)) || bf16_rne(x) != bf16_rne_soft(x))
+            ++c[4];
+    }
+#pragma unroll
+    for (int k = 0; k < kConvChecks; ++k)
+        if (c[k]) atomicAdd(&counts[k], c[k]);
 }
 
 }  // namespace abh

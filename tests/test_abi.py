@@ -148,3 +148,11 @@ def test_fused_adamw_argument_codes():
     assert call(p, p, F32, p, p, FP8, p, BF16, 8, 0, ctypes.byref(hp)) == -4
     assert call(p, p, F32, p, p, F32, p, FP8, 8, 0, ctypes.byref(hp)) == -5
     assert call(p, p, F32, p, p, F32, None, BF16, 8, 0, ctypes.byref(hp)) == -6
+
+
+def test_check_conversions_argument_codes():
+    """adambridge_check_conversions rejects a missing or empty result array before any device call."""
+    lib = _hip.open_library()
+    assert lib.adambridge_check_conversions(0, None, 5) == -2
+    buf = (ctypes.c_uint64 * 5)()
+    assert lib.adambridge_check_conversions(0, buf, 0) == -2
