@@ -591,12 +591,15 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     // the update, FP32 moments in registers; sq = sqrt(new v), reused for the v code below
     float sq[8];
     const bool lane_fused = FULL || kLion || e0 + 8 <= n_main;
+    if constexpr (FULL && !kLion) {
+        adamw8_fused(p, g, mt, vt, c, sq);
+    } else {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        if constexpr (kLion) p[k] = lion(p[k], g[k], mt[k], c);
-        else if constexpr (FULL) p[k] = adamw<true>(p[k], g[k], mt[k], vt[k], c, sq[k]);
-        else p[k] = lane_fused ? adamw<true>(p[k], g[k], mt[k], vt[k], c, sq[k])
-                               : adamw_sel(p[k], g[k], mt[k], vt[k], c, e0 + k < n_main, sq[k]);
+        for (int k = 0; k < 8; ++k) {
+            if constexpr (kLion) p[k] = lion(p[k], g[k], mt[k], c);
+            else p[k] = lane_fused ? adamw<true>(p[k], g[k], mt[k], vt[k], c, sq[k])
+                                   : adamw_sel(p[k], g[k], mt[k], vt[k], c, e0 + k < n_main, sq[k]);
+        }
     }
     if (full) {
         store_master8<PT, SR>(s, e0, p, idx);
@@ -868,9 +871,10 @@ inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
 // Every FP32 bit pattern through the conversion instructions the kernels use, compared with the
 // integer forms of the reference's rules (fp8_encode, bf16_rne_soft) in the ranges where the
 // kernels use the instructions.  counts[c] accumulates the differing results of check c:
-// 0 stochastic E4M3, 1 stochastic E5M2, 2 nearest-even E4M3, 3 nearest-even E5M2, 4 BF16.
+// 0 stochastic E4M3, 1 stochastic E5M2, 2 nearest-even E4M3, 3 nearest-even E5M2, 4 BF16,
+// 5 sqrt_mid against sqrtf.
 // The random bits of input x are hash32(x ^ seed); every byte / half-word position is exercised.
-constexpr int kConvChecks = 5;
+constexpr int kConvChecks = 6;
 
 template <bool E5M2>
 __device__ __forceinline__ uint32_t sr_code_at(float x, uint32_t r, uint32_t pos)
@@ -885,7 +889,7 @@ __device__ __forceinline__ uint32_t sr_code_at(float x, uint32_t r, uint32_t pos
 
 __global__ __launch_bounds__(kThreads) void k_check_conversions(unsigned long long* counts, uint32_t seed)
 {
-    unsigned long long c[kConvChecks] = {0ull, 0ull, 0ull, 0ull, 0ull};
+    unsigned long long c[kConvChecks] = {0ull, 0ull, 0ull, 0ull, 0ull, 0ull};
     const uint64_t stride = (uint64_t)gridDim.x * kThreads;
     for (uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x; i < (1ull << 32); i += stride) {
         const uint32_t u = (uint32_t)i;
@@ -907,6 +911,7 @@ __global__ __launch_bounds__(kThreads) void k_check_conversions(unsigned long lo
         const uint32_t h = bf16x2_rne(x, bitsf(u ^ 0x80000000u));
         if (h != (bf16_rne_soft(x) | (bf16_rne_soft(bitsf(u ^ 0x80000000u)) << 16)) || bf16_rne(x) != bf16_rne_soft(x))
             ++c[4];
+        if (sqrt_mid_range(x) && fbits(sqrt_mid(x)) != fbits(__builtin_sqrtf(x))) ++c[5];
     }
 #pragma unroll
     for (int k = 0; k < kConvChecks; ++k)
