@@ -454,10 +454,16 @@ __device__ __forceinline__ void store_codes8(uint8_t* q, const uint32_t (&w)[2])
     for (int k = 0; k < 8; ++k) st(q + k, (uint8_t)(w[k >> 2] >> (8 * (k & 3))));
 }
 
-// The 8 codes of a lane (two words, byte k & 3 of word k >> 2) as FP32.
+// The 8 codes of a lane (two words, byte k & 3 of word k >> 2) as FP32: packed conversions, and
+// on a lane holding a NaN code, per-code conversions that keep the NaN's sign.
 template <bool E5M2>
 __device__ __forceinline__ void decode_codes(const u32x2 w, float (&x)[8])
 {
+    fp8_decode2<E5M2, false>(w.x, x[0], x[1]);
+    fp8_decode2<E5M2, true>(w.x, x[2], x[3]);
+    fp8_decode2<E5M2, false>(w.y, x[4], x[5]);
+    fp8_decode2<E5M2, true>(w.y, x[6], x[7]);
+    if (!fp8_has_nan<E5M2>(w.x, w.y)) return;
     if constexpr (E5M2) {
         x[0] = e5m2_decode<0>(w.x); x[1] = e5m2_decode<1>(w.x); x[2] = e5m2_decode<2>(w.x); x[3] = e5m2_decode<3>(w.x);
         x[4] = e5m2_decode<0>(w.y); x[5] = e5m2_decode<1>(w.y); x[6] = e5m2_decode<2>(w.y); x[7] = e5m2_decode<3>(w.y);
@@ -872,9 +878,10 @@ inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
 // integer forms of the reference's rules (fp8_encode, bf16_rne_soft) in the ranges where the
 // kernels use the instructions.  counts[c] accumulates the differing results of check c:
 // 0 stochastic E4M3, 1 stochastic E5M2, 2 nearest-even E4M3, 3 nearest-even E5M2, 4 BF16,
-// 5 sqrt_mid against sqrtf.
+// 5 sqrt_mid against sqrtf, 6 FP8 decoding (every code of both formats at every byte position:
+// packed conversion, NaN detection, per-code conversion) against the formats' definitions.
 // The random bits of input x are hash32(x ^ seed); every byte / half-word position is exercised.
-constexpr int kConvChecks = 6;
+constexpr int kConvChecks = 7;
 
 template <bool E5M2>
 __device__ __forceinline__ uint32_t sr_code_at(float x, uint32_t r, uint32_t pos)
@@ -887,9 +894,33 @@ __device__ __forceinline__ uint32_t sr_code_at(float x, uint32_t r, uint32_t pos
     }
 }
 
+// Code `code` of format E5M2 (else E4M3FN) placed in byte `pos` of a word with other bytes
+// zero: packed and per-code decoders against fp8_value_soft (NaN: a NaN of the code's sign from
+// the per-code decoder), and NaN detection.
+template <bool E5M2>
+__device__ __forceinline__ bool decode_matches_fmt(uint32_t code, uint32_t pos)
+{
+    const uint32_t word = code << (8 * pos);
+    float x[8];
+    decode_codes<E5M2>(u32x2{word, 0u}, x);
+    float y[8];
+    decode_codes<E5M2>(u32x2{0u, word}, y);
+    const float want = fp8_value_soft<E5M2>(code);
+    const float got = x[pos], got_hi = y[4 + pos];
+    const bool nan = want != want;
+    if (fp8_has_nan<E5M2>(word, 0u) != nan) return false;
+    if (nan) return got != got && got_hi != got_hi && (fbits(got) >> 31) == (code >> 7) && (fbits(got_hi) >> 31) == (code >> 7);
+    return fbits(got) == fbits(want) && fbits(got_hi) == fbits(want);
+}
+
+__device__ __forceinline__ bool decode_matches(uint32_t code, uint32_t e5m2, uint32_t pos)
+{
+    return e5m2 ? decode_matches_fmt<true>(code, pos) : decode_matches_fmt<false>(code, pos);
+}
+
 __global__ __launch_bounds__(kThreads) void k_check_conversions(unsigned long long* counts, uint32_t seed)
 {
-    unsigned long long c[kConvChecks] = {0ull, 0ull, 0ull, 0ull, 0ull, 0ull};
+    unsigned long long c[kConvChecks] = {0ull, 0ull, 0ull, 0ull, 0ull, 0ull, 0ull};
     const uint64_t stride = (uint64_t)gridDim.x * kThreads;
     for (uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x; i < (1ull << 32); i += stride) {
         const uint32_t u = (uint32_t)i;
@@ -912,6 +943,7 @@ __global__ __launch_bounds__(kThreads) void k_check_conversions(unsigned long lo
         if (h != (bf16_rne_soft(x) | (bf16_rne_soft(bitsf(u ^ 0x80000000u)) << 16)) || bf16_rne(x) != bf16_rne_soft(x))
             ++c[4];
         if (sqrt_mid_range(x) && fbits(sqrt_mid(x)) != fbits(__builtin_sqrtf(x))) ++c[5];
+        if (i < 2048u && !decode_matches(u & 0xffu, (u >> 8) & 1u, u >> 9)) ++c[6];
     }
 #pragma unroll
     for (int k = 0; k < kConvChecks; ++k)

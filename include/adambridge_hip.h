@@ -194,11 +194,12 @@ ADAMBRIDGE_API const char* adambridge_backend(void);
  * those give the reference's codes (kernels.c:108-112, 857-876), and take square roots with a
  * short sequence where it equals sqrtf; this runs every FP32 bit pattern through them and through
  * integer forms of the reference's rules (sqrtf), in those ranges, with random bits
- * hash32(x ^ seed) for the stochastic ones.  Writes min(count, 6) counts of differing results:
+ * hash32(x ^ seed) for the stochastic ones.  Writes min(count, 7) counts of differing results:
  * [0] stochastic E4M3, [1] stochastic E5M2, [2] nearest-even E4M3, [3] nearest-even E5M2,
  * [4] BF16 nearest-even, [5] the short square root (v_sqrt_f32 and a neighbour correction,
- * 2^-100 <= x < 2^100) against the correctly rounded sqrtf -- all zero on a conforming device.
- * Returns the number of checks (6),
+ * 2^-100 <= x < 2^100) against the correctly rounded sqrtf, [6] FP8 decoding of every code of
+ * both formats against the formats' definitions -- all zero on a conforming device.
+ * Returns the number of checks (7),
  * ADAMBRIDGE_ENULL for a NULL array or count < 1, ADAMBRIDGE_EHIP on a HIP failure. */
 ADAMBRIDGE_API int adambridge_check_conversions(uint32_t seed, uint64_t* mismatches, int32_t count);
 
