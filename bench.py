@@ -387,6 +387,10 @@ def main() -> int:
     ap.add_argument("--traffic", type=float, default=None,
                     help="HBM bytes per launch measured by rocprofv3 (FETCH_SIZE+WRITE_SIZE, scaled); "
                          "default: the figure measured for this configuration, when there is one")
+    ap.add_argument("--rebuilds", type=int, default=1, metavar="N",
+                    help="diagnostic: build and time the state N times in this process, printing each "
+                         "on stderr (the GPU's power state can change between them); the JSON line "
+                         "reports the first")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="first run 3 device-to-device copies of BYTES bytes (a known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -395,8 +399,8 @@ def main() -> int:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
               "the update shards by element ranges, see DESIGN.md", file=sys.stderr)
         return 2
-    if args.steps < 1 or args.warmup < 0:
-        ap.error("--steps must be >= 1 and --warmup >= 0")
+    if args.steps < 1 or args.warmup < 0 or args.rebuilds < 1:
+        ap.error("--steps and --rebuilds must be >= 1 and --warmup >= 0")
     if args.config == "c5":
         return main_pipeline(args)
     cfg = CONFIGS[args.config]
@@ -406,6 +410,10 @@ def main() -> int:
           file=sys.stderr, flush=True)
     g = gpu_bench(cfg, args.steps, args.warmup, args.layout, args.double_buffer)
     print(f"[bench] GPU: {g['kernel_ms']:.3f} ms/launch, {g['achieved_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+    for k in range(1, args.rebuilds):
+        r = gpu_bench(cfg, args.steps, args.warmup, args.layout, args.double_buffer)
+        print(f"[bench] rebuild {k}: {r['kernel_ms']:.3f} ms/launch, {r['achieved_gbs']:.0f} GB/s", file=sys.stderr,
+              flush=True)
     cpu = None if args.no_cpu else cpu_bench(cfg, args.cpu_params, args.cpu_steps)
     if cpu is not None:
         print(f"[bench] CPU reference: {cpu['ms_per_step']:.1f} ms/step on {cpu['cores']} threads",

@@ -684,7 +684,7 @@ def _oracle_state_after(params_bf16, grads_seq, precision, master, lr, wd, betas
 
 @pytest.mark.parametrize("precision,master,lion", [("bf16", "fp32", False), ("fp32", "fp32", False),
                                                    ("fp8", "fp24", False), ("bf16", "fp24", True),
-                                                   ("fp8", "fp32", True)])
+                                                   ("fp8", "fp32", True), ("fp8", "fp32", False)])
 @pytest.mark.parametrize("hooks", [False, True])
 def test_api_updates_are_bit_exact_against_the_oracle(precision, master, lion, hooks):
     """AdamBridge/LionBridge on bf16 parameters (sync step or per-parameter hooks plus a batched
