@@ -69,7 +69,7 @@ EXPORTS = (
     "adambridge_fused_adamw", "adambridge_pool_create", "adambridge_pool_destroy", "adambridge_pool_threads",
     "adambridge_pool_set_spin", "adambridge_multi_step", "adambridge_multi_apply", "adambridge_pool_set_stream",
     "adambridge_pool_sync", "adambridge_set_stream", "adambridge_last_error", "adambridge_backend",
-    "adambridge_check_conversions",
+    "adambridge_check_conversions", "adambridge_convert",
 )
 
 
@@ -102,6 +102,7 @@ def open_library(path: Path = LIB_PATH) -> ctypes.CDLL:
         "adambridge_last_error": (ctypes.c_char_p, []),
         "adambridge_backend": (ctypes.c_char_p, []),
         "adambridge_check_conversions": (ctypes.c_int, [ctypes.c_uint32, ctypes.POINTER(u64), i32]),
+        "adambridge_convert": (ctypes.c_int, [vp, vp, i32, vp, vp, i32, i64, i32]),
     }
     for name in EXPORTS:
         fn = getattr(lib, name)
@@ -207,6 +208,43 @@ class HipKernels:
         hps = (HParams * len(hparams))(*hparams)
         self._check(self._lib.adambridge_multi_apply(pool, segments, hps, len(segments), threads),
                     "adambridge_multi_apply")
+
+    _CONVERT_DTYPES = {torch.float32: DT_F32, torch.bfloat16: DT_BF16, torch.float8_e4m3fn: DT_FP8,
+                       torch.float8_e5m2: DT_FP8, torch.uint8: DT_FP8}
+
+    def convert(self, src: torch.Tensor, src_scale: torch.Tensor | None, dst: torch.Tensor,
+                dst_scale: torch.Tensor | None, n: int, role: str) -> None:
+        """Re-encode ``n`` values of moment ``role`` ('m' or 'v') from ``src`` into ``dst`` on the current
+        stream (adambridge_convert).  Formats follow the dtypes: float32, bfloat16, or FP8 codes (an
+        FP8 / uint8 tensor padded to whole 128-element blocks, with one float32 scale per block)."""
+        if role not in ("m", "v"):
+            raise ValueError(f"role must be 'm' or 'v', got {role!r}")
+        codes = []
+        for what, t, scale in (("source", src, src_scale), ("destination", dst, dst_scale)):
+            if t.device.type != "cuda" or not t.is_contiguous():
+                raise ValueError(f"convert: the {what} must be a contiguous device tensor")
+            code = self._CONVERT_DTYPES.get(t.dtype)
+            if code is None:
+                raise TypeError(f"convert: unsupported {what} dtype {t.dtype}")
+            nb = -(-n // 128)
+            need = nb * 128 if code == DT_FP8 else n
+            if t.numel() < need:
+                raise ValueError(f"convert: the {what} holds {t.numel()} values, {need} needed")
+            if code == DT_FP8:
+                if scale is None or scale.dtype != torch.float32 or not scale.is_contiguous() or scale.numel() < nb:
+                    raise ValueError(f"convert: the FP8 {what} needs {nb} contiguous float32 scales")
+                if scale.device != t.device:
+                    raise ValueError("convert: scales on another device")
+            codes.append(code)
+        if src.device != dst.device:
+            raise ValueError("convert: source and destination on different devices")
+        with torch.cuda.device(dst.device):
+            self._lib.adambridge_set_stream(torch.cuda.current_stream(dst.device).cuda_stream)
+            rc = self._lib.adambridge_convert(src.data_ptr(), src_scale.data_ptr() if codes[0] == DT_FP8 else None,
+                                              codes[0], dst.data_ptr(),
+                                              dst_scale.data_ptr() if codes[1] == DT_FP8 else None, codes[1], n,
+                                              0 if role == "m" else 1)
+        self._check(rc, "adambridge_convert")
 
     def fused_adamw(self, master: torch.Tensor, grad: torch.Tensor, m: torch.Tensor, v: torch.Tensor,
                     out: torch.Tensor | None, hp: HParams, lo: int, hi: int) -> None:

@@ -872,6 +872,103 @@ inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
     return (((algo * 3 + mvi) * 2 + pti) * 2 + gti) * 3 + oti;
 }
 
+// ----------------------------------------------------- storage conversion kernel
+
+// Re-encoding of one moment (or an FP32 master) between storage formats, the device form of the
+// reference's torch-side stores (precision.py:341-418): values decoded exactly (FP8: code x
+// scale, squared for the sqrt-domain v), then encoded to nearest: BF16, or FP8 per 128-element
+// block with v = sqrt(clamp(v, min=0)), scale = absmax / format max (1 for an all-zero block, and,
+// as torch's amax propagates NaN, for a block holding a NaN), codes of clamp(x / scale, +-max).
+// NaN encodes as torch's casts encode it: BF16 0x7fc0, FP8 0x7f with the value's sign (E5M2
+// included, where the update kernel's code is 0x7e).  Positions past n encode as zero (padding).
+// 16 lanes per block, element b0 + 16k + lane for k < 8: every access of the 16 lanes is
+// contiguous.
+template <int SRC, int DST, bool V>
+__global__ __launch_bounds__(kThreads) void k_convert(const void* src, const float* src_scale, void* dst,
+                                                      float* dst_scale, int64_t n)
+{
+    const int64_t nb = (n + kFp8Block - 1) / kFp8Block;
+    const int64_t blk = (int64_t)blockIdx.x * (kThreads / 16) + (threadIdx.x >> 4);
+    if (blk >= nb) return;   // a 16-lane group leaves whole: the shuffles below stay within live groups
+    const int lane = threadIdx.x & 15;
+    const int64_t b0 = blk * kFp8Block;
+    float x[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int64_t e = b0 + 16 * k + lane;
+        float val = 0.0f;
+        if constexpr (SRC == DT_FP8) {   // codes exist for the whole padded block
+            const uint32_t code = ld(static_cast<const uint8_t*>(src) + e);
+            const float u = (V ? e5m2_decode<0>(code) : e4m3_decode<0>(code)) * ld(src_scale + blk);
+            val = V ? u * u : u;
+            if (e >= n) val = 0.0f;
+        } else if (e < n) {
+            if constexpr (SRC == DT_BF16) val = bitsf((uint32_t)ld(static_cast<const uint16_t*>(src) + e) << 16);
+            else val = ld(static_cast<const float*>(src) + e);
+        }
+        x[k] = val;
+    }
+    if constexpr (DST == DT_F32 || DST == DT_BF16) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int64_t e = b0 + 16 * k + lane;
+            if (e >= n) continue;
+            if constexpr (DST == DT_F32) st(static_cast<float*>(dst) + e, x[k]);
+            else st(static_cast<uint16_t*>(dst) + e, (uint16_t)(x[k] != x[k] ? 0x7fc0u : bf16_rne(x[k])));
+        }
+    } else {
+        constexpr float kMax = V ? 57344.0f : 448.0f;
+        float amax = 0.0f;
+        int nan = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if constexpr (V) x[k] = __builtin_sqrtf(x[k] < 0.0f ? 0.0f : x[k]);   // NaN and -0 pass through
+            const float a = fabsf(x[k]);
+            nan |= a != a;
+            amax = a > amax ? a : amax;
+        }
+#pragma unroll
+        for (int d = 1; d < 16; d <<= 1) {
+            amax = fmaxf(amax, __shfl_xor(amax, d, 16));
+            nan |= __shfl_xor(nan, d, 16);
+        }
+        const float scale = (!nan && amax > 0.0f) ? amax / kMax : 1.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            float y = x[k] / scale;
+            y = y > kMax ? kMax : (y < -kMax ? -kMax : y);   // NaN passes
+            const uint32_t code = y != y ? ((fbits(y) >> 24) & 0x80u) | 0x7fu
+                                         : V ? e5m2_encode<false>(y, 0u) : e4m3_encode<false>(y, 0u);
+            st(static_cast<uint8_t*>(dst) + b0 + 16 * k + lane, (uint8_t)code);
+        }
+        if (lane == 0) st(dst_scale + blk, scale);
+    }
+}
+
+using ConvertFn = void (*)(const void*, const float*, void*, float*, int64_t);
+
+template <int SRC, int DST>
+constexpr ConvertFn convert_for(bool v)
+{
+    return v ? &k_convert<SRC, DST, true> : &k_convert<SRC, DST, false>;
+}
+
+inline ConvertFn convert_kernel(int src, int dst, bool v)
+{
+    const int si = src == DT_F32 ? 0 : src == DT_BF16 ? 1 : 2, di = dst == DT_F32 ? 0 : dst == DT_BF16 ? 1 : 2;
+    switch (si * 3 + di) {
+    case 0: return convert_for<DT_F32, DT_F32>(v);
+    case 1: return convert_for<DT_F32, DT_BF16>(v);
+    case 2: return convert_for<DT_F32, DT_FP8>(v);
+    case 3: return convert_for<DT_BF16, DT_F32>(v);
+    case 4: return convert_for<DT_BF16, DT_BF16>(v);
+    case 5: return convert_for<DT_BF16, DT_FP8>(v);
+    case 6: return convert_for<DT_FP8, DT_F32>(v);
+    case 7: return convert_for<DT_FP8, DT_BF16>(v);
+    default: return convert_for<DT_FP8, DT_FP8>(v);
+    }
+}
+
 // ------------------------------------------------------ conversion self-check
 
 // Every FP32 bit pattern through the conversion instructions the kernels use, compared with the

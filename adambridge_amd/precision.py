@@ -215,20 +215,34 @@ class FP32Store(MomentStore):
         return {"precision": "fp32", "data": self.data}
 
 
+def _device_encode(x: torch.Tensor, dst: torch.Tensor, dst_scale: torch.Tensor | None, n: int, role: str) -> None:
+    """Nearest-even encode of ``n`` values into a device store's buffers with the library's
+    conversion kernel (adambridge_convert): the same bits as the torch casts below produce on the
+    host, in one pass over HBM."""
+    from . import _hip   # the library is needed only once a store lives on the device
+
+    src = x.detach().reshape(-1)[:n].to(dst.device, torch.float32).contiguous()
+    _hip.load().convert(src, None, dst, dst_scale, n, role)
+
+
 class BF16Store(MomentStore):
+    """BF16 values, nearest-even from FP32 (torch's rounding: NaN becomes 0x7fc0)."""
+
     precision = "bf16"
 
     def __init__(self, numel: int, init: torch.Tensor | None = None, device=None):
         super().__init__(numel, device)
         self.data = torch.zeros(numel, dtype=torch.bfloat16, device=self.device)
         if init is not None:
-            self.data.copy_(init.detach().reshape(-1))   # torch rounds to nearest even
+            self.write(0, numel, init)
 
     def write(self, lo, hi, x, seed=None):
         if seed is not None:
             self.data[lo:hi].copy_(round_to_bf16_stochastic(x, seed, lo))
+        elif self.data.is_cuda:
+            _device_encode(x, self.data[lo:hi], None, hi - lo, "m")
         else:
-            self.data[lo:hi].copy_(x)
+            self.data[lo:hi].copy_(x.detach().reshape(-1))   # torch rounds to nearest even
 
     def to_fp32(self):
         return self.data.float()
@@ -277,6 +291,11 @@ class FP8Store(MomentStore):
     def write(self, lo, hi, x, seed=None):
         n = hi - lo
         b0, b1 = lo // self.block, math.ceil(hi / self.block)
+        if seed is None and self.q.is_cuda and self.block == FP8_BLOCK:
+            if lo % self.block:
+                raise ValueError("FP8 writes start on a block boundary")
+            _device_encode(x, self.q[b0 * self.block: b1 * self.block], self.scale[b0:b1], n, self.role)
+            return
         if self.sqrt_domain:
             x = x.clamp_(min=0).sqrt_()
         padded = (b1 - b0) * self.block

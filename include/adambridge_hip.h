@@ -189,6 +189,19 @@ ADAMBRIDGE_API const char* adambridge_last_error(void);
 /* Name of the device code this library carries, e.g. "hip/gfx950". */
 ADAMBRIDGE_API const char* adambridge_backend(void);
 
+/* Re-encodes n values of one moment (role 0: m, FP8 as E4M3FN; role 1: v, FP8 as E5M2 of
+ * sqrt(v)) or of an FP32 master (role 0) from src_dtype to dst_dtype (ADAMBRIDGE_DT_F32, _BF16 or
+ * _FP8), on the calling thread's stream (asynchronous).  The device form of the conversions the
+ * reference's stores make with torch when precision or a checkpoint's format changes
+ * (precision.py:341-418, 555-575; engine.py:1030-1043): values decoded exactly, then encoded to
+ * nearest -- BF16, or FP8 per 128-element block with scale = absmax / format max (1 for an
+ * all-zero block or one holding a NaN), v in the sqrt domain after clamping at zero.  FP8 buffers
+ * hold codes padded to whole blocks (all written) and one scale per block.  Returns 0,
+ * ADAMBRIDGE_EBADN (n < 0), _EMVDTYPE (unknown dtype or role), _ENULL, _ESCALES (FP8 without its
+ * scales) or _EHIP (launch failure). */
+ADAMBRIDGE_API int adambridge_convert(const void* src, const float* src_scale, int32_t src_dtype, void* dst,
+                                      float* dst_scale, int32_t dst_dtype, int64_t n, int32_t role);
+
 /* Self-check of the device's conversion and square-root instructions, on the current device
  * (synchronous).  The kernels round to FP8 and BF16 with gfx950's conversion instructions wherever
  * those give the reference's codes (kernels.c:108-112, 857-876), and take square roots with a

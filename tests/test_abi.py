@@ -156,3 +156,20 @@ def test_check_conversions_argument_codes():
     assert lib.adambridge_check_conversions(0, None, 5) == -2
     buf = (ctypes.c_uint64 * 5)()
     assert lib.adambridge_check_conversions(0, buf, 0) == -2
+
+
+def test_convert_argument_codes():
+    """adambridge_convert's checks; none reaches the device."""
+    lib = _hip.open_library()
+    buf = (ctypes.c_float * 16)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    F32, BF16, FP8 = _hip.DT_F32, _hip.DT_BF16, _hip.DT_FP8
+    assert lib.adambridge_convert(p, None, F32, p, None, BF16, -1, 0) == -1
+    assert lib.adambridge_convert(p, None, F32, p, None, 7, 8, 0) == -4
+    assert lib.adambridge_convert(p, None, _hip.DT_F24, p, None, F32, 8, 0) == -4
+    assert lib.adambridge_convert(p, None, F32, p, None, BF16, 8, 2) == -4
+    assert lib.adambridge_convert(p, None, F32, p, None, BF16, 0, 0) == 0
+    assert lib.adambridge_convert(None, None, F32, p, None, BF16, 8, 0) == -2
+    assert lib.adambridge_convert(p, None, F32, None, None, BF16, 8, 0) == -2
+    assert lib.adambridge_convert(p, None, FP8, p, None, F32, 8, 0) == -7
+    assert lib.adambridge_convert(p, None, F32, p, None, FP8, 8, 1) == -7
