@@ -130,7 +130,7 @@ class HipKernels:
         return self._lib.adambridge_backend().decode()
 
     CONVERSION_CHECKS = ("stochastic E4M3", "stochastic E5M2", "nearest-even E4M3", "nearest-even E5M2",
-                         "nearest-even BF16", "short sqrt", "FP8 decode")
+                         "nearest-even BF16", "square roots", "FP8 decode")
 
     def check_conversions(self, seed: int = 0) -> dict[str, int]:
         """Differing results between the current device's conversion instructions and the

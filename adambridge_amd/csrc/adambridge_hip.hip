@@ -975,7 +975,8 @@ inline ConvertFn convert_kernel(int src, int dst, bool v)
 // integer forms of the reference's rules (fp8_encode, bf16_rne_soft) in the ranges where the
 // kernels use the instructions.  counts[c] accumulates the differing results of check c:
 // 0 stochastic E4M3, 1 stochastic E5M2, 2 nearest-even E4M3, 3 nearest-even E5M2, 4 BF16,
-// 5 sqrt_mid against sqrtf, 6 FP8 decoding (every code of both formats at every byte position:
+// 5 square roots (sqrtf on every finite x >= 0, sqrt_mid on its range) against the exact nearest
+// root, 6 FP8 decoding (every code of both formats at every byte position:
 // packed conversion, NaN detection, per-code conversion) against the formats' definitions.
 // The random bits of input x are hash32(x ^ seed); every byte / half-word position is exercised.
 constexpr int kConvChecks = 7;
@@ -989,6 +990,40 @@ __device__ __forceinline__ uint32_t sr_code_at(float x, uint32_t r, uint32_t pos
     case 2: return (fp8_hw_sr<E5M2, 2>(x, r, 0u) >> 16) & 0xffu;
     default: return fp8_hw_sr<E5M2, 3>(x, r, 0u) >> 24;
     }
+}
+
+// Whether s is the float nearest to sqrt(x), for finite x >= 0, in exact integer arithmetic
+// (no floating-point operation involved): with x = X 2^ex and s = S 2^es (S, X the significands),
+// s is nearest iff 16 X 2^(ex - 2 es) lies strictly between (4S - 2)^2 and (4S + 2)^2 -- (4S - 1)^2
+// below a power of two, where the float beneath is only half an ulp away.  Ties cannot occur.
+__device__ __forceinline__ void float_parts(uint32_t b, uint64_t& m, int& e)
+{
+    const uint32_t be = (b >> 23) & 0xffu, bm = b & 0x7fffffu;
+    m = be ? (bm | 0x800000u) : bm;
+    e = be ? (int)be - 150 : -149;
+}
+
+__device__ bool is_nearest_root(uint32_t xb, uint32_t sb)
+{
+    if (xb == 0u) return sb == 0u;
+    uint64_t X, S;
+    int ex, es;
+    float_parts(xb, X, ex);
+    float_parts(sb, S, es);
+    if (S == 0u || (sb >> 31)) return false;
+    typedef unsigned __int128 u128;
+    const uint64_t l4 = (S == 0x800000u && es > -149) ? 4 * S - 1 : 4 * S - 2;
+    u128 L = (u128)(16 * X), lo = (u128)l4 * l4, hi = (u128)(4 * S + 2) * (4 * S + 2);
+    const int k = ex - 2 * es;
+    if (k >= 0) {
+        if (k > 70) return false;
+        L <<= k;
+    } else {
+        if (-k > 70) return false;
+        lo <<= -k;
+        hi <<= -k;
+    }
+    return lo < L && L < hi;
 }
 
 // Code `code` of format E5M2 (else E4M3FN) placed in byte `pos` of a word with other bytes
@@ -1039,7 +1074,9 @@ __global__ __launch_bounds__(kThreads) void k_check_conversions(unsigned long lo
         const uint32_t h = bf16x2_rne(x, bitsf(u ^ 0x80000000u));
         if (h != (bf16_rne_soft(x) | (bf16_rne_soft(bitsf(u ^ 0x80000000u)) << 16)) || bf16_rne(x) != bf16_rne_soft(x))
             ++c[4];
-        if (sqrt_mid_range(x) && fbits(sqrt_mid(x)) != fbits(__builtin_sqrtf(x))) ++c[5];
+        if (u < 0x7f800000u &&   // x >= 0, finite: sqrtf, and the short form on its range, are the nearest root
+            (!is_nearest_root(u, fbits(__builtin_sqrtf(x))) || (sqrt_mid_range(x) && !is_nearest_root(u, fbits(sqrt_mid(x))))))
+            ++c[5];
         if (i < 2048u && !decode_matches(u & 0xffu, (u >> 8) & 1u, u >> 9)) ++c[6];
     }
 #pragma unroll

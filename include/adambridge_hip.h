@@ -209,8 +209,9 @@ ADAMBRIDGE_API int adambridge_convert(const void* src, const float* src_scale, i
  * integer forms of the reference's rules (sqrtf), in those ranges, with random bits
  * hash32(x ^ seed) for the stochastic ones.  Writes min(count, 7) counts of differing results:
  * [0] stochastic E4M3, [1] stochastic E5M2, [2] nearest-even E4M3, [3] nearest-even E5M2,
- * [4] BF16 nearest-even, [5] the short square root (v_sqrt_f32 and a neighbour correction,
- * 2^-100 <= x < 2^100) against the correctly rounded sqrtf, [6] FP8 decoding of every code of
+ * [4] BF16 nearest-even, [5] square roots -- sqrtf on every finite x >= 0, and the short form
+ * (v_sqrt_f32 and a neighbour correction) on 2^-100 <= x < 2^100 -- against the nearest root
+ * decided in exact integer arithmetic, [6] FP8 decoding of every code of
  * both formats against the formats' definitions -- all zero on a conforming device.
  * Returns the number of checks (7),
  * ADAMBRIDGE_ENULL for a NULL array or count < 1, ADAMBRIDGE_EHIP on a HIP failure. */
