@@ -130,7 +130,8 @@ class HipKernels:
         return self._lib.adambridge_backend().decode()
 
     CONVERSION_CHECKS = ("stochastic E4M3", "stochastic E5M2", "nearest-even E4M3", "nearest-even E5M2",
-                         "nearest-even BF16", "square roots", "FP8 decode")
+                         "nearest-even BF16", "square roots", "FP8 decode",
+                         "divisions (sampled)")
 
     def check_conversions(self, seed: int = 0) -> dict[str, int]:
         """Differing results between the current device's conversion instructions and the

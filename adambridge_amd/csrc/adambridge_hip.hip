@@ -977,9 +977,10 @@ inline ConvertFn convert_kernel(int src, int dst, bool v)
 // 0 stochastic E4M3, 1 stochastic E5M2, 2 nearest-even E4M3, 3 nearest-even E5M2, 4 BF16,
 // 5 square roots (sqrtf on every finite x >= 0, sqrt_mid on its range) against the exact nearest
 // root, 6 FP8 decoding (every code of both formats at every byte position:
-// packed conversion, NaN detection, per-code conversion) against the formats' definitions.
+// packed conversion, NaN detection, per-code conversion) against the formats' definitions,
+// 7 divisions (one sampled pair per input: divisions_match) against the exact nearest quotient.
 // The random bits of input x are hash32(x ^ seed); every byte / half-word position is exercised.
-constexpr int kConvChecks = 7;
+constexpr int kConvChecks = 8;
 
 template <bool E5M2>
 __device__ __forceinline__ uint32_t sr_code_at(float x, uint32_t r, uint32_t pos)
@@ -1026,6 +1027,63 @@ __device__ bool is_nearest_root(uint32_t xb, uint32_t sb)
     return lo < L && L < hi;
 }
 
+// Whether q is the float nearest to a / b, for finite nonzero a, b and a normal q, in exact integer
+// arithmetic: 2|a - q b| < ulp(q) |b|, with the bound halved below a power of two (where the float
+// beneath q is half an ulp away).
+__device__ bool is_nearest_quotient(uint32_t ab, uint32_t bb, uint32_t qb)
+{
+    if ((qb >> 31) != ((ab ^ bb) >> 31)) return false;
+    uint64_t A, B, Q;
+    int ea, eb, eq;
+    float_parts(ab & 0x7fffffffu, A, ea);
+    float_parts(bb & 0x7fffffffu, B, eb);
+    float_parts(qb & 0x7fffffffu, Q, eq);
+    if (Q < 0x800000u) return false;   // callers keep quotients normal
+    typedef unsigned __int128 u128;
+    const int ep = eq + eb, e0 = ea < ep ? ea : ep;
+    if (ea - e0 > 60 || ep - e0 > 60) return false;
+    const u128 x1 = (u128)(4 * A) << (ea - e0), x2 = (u128)(4 * Q * B) << (ep - e0);
+    const bool below = x1 < x2;   // a / b below q
+    const u128 dist = below ? x2 - x1 : x1 - x2;
+    const u128 bound = (u128)((Q == 0x800000u && below) ? B : 2 * B) << (ep - e0);
+    return dist < bound;
+}
+
+// A float of random significand and sign with exponent in [emin, emax], from two hash draws.
+__device__ __forceinline__ float random_float(uint32_t h1, uint32_t h2, int emin, int emax, bool positive)
+{
+    const uint32_t e = (uint32_t)(emin + (int)(h2 % (uint32_t)(emax - emin + 1)) + 127);
+    return bitsf((positive ? 0u : (h2 & 0x80000000u)) | (e << 23) | (h1 & 0x7fffffu));
+}
+
+// The divisions the kernels rely on, one sampled pair each per call: the correctly rounded '/'
+// of the AdamW step (m / den), and the FP8 block quotients x / scale (block_scale, block_div,
+// block_quot_fast, both sign variants).
+__device__ bool divisions_match(uint32_t u, uint32_t seed)
+{
+    const uint32_t h1 = hash32(u ^ seed ^ 0x3c6ef372u), h2 = hash32(h1 ^ 0xa54ff53au);
+    const uint32_t h3 = hash32(h2 ^ 0x510e527fu), h4 = hash32(h3 ^ 0x9b05688cu);
+    // m / den: |m| in [2^-60, 2^60], den in [2^-40, 2^40]
+    const float m = random_float(h1, h2, -60, 60, false), den = random_float(h3, h4, -40, 40, true);
+    if (!is_nearest_quotient(fbits(m), fbits(den), fbits(m / den))) return false;
+    // block quotient: absmax in [2^-110, 2^60] (all three paths of block_div), |x| <= absmax
+    const float amax = random_float(h2, h3, -110, 60, true);
+    const bool e5m2 = h4 & 1u;
+    const float s = e5m2 ? block_scale<true>(amax) : block_scale<false>(amax);
+    const BlockDiv d = block_div(s, amax);
+    const float r = bitsf((h1 & 0x807fffffu) | (126u << 23));   // (-1, -0.5] or [0.5, 1)
+    const float x = amax * r;
+    if (!(x != 0.0f)) return true;
+    const bool nonneg = x > 0.0f && (h4 & 2u);
+    float q;
+    if (!d.fast) q = x / d.s;
+    else if (d.pre == 1.0f) q = nonneg ? block_quot_fast<false, true>(x, d) : block_quot_fast<false, false>(x, d);
+    else q = nonneg ? block_quot_fast<true, true>(x, d) : block_quot_fast<true, false>(x, d);
+    const float aq = fabsf(q);
+    if (!(aq >= 0x1p-126f)) return true;   // quotients below the normal range are not asserted here
+    return is_nearest_quotient(fbits(x), fbits(s), fbits(q));
+}
+
 // Code `code` of format E5M2 (else E4M3FN) placed in byte `pos` of a word with other bytes
 // zero: packed and per-code decoders against fp8_value_soft (NaN: a NaN of the code's sign from
 // the per-code decoder), and NaN detection.
@@ -1052,7 +1110,7 @@ __device__ __forceinline__ bool decode_matches(uint32_t code, uint32_t e5m2, uin
 
 __global__ __launch_bounds__(kThreads) void k_check_conversions(unsigned long long* counts, uint32_t seed)
 {
-    unsigned long long c[kConvChecks] = {0ull, 0ull, 0ull, 0ull, 0ull, 0ull, 0ull};
+    unsigned long long c[kConvChecks] = {0ull, 0ull, 0ull, 0ull, 0ull, 0ull, 0ull, 0ull};
     const uint64_t stride = (uint64_t)gridDim.x * kThreads;
     for (uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x; i < (1ull << 32); i += stride) {
         const uint32_t u = (uint32_t)i;
@@ -1078,6 +1136,7 @@ __global__ __launch_bounds__(kThreads) void k_check_conversions(unsigned long lo
             (!is_nearest_root(u, fbits(__builtin_sqrtf(x))) || (sqrt_mid_range(x) && !is_nearest_root(u, fbits(sqrt_mid(x))))))
             ++c[5];
         if (i < 2048u && !decode_matches(u & 0xffu, (u >> 8) & 1u, u >> 9)) ++c[6];
+        if (!divisions_match(u, seed)) ++c[7];
     }
 #pragma unroll
     for (int k = 0; k < kConvChecks; ++k)

@@ -207,13 +207,15 @@ ADAMBRIDGE_API int adambridge_convert(const void* src, const float* src_scale, i
  * those give the reference's codes (kernels.c:108-112, 857-876), and take square roots with a
  * short sequence where it equals sqrtf; this runs every FP32 bit pattern through them and through
  * integer forms of the reference's rules (sqrtf), in those ranges, with random bits
- * hash32(x ^ seed) for the stochastic ones.  Writes min(count, 7) counts of differing results:
+ * hash32(x ^ seed) for the stochastic ones.  Writes min(count, 8) counts of differing results:
  * [0] stochastic E4M3, [1] stochastic E5M2, [2] nearest-even E4M3, [3] nearest-even E5M2,
  * [4] BF16 nearest-even, [5] square roots -- sqrtf on every finite x >= 0, and the short form
  * (v_sqrt_f32 and a neighbour correction) on 2^-100 <= x < 2^100 -- against the nearest root
  * decided in exact integer arithmetic, [6] FP8 decoding of every code of
- * both formats against the formats' definitions -- all zero on a conforming device.
- * Returns the number of checks (7),
+ * both formats against the formats' definitions, [7] divisions -- 2^32 sampled pairs of the
+ * AdamW step's m / den and of the FP8 block quotients -- against the nearest quotient in exact
+ * integer arithmetic -- all zero on a conforming device.
+ * Returns the number of checks (8),
  * ADAMBRIDGE_ENULL for a NULL array or count < 1, ADAMBRIDGE_EHIP on a HIP failure. */
 ADAMBRIDGE_API int adambridge_check_conversions(uint32_t seed, uint64_t* mismatches, int32_t count);
 
