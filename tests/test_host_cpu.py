@@ -299,3 +299,45 @@ def test_segment_struct_mirrors_match_the_library():
     assert ctypes.sizeof(_hip.Segment) == lib.adambridge_segment_size() == ctypes.sizeof(O.Segment)
     assert ctypes.sizeof(_hip.HParams) == lib.adambridge_hparams_size() == ctypes.sizeof(O.HParams)
     assert ctypes.sizeof(_hip.Group) == lib.adambridge_group_size() == ctypes.sizeof(O.Group)
+
+
+# -------------------------------------- store behaviour (reference tests/test_precision.py,
+#                                         tests/test_hardening.py:80-89)
+
+def test_fp8_store_saved_under_the_other_role_is_converted():
+    """A checkpointed m store loaded as v is decoded in its own format and re-encoded as v
+    (E5M2, sqrt domain), not reinterpreted."""
+    n = 256
+    x = torch.rand(n, generator=torch.Generator().manual_seed(4)) * 1e-3
+    saved = P.make_store("fp8", n, "m", init=x)
+    loaded = P.store_from_state_dict(saved.state_dict(), n, "v")
+    assert loaded.role == "v" and loaded.dtype == torch.float8_e5m2
+    assert torch.equal(loaded.to_fp32(), P.make_store("fp8", n, "v", init=saved.to_fp32()).to_fp32())
+
+
+def test_fp8_stochastic_rounding_is_unbiased():
+    x = torch.full((200_000,), 1.03)
+    y = P.round_to_fp8_stochastic(x.clone(), torch.float8_e4m3fn, seed=0).float()
+    assert abs(y.mean().item() / 1.03 - 1.0) < 1e-3
+    # the two neighbouring codes of 1.03 (1.0 and 1.125) both occur
+    assert set(torch.unique(y).tolist()) == {1.0, 1.125}
+
+
+def test_fp8_store_keeps_small_second_moments():
+    """v is stored as sqrt(v): values 2^40 below the block's largest stay non-zero."""
+    v = torch.full((128,), 1e-12)
+    v[0] = 1.0
+    out = P.make_store("fp8", 128, "v", init=v).to_fp32()
+    assert abs(out[0].item() - 1.0) < 0.3
+    assert (out[1:] > 0).all()
+
+
+def test_fp24_store_initialises_exactly_from_bf16_and_in_chunks(monkeypatch):
+    n = 1000
+    x = torch.randn(n, generator=torch.Generator().manual_seed(5)) * 3
+    from_bf16 = P.make_master("fp24", n, init=x.to(torch.bfloat16).view(10, 100))
+    assert torch.equal(from_bf16.to_fp32(), x.to(torch.bfloat16).float()) and not from_bf16.lo.any()
+    whole = P.make_master("fp24", n, init=x)
+    monkeypatch.setattr(P.FP24Store, "INIT_CHUNK", 96)
+    chunked = P.make_master("fp24", n, init=x.view(20, 50))
+    assert torch.equal(chunked.to_fp32(), whole.to_fp32())
