@@ -6,7 +6,7 @@ of parameters per launch.  The public API mirrors the reference package
 ``adambridge`` (adambridge/__init__.py:4-25).
 """
 
-from . import precision
+from . import native, precision
 from .engine import StepStats
 from .losses import causal_lm_loss
 from .optimizer import AdamBridge, AutoTuneConfig, LionBridge, OptiComputeAdamW
@@ -22,6 +22,7 @@ __all__ = [
     "StepStats",
     "bytes_per_param",
     "causal_lm_loss",
+    "native",
     "precision",
     "__version__",
 ]

@@ -341,3 +341,36 @@ def test_fp24_store_initialises_exactly_from_bf16_and_in_chunks(monkeypatch):
     monkeypatch.setattr(P.FP24Store, "INIT_CHUNK", 96)
     chunked = P.make_master("fp24", n, init=x.view(20, 50))
     assert torch.equal(chunked.to_fp32(), whole.to_fp32())
+
+
+# ------------------------------------------ the native module (reference adambridge/native.py)
+
+def test_native_module_mirrors_the_reference_names():
+    from adambridge_amd import _hip, native
+    assert native.NativeKernels is _hip.HipKernels and native.Group is _hip.Group and native.Segment is _hip.Segment
+    assert native.library_path().exists() and native.library_path().parent == native.cache_dir()
+    k = native.load(build_if_missing=False)
+    assert k is not None and native.available() and native.load_error() is None
+    assert k.backend == "hip/gfx950"
+    assert issubclass(native.BuildError, RuntimeError)
+
+
+@pytest.mark.parametrize("step", [1, 2, 7, 100, 5000])
+def test_step_coefficients_equal_the_librarys_own(step):
+    """StepCoefficients -> multi_apply hparams (reference native.py:243-270, 381-387) carry the
+    bits multi_step derives from the group (kernels.c:793-809, restated by the oracle)."""
+    from adambridge_amd import _hip, native
+    lr, b1, b2, eps, wd = 3e-4, 0.9, 0.999, 1e-8, 0.01
+    case = O.make_case(np.random.default_rng(0), 16, explicit=False, lr=lr, betas=(b1, b2), eps=eps,
+                       weight_decay=wd, step=step)
+    want = O.hparams_for(case)
+    got = _hip.HipKernels.make_hparams(native.StepCoefficients.for_step(lr, b1, b2, eps, wd, step),
+                                      seed=want["seed"], stochastic=True)
+    for field, _ in _hip.HParams._fields_:
+        a, b = getattr(got, field), want[field]
+        if isinstance(a, float):
+            assert np.float32(a).view(np.uint32) == np.float32(b).view(np.uint32), (field, a, b)
+        else:
+            assert a == b, (field, a, b)
+    lion = native.StepCoefficients.for_lion(1e-4, 0.9, 0.99, 0.1)
+    assert (lion.step_size, lion.inv_sqrt_bc2, lion.eps) == (1e-4, 1.0, 0.0)
