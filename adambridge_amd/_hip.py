@@ -131,7 +131,7 @@ class HipKernels:
 
     CONVERSION_CHECKS = ("stochastic E4M3", "stochastic E5M2", "nearest-even E4M3", "nearest-even E5M2",
                          "nearest-even BF16", "square roots", "FP8 decode",
-                         "divisions (sampled)")
+                         "divisions (sampled)", "reciprocals")
 
     def check_conversions(self, seed: int = 0) -> dict[str, int]:
         """Differing results between the current device's conversion instructions and the

@@ -490,12 +490,26 @@ __device__ __forceinline__ void block_quotients(float (&x)[8], const BlockDiv& d
     }
 }
 
-// Max over the 16 lanes of a block group (values are >= 0 and never NaN).
+// One DPP move: lane i reads lane perm(i) of its own row of 16 (the whole row is active).
+template <int CTRL>
+__device__ __forceinline__ uint32_t row_dpp(uint32_t u)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, CTRL, 0xf, 0xf, false);
+}
+
+// Max over the 16 lanes of a block group, which form one DPP row of the wavefront (lanes
+// 16r .. 16r + 15).  The values are >= 0 and never NaN, so they order as their bits: four
+// unsigned maxima, each with another lane's value -- within pairs, within quads (quad_perm
+// [1,0,3,2] and [2,3,0,1]), then across half rows (row_half_mirror, lane i <-> 7 - i) and halves
+// (row_mirror, lane i <-> 15 - i).
 __device__ __forceinline__ float group16_max(float x)
 {
-#pragma unroll
-    for (int d = 1; d < 16; d <<= 1) x = fmaxf(x, __shfl_xor(x, d, 16));
-    return x;
+    uint32_t u = fbits(x);
+    u = __builtin_elementwise_max(u, row_dpp<0xb1>(u));
+    u = __builtin_elementwise_max(u, row_dpp<0x4e>(u));
+    u = __builtin_elementwise_max(u, row_dpp<0x141>(u));
+    u = __builtin_elementwise_max(u, row_dpp<0x140>(u));
+    return bitsf(u);
 }
 
 // A lane's 8 codes (two words, byte k & 3 of word k >> 2) through gfx950's conversion
@@ -506,9 +520,10 @@ __device__ __forceinline__ float group16_max(float x)
 template <bool E5M2, bool SR>
 __device__ __forceinline__ bool hw_codes8(const float (&x)[8], uint32_t idx, uint32_t seed, uint32_t (&q)[2])
 {
-    bool ok = true;
+    uint32_t worst = 0u;   // largest offset from the range's start (unsigned): no branches
 #pragma unroll
-    for (int k = 0; k < 8; ++k) ok &= fp8_hw_range<E5M2, SR>(x[k]);   // no short circuit: no branches
+    for (int k = 0; k < 8; ++k) worst = __builtin_elementwise_max(worst, fp8_hw_offset<E5M2, SR>(x[k]));
+    const bool ok = worst <= fp8_hw_span<E5M2, SR>;
     if constexpr (SR) {
         const uint32_t head = hash32_head(idx ^ seed);
         uint32_t r[8];
@@ -597,8 +612,9 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     // the update, FP32 moments in registers; sq = sqrt(new v), reused for the v code below
     float sq[8];
     const bool lane_fused = FULL || kLion || e0 + 8 <= n_main;
+    bool v_pos = false;   // every new v of the wavefront positive and finite (uniform)
     if constexpr (FULL && !kLion) {
-        adamw8_fused(p, g, mt, vt, c, sq);
+        v_pos = adamw8_fused(p, g, mt, vt, c, sq);
     } else {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
@@ -625,12 +641,24 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         if (!FULL && e0 + k >= n) { mt[k] = 0.0f; vt[k] = 0.0f; }
-        const float a = fabsf(mt[k]);
-        am = a > am ? a : am;
-        if constexpr (!kLion) {
-            const float u = vt[k] > 0.0f ? sq[k] : 0.0f;
-            vt[k] = u;
-            au = u > au ? u : au;
+        am = __builtin_fmaxf(am, fabsf(mt[k]));   // a NaN m is skipped (IEEE maxNum)
+    }
+    if constexpr (!kLion) {
+        if (v_pos) {   // u = sq; positive floats order as their bits
+            uint32_t ub = 0u;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                vt[k] = sq[k];
+                ub = __builtin_elementwise_max(ub, fbits(sq[k]));
+            }
+            au = bitsf(ub);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float u = vt[k] > 0.0f ? sq[k] : 0.0f;
+                vt[k] = u;
+                au = u > au ? u : au;
+            }
         }
     }
     am = group16_max(am);
@@ -978,9 +1006,10 @@ inline ConvertFn convert_kernel(int src, int dst, bool v)
 // 5 square roots (sqrtf on every finite x >= 0, sqrt_mid on its range) against the exact nearest
 // root, 6 FP8 decoding (every code of both formats at every byte position:
 // packed conversion, NaN detection, per-code conversion) against the formats' definitions,
-// 7 divisions (one sampled pair per input: divisions_match) against the exact nearest quotient.
+// 7 divisions (one sampled pair per input: divisions_match) against the exact nearest quotient,
+// 8 reciprocals (recip_nearest on every s of its range) against the exact nearest quotient 1 / s.
 // The random bits of input x are hash32(x ^ seed); every byte / half-word position is exercised.
-constexpr int kConvChecks = 8;
+constexpr int kConvChecks = 9;
 
 template <bool E5M2>
 __device__ __forceinline__ uint32_t sr_code_at(float x, uint32_t r, uint32_t pos)
@@ -1110,7 +1139,7 @@ __device__ __forceinline__ bool decode_matches(uint32_t code, uint32_t e5m2, uin
 
 __global__ __launch_bounds__(kThreads) void k_check_conversions(unsigned long long* counts, uint32_t seed)
 {
-    unsigned long long c[kConvChecks] = {0ull, 0ull, 0ull, 0ull, 0ull, 0ull, 0ull, 0ull};
+    unsigned long long c[kConvChecks] = {0ull, 0ull, 0ull, 0ull, 0ull, 0ull, 0ull, 0ull, 0ull};
     const uint64_t stride = (uint64_t)gridDim.x * kThreads;
     for (uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x; i < (1ull << 32); i += stride) {
         const uint32_t u = (uint32_t)i;
@@ -1137,6 +1166,7 @@ __global__ __launch_bounds__(kThreads) void k_check_conversions(unsigned long lo
             ++c[5];
         if (i < 2048u && !decode_matches(u & 0xffu, (u >> 8) & 1u, u >> 9)) ++c[6];
         if (!divisions_match(u, seed)) ++c[7];
+        if (recip_range(x) && !is_nearest_quotient(0x3f800000u, u, fbits(recip_nearest(x)))) ++c[8];
     }
 #pragma unroll
     for (int k = 0; k < kConvChecks; ++k)

@@ -202,20 +202,23 @@ ADAMBRIDGE_API const char* adambridge_backend(void);
 ADAMBRIDGE_API int adambridge_convert(const void* src, const float* src_scale, int32_t src_dtype, void* dst,
                                       float* dst_scale, int32_t dst_dtype, int64_t n, int32_t role);
 
-/* Self-check of the device's conversion and square-root instructions, on the current device
- * (synchronous).  The kernels round to FP8 and BF16 with gfx950's conversion instructions wherever
- * those give the reference's codes (kernels.c:108-112, 857-876), and take square roots with a
- * short sequence where it equals sqrtf; this runs every FP32 bit pattern through them and through
- * integer forms of the reference's rules (sqrtf), in those ranges, with random bits
- * hash32(x ^ seed) for the stochastic ones.  Writes min(count, 8) counts of differing results:
+/* Self-check of the device's conversion, square-root and reciprocal instructions, on the current
+ * device (synchronous).  The kernels round to FP8 and BF16 with gfx950's conversion instructions
+ * wherever those give the reference's codes (kernels.c:108-112, 857-876), and take square roots
+ * and FP8 block reciprocals with short sequences where they are correctly rounded; this runs every
+ * FP32 bit pattern through them and through integer forms of the reference's rules (sqrtf), in
+ * those ranges, with random bits hash32(x ^ seed) for the stochastic ones.  Writes min(count, 9)
+ * counts of differing results:
  * [0] stochastic E4M3, [1] stochastic E5M2, [2] nearest-even E4M3, [3] nearest-even E5M2,
  * [4] BF16 nearest-even, [5] square roots -- sqrtf on every finite x >= 0, and the short form
  * (v_sqrt_f32 and a neighbour correction) on 2^-100 <= x < 2^100 -- against the nearest root
  * decided in exact integer arithmetic, [6] FP8 decoding of every code of
  * both formats against the formats' definitions, [7] divisions -- 2^32 sampled pairs of the
  * AdamW step's m / den and of the FP8 block quotients -- against the nearest quotient in exact
- * integer arithmetic -- all zero on a conforming device.
- * Returns the number of checks (8),
+ * integer arithmetic, [8] reciprocals -- the short form (v_rcp_f32 and one Newton step) on every
+ * 2^-126 <= s < 2^126 -- against the nearest quotient 1 / s in exact integer arithmetic -- all
+ * zero on a conforming device.
+ * Returns the number of checks (9),
  * ADAMBRIDGE_ENULL for a NULL array or count < 1, ADAMBRIDGE_EHIP on a HIP failure. */
 ADAMBRIDGE_API int adambridge_check_conversions(uint32_t seed, uint64_t* mismatches, int32_t count);
 
