@@ -211,7 +211,7 @@ ADAMBRIDGE_API int adambridge_convert(const void* src, const float* src_scale, i
  * counts of differing results:
  * [0] stochastic E4M3, [1] stochastic E5M2, [2] nearest-even E4M3, [3] nearest-even E5M2,
  * [4] BF16 nearest-even, [5] square roots -- sqrtf on every finite x >= 0, and the short form
- * (v_sqrt_f32 and a neighbour correction) on 2^-100 <= x < 2^100 -- against the nearest root
+ * (v_sqrt_f32 and one Newton correction with v_rsq_f32) on 2^-100 <= x < 2^100 -- against the nearest root
  * decided in exact integer arithmetic, [6] FP8 decoding of every code of
  * both formats against the formats' definitions, [7] divisions -- 2^32 sampled pairs of the
  * AdamW step's m / den and of the FP8 block quotients -- against the nearest quotient in exact
