@@ -185,6 +185,25 @@ __device__ __forceinline__ void store8_u16(void* base, int64_t i, const uint32_t
 }
 
 // Master: FP32, or FP24 = hi plane (BF16 bits) << 16 | lo plane << 8.
+// FP8 records (p_dtype DT_PACKED8): the FP32 master and both FP8 moments of a 128-element block
+// in one 768-byte record, in the FP8 kernel's lane order.  Lane l of the block's 16 holds
+// elements 8l .. 8l + 7: their master at byte 16l (elements 8l .. 8l + 3) and 256 + 16l
+// (8l + 4 .. 8l + 7), their E4M3 m codes at 512 + 16l and E5M2 v codes at 520 + 16l.  Each of
+// the lane's three 16-byte accesses is one contiguous 256-byte span per block.
+constexpr int64_t kRecordBytes = 768;
+
+// Byte offset of element i's master value within the records.
+__device__ __forceinline__ int64_t record_master_offset(int64_t i)
+{
+    return (i >> 7) * kRecordBytes + ((i & 4) ? 256 : 0) + ((i >> 3) & 15) * 16 + (i & 3) * 4;
+}
+
+// Byte offset of the codes of elements i .. i + 7 (i % 8 == 0): m codes, then v codes 8 bytes on.
+__device__ __forceinline__ int64_t record_codes_offset(int64_t i)
+{
+    return (i >> 7) * kRecordBytes + 512 + ((i >> 3) & 15) * 16;
+}
+
 template <int PT>
 __device__ __forceinline__ void load_master8(const DevSeg& s, int64_t i, float (&x)[8])
 {
@@ -199,6 +218,11 @@ __device__ __forceinline__ void load_master8(const DevSeg& s, int64_t i, float (
             const uint32_t lo8 = (lu[k >> 2] >> (8 * (k & 3))) & 0xffu;
             x[k] = bitsf((hi16 << 16) | (lo8 << 8));
         }
+    } else if constexpr (PT == DT_PACKED8) {
+        const uint8_t* r = static_cast<const uint8_t*>(s.p) + record_master_offset(i);
+        const f32x4 a = ld(reinterpret_cast<const f32x4*>(r)), b = ld(reinterpret_cast<const f32x4*>(r + 256));
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
     } else {
         load8<DT_F32>(s.p, i, x);
     }
@@ -219,6 +243,10 @@ __device__ __forceinline__ void store_master8(const DevSeg& s, int64_t i, float 
         }
         store8_u16(s.p, i, hi);
         st(reinterpret_cast<u32x2*>(s.p_lo + i), u32x2{lo[0], lo[1]});
+    } else if constexpr (PT == DT_PACKED8) {
+        uint8_t* r = static_cast<uint8_t*>(s.p) + record_master_offset(i);
+        st(reinterpret_cast<f32x4*>(r), f32x4{x[0], x[1], x[2], x[3]});
+        st(reinterpret_cast<f32x4*>(r + 256), f32x4{x[4], x[5], x[6], x[7]});
     } else {
         store8_f32(s.p, i, x);
     }
@@ -341,6 +369,8 @@ __device__ __forceinline__ float load_master1(const DevSeg& s, int64_t i)
 {
     if constexpr (PT == DT_F24)
         return bitsf(((uint32_t)ld(static_cast<const uint16_t*>(s.p) + i) << 16) | ((uint32_t)ld(s.p_lo + i) << 8));
+    else if constexpr (PT == DT_PACKED8)
+        return ld(reinterpret_cast<const float*>(static_cast<const uint8_t*>(s.p) + record_master_offset(i)));
     else return ld(static_cast<const float*>(s.p) + i);
 }
 
@@ -352,6 +382,9 @@ __device__ __forceinline__ float store_master1(const DevSeg& s, int64_t i, float
         st(static_cast<uint16_t*>(s.p) + i, (uint16_t)(b >> 16));
         st(s.p_lo + i, (uint8_t)(b >> 8));
         return bitsf(b);
+    } else if constexpr (PT == DT_PACKED8) {
+        st(reinterpret_cast<float*>(static_cast<uint8_t*>(s.p) + record_master_offset(i)), x);
+        return x;
     } else {
         st(static_cast<float*>(s.p) + i, x);
         return x;
@@ -580,9 +613,15 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     const float sm = ld(s.m_scale + blk);
     const float sv = kLion ? 0.0f : ld(s.v_scale + blk);
     // codes are stored padded to whole blocks, so all 8 of this lane's exist
-    const u32x2 cm = vec ? ld(reinterpret_cast<const u32x2*>(mq + e0)) : load_codes8(mq + e0);
-    u32x2 cv = {0u, 0u};
-    if constexpr (!kLion) cv = vec ? ld(reinterpret_cast<const u32x2*>(vq + e0)) : load_codes8(vq + e0);
+    u32x2 cm, cv = {0u, 0u};
+    if constexpr (PT == DT_PACKED8) {   // AdamW only
+        const u32x4 c = ld(reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(s.p) + record_codes_offset(e0)));
+        cm = u32x2{c.x, c.y};
+        cv = u32x2{c.z, c.w};
+    } else {
+        cm = vec ? ld(reinterpret_cast<const u32x2*>(mq + e0)) : load_codes8(mq + e0);
+        if constexpr (!kLion) cv = vec ? ld(reinterpret_cast<const u32x2*>(vq + e0)) : load_codes8(vq + e0);
+    }
     float g[8], p[8], mt[8], vt[8];
     if (full) {
         load8<GT>(s.g, e0, g);
@@ -697,7 +736,10 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
             qv[k >> 2] |= (in ? b : 0u) << (8 * (k & 3));
         }
     }
-    if (vec) {
+    if constexpr (PT == DT_PACKED8) {
+        st(reinterpret_cast<u32x4*>(static_cast<uint8_t*>(s.p) + record_codes_offset(e0)),
+           u32x4{qm[0], qm[1], qv[0], qv[1]});
+    } else if (vec) {
         st(reinterpret_cast<u32x2*>(mq + e0), u32x2{qm[0], qm[1]});
         if constexpr (!kLion) st(reinterpret_cast<u32x2*>(vq + e0), u32x2{qv[0], qv[1]});
     } else {
@@ -875,24 +917,43 @@ constexpr auto make_packed_table(std::integer_sequence<int, I...>)
     return std::array<KernelFn, sizeof...(I)>{packed_entry<I>()...};
 }
 
+// FP8-record kernels (AdamW) follow: index kNumKernels + kNumPacked + gt * 3 + ot.
+template <int I>
+constexpr KernelFn packed8_entry()
+{
+    constexpr int ot = I % 3, gt = I / 3;
+    return &k_update_fp8<ALGO_ADAMW, DT_PACKED8, gt ? DT_BF16 : DT_F32, ot == 0 ? DT_NONE : ot == 1 ? DT_F32 : DT_BF16>;
+}
+
+template <int... I>
+constexpr auto make_packed8_table(std::integer_sequence<int, I...>)
+{
+    return std::array<KernelFn, sizeof...(I)>{packed8_entry<I>()...};
+}
+
 static const auto kKernels = make_table(std::make_integer_sequence<int, kNumKernels>{});
 static const auto kPacked = make_packed_table(std::make_integer_sequence<int, kNumPacked>{});
+static const auto kPacked8 = make_packed8_table(std::make_integer_sequence<int, kNumPacked>{});
 
 // Kernel family of a table index: the FP8 block kernel, or a two-element-per-lane kernel.
 inline bool kernel_is_fp8(int index)
 {
-    return index < kNumKernels && (index / 12) % 3 == 2;
+    return index < kNumKernels ? (index / 12) % 3 == 2 : index >= kNumKernels + kNumPacked;
 }
 
 inline KernelFn kernel_at(int index)
 {
-    return index < kNumKernels ? kKernels[index] : kPacked[index - kNumKernels];
+    if (index < kNumKernels) return kKernels[index];
+    if (index < kNumKernels + kNumPacked) return kPacked[index - kNumKernels];
+    return kPacked8[index - kNumKernels - kNumPacked];
 }
 
 inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
 {
     if (pt == DT_PACKED)
         return kNumKernels + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
+    if (pt == DT_PACKED8)
+        return kNumKernels + kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
     const int mvi = mv == DT_F32 ? 0 : mv == DT_BF16 ? 1 : 2;
     const int pti = pt == DT_F24 ? 1 : 0;
     const int gti = gt == DT_BF16 ? 1 : 0;

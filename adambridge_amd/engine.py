@@ -44,7 +44,8 @@ from dataclasses import dataclass, field
 import torch
 
 from . import _hip
-from .precision import (BF16Store, FP32Store, MomentStore, PackedMaster, PackedMoment, PackedState, make_master,
+from .precision import (FP8_BLOCK, BF16Store, FP8Store, FP32Store, MomentStore, PackedMaster, PackedMoment,
+                        PackedState, RecordMaster, RecordMoment, RecordState, make_master,
                         make_store)
 
 __all__ = ["UpdateEngine", "ParamSlot", "SmallGroup", "StepStats"]
@@ -78,7 +79,8 @@ class ParamSlot:
         self.done_ev: torch.cuda.Event | None = None   # the last update of this slot has run
         self.in_place = False                    # master is the FP32 parameter itself
         self.pending_grad = None                 # keeps a grad alive until its update is enqueued
-        self.packed: PackedState | None = None   # master + BF16 moments interleaved (m, v, master view it)
+        # master + BF16 moments interleaved, or master + FP8 codes in block records (m, v, master view it)
+        self.packed: PackedState | RecordState | None = None
 
     @property
     def initialized(self) -> bool:
@@ -194,9 +196,12 @@ class UpdateEngine:
                 slot.master = make_master(self.master_precision, slot.numel, init=src, device=dev)
             slot.in_place = in_place
             slot.packed = None
-            if self._packable(slot):
+            kind = self._packable(slot)
+            if kind == "bf16":
                 packed = PackedState(slot.numel, init=slot.master.data, device=dev, double_buffer=self.double_buffer)
                 self._adopt_packed(slot, packed)
+            elif kind == "fp8":
+                self._adopt_records(slot, RecordState(slot.numel, init=slot.master.data, device=dev))
             else:
                 slot.m = make_store(self.precision, slot.numel, "m", device=dev)
                 slot.v = None if self.lion else make_store(self.precision, slot.numel, "v", device=dev)
@@ -206,10 +211,12 @@ class UpdateEngine:
         slot.seg = None
         slot.seg_ptr = None
 
-    def _packable(self, slot: ParamSlot) -> bool:
-        """The interleaved layout serves AdamW with an FP32 master (a buffer of its own) and BF16 moments."""
-        return (self.state_layout != "separate" and not self.lion and self.precision == "bf16"
-                and self.master_precision == "fp32" and not slot.in_place)
+    def _packable(self, slot: ParamSlot) -> str | None:
+        """Which interleaved layout serves the slot: 'bf16' (pairs, BF16 moments) or 'fp8' (block
+        records, FP8 moments), for AdamW with an FP32 master of its own; None for the separate one."""
+        if self.state_layout == "separate" or self.lion or self.master_precision != "fp32" or slot.in_place:
+            return None
+        return self.precision if self.precision in ("bf16", "fp8") else None
 
     @staticmethod
     def _adopt_packed(slot: ParamSlot, packed: PackedState) -> None:
@@ -217,6 +224,15 @@ class UpdateEngine:
         slot.master = PackedMaster(packed)
         slot.m = PackedMoment(packed, "m")
         slot.v = PackedMoment(packed, "v")
+        slot.seg = None
+        slot.seg_ptr = None
+
+    @staticmethod
+    def _adopt_records(slot: ParamSlot, records: RecordState) -> None:
+        slot.packed = records
+        slot.master = RecordMaster(records)
+        slot.m = RecordMoment(records, "m")
+        slot.v = RecordMoment(records, "v")
         slot.seg = None
         slot.seg_ptr = None
 
@@ -242,7 +258,14 @@ class UpdateEngine:
         slot.seg_ptr = None
 
     def _pack(self, slot: ParamSlot) -> None:
-        """Move an FP32 master and BF16 moments (separate stores) into the interleaved layout."""
+        """Move an FP32 master and BF16 (FP8) moments, separate stores, into the interleaved layout
+        (block records)."""
+        if self._packable(slot) == "fp8":
+            m, v = slot.m, slot.v
+            self._adopt_records(slot, RecordState(slot.numel, init=slot.master.to_fp32(), device=slot.param.device))
+            slot.m.adopt(m)
+            slot.v.adopt(v)
+            return
         packed = PackedState(slot.numel, init=slot.master.to_fp32(), device=slot.param.device,
                              double_buffer=self.double_buffer)
         packed.set("m", slot.m.data)
@@ -250,10 +273,16 @@ class UpdateEngine:
         self._adopt_packed(slot, packed)
 
     def replace_moments(self, slot: ParamSlot, m: MomentStore, v: MomentStore | None) -> None:
-        if slot.packed is not None and isinstance(m, BF16Store) and isinstance(v, BF16Store):
+        if isinstance(slot.packed, PackedState) and isinstance(m, BF16Store) and isinstance(v, BF16Store):
             with torch.no_grad():
                 slot.packed.set("m", m.data)
                 slot.packed.set("v", v.data)
+            return
+        if (isinstance(slot.packed, RecordState) and isinstance(m, FP8Store) and isinstance(v, FP8Store)
+                and m.block == v.block == FP8_BLOCK):
+            with torch.no_grad():
+                slot.m.adopt(m)
+                slot.v.adopt(v)
             return
         if slot.packed is not None:   # another precision: the slot leaves the interleaved layout
             slot.master = FP32Store(slot.numel, init=slot.packed.get("p"), device=slot.param.device)
@@ -285,7 +314,13 @@ class UpdateEngine:
         """The slot's descriptor: its state buffers, size, index and formats (fixed until the state
         is replaced); the per-update fields are filled by :meth:`_segment`."""
         seg = _hip.Segment()
-        if slot.packed is not None:
+        if isinstance(slot.packed, RecordState):
+            seg.p_dtype = _hip.DT_PACKED8
+            seg.m = seg.v = seg.p_lo = None
+            seg.m_scale = slot.packed.scales["m"].data_ptr()
+            seg.v_scale = slot.packed.scales["v"].data_ptr()
+            seg.mv_dtype = _hip.DT_FP8
+        elif slot.packed is not None:
             seg.p_dtype = _hip.DT_PACKED
             seg.m = seg.v = seg.m_scale = seg.v_scale = seg.p_lo = None
             seg.mv_dtype = _hip.DT_BF16

@@ -30,7 +30,7 @@ import torch
 
 from . import _hip
 from .engine import ParamSlot, SmallGroup, StepStats, UpdateEngine
-from .precision import (FP32Store, PackedMaster, _checked, bytes_per_param, canonical_master_precision,
+from .precision import (FP32Store, PackedMaster, RecordMaster, _checked, bytes_per_param, canonical_master_precision,
                         canonical_precision, check_master_state, load_master_, make_store, store_from_state_dict)
 
 __all__ = ["AdamBridge", "LionBridge", "OptiComputeAdamW", "AutoTuneConfig"]
@@ -83,11 +83,13 @@ class AdamBridge(torch.optim.Optimizer):
     there is no second implementation to switch to.
 
     HIP-specific: ``state_layout`` -- 'auto' (default) keeps an FP32 master and BF16
-    moments interleaved, 16 bytes per pair of elements, which streams faster from HBM
-    than three separate arrays; 'separate' keeps the reference's layout; values,
-    rounding and checkpoints are identical either way.  ``double_buffer`` -- the
-    interleaved state alternates between two buffers (reads and writes go to different
-    memory), faster still at 8 more bytes per parameter.
+    moments interleaved, 16 bytes per pair of elements, and an FP32 master and FP8
+    moments in one 768-byte record per 128-element block (block scales apart), which
+    stream faster from HBM than separate arrays; 'separate' keeps the reference's layout;
+    values, rounding and checkpoints are identical either way.  ``double_buffer`` -- the
+    BF16 interleaved state alternates between two buffers (reads and writes go to
+    different memory), faster still at 8 more bytes per parameter (FP8 records are
+    updated in place).
     """
 
     _algorithm = "adamw"
@@ -399,8 +401,8 @@ class AdamBridge(torch.optim.Optimizer):
         for slot in self._ordered:
             if not slot.initialized:
                 continue
-            if isinstance(slot.master, (FP32Store, PackedMaster)):
-                master = slot.master.data   # a plain FP32 tensor (packed: a contiguous copy)
+            if isinstance(slot.master, (FP32Store, PackedMaster, RecordMaster)):
+                master = slot.master.data   # a plain FP32 tensor (interleaved layouts: a contiguous copy)
             else:
                 master = slot.master.state_dict()
             st = sd["state"][slot.index] = {"step": slot.step, "master": master, "exp_avg": slot.m.state_dict()}

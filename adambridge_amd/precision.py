@@ -36,7 +36,8 @@ __all__ = [
     "MomentStore", "FP32Store", "BF16Store", "FP8Store", "FP24Store", "make_store", "make_master",
     "store_from_state_dict", "check_master_state", "load_master_", "master_to_fp32", "bytes_per_param",
     "round_to_bf16_stochastic", "round_to_fp8_stochastic", "round_to_fp24_stochastic", "round_to_fp24_nearest_",
-    "moment_seed", "random_bits", "PackedState", "PackedMaster", "PackedMoment",
+    "moment_seed", "random_bits", "PackedState", "PackedMaster", "PackedMoment", "RecordState",
+    "RecordMaster", "RecordMoment",
 ]
 
 # Accepted spellings (precision.py:64-75), case-insensitive.
@@ -499,6 +500,162 @@ class PackedMoment(MomentStore):
 
     def state_dict(self):
         return {"precision": "bf16", "data": self.packed.get(self.role)}
+
+
+RECORD_BYTES = 768
+
+
+class RecordState:
+    """FP32 master and both FP8 moments of one parameter in one 768-byte record per 128-element
+    block (the kernel's ADAMBRIDGE_DT_PACKED_FP8 layout), plus the two block-scale arrays.  In the
+    record of block b, lane l's elements 128b + 8l + j (j < 8) hold their master at byte 16l + 4j
+    (j < 4) or 256 + 16l + 4(j - 4) (j >= 4), their E4M3 m code at 512 + 16l + j and their E5M2
+    code of sqrt(v) at 520 + 16l + j.  The kernel then reads and writes one contiguous stream of
+    state instead of three, which keeps its speed the same wherever the buffers land in HBM.
+
+    The values are exactly those of an FP32Store master and two FP8Store moments; ``get`` /
+    ``set`` convert the master, ``codes`` / ``set_codes`` the moments' codes."""
+
+    def __init__(self, numel: int, init: torch.Tensor | None = None, device=None):
+        self.numel = numel
+        self.device = torch.device(device) if device is not None else torch.device("cpu")
+        self.blocks = max(1, math.ceil(numel / FP8_BLOCK))
+        self.rec = torch.zeros(self.blocks, RECORD_BYTES, dtype=torch.uint8, device=self.device)
+        self.scales = {"m": torch.ones(self.blocks, dtype=torch.float32, device=self.device),
+                       "v": torch.ones(self.blocks, dtype=torch.float32, device=self.device)}
+        if init is not None:
+            self.set("p", init.detach().reshape(-1).to(self.device, torch.float32))
+
+    # the kernel's buffer, in the interface of PackedState (one buffer, updated in place)
+    @property
+    def current(self) -> torch.Tensor:
+        return self.rec
+
+    other = None
+
+    def flip(self) -> None:
+        pass
+
+    def _master(self) -> torch.Tensor:
+        """(blocks, 16, 2, 4) strided FP32 view: [b, l, h, j] is element 128b + 8l + 4h + j."""
+        return self.rec[:, :512].view(torch.float32).view(self.blocks, 2, 16, 4).permute(0, 2, 1, 3)
+
+    def _codes(self, role: str) -> torch.Tensor:
+        """(blocks, 16, 8) strided uint8 view of the role's codes, element order."""
+        lo = 0 if role == "m" else 8
+        return self.rec[:, 512:].view(self.blocks, 16, 16)[:, :, lo:lo + 8]
+
+    def get(self, role: str) -> torch.Tensor:
+        """Flat contiguous copy of the FP32 master (role 'p')."""
+        if role != "p":
+            raise ValueError("records hold the master as values and the moments as codes")
+        return self._master().reshape(-1)[: self.numel].clone()
+
+    def set(self, role: str, x: torch.Tensor) -> None:
+        if role != "p":
+            raise ValueError("records hold the master as values and the moments as codes")
+        flat = x.reshape(-1).to(self.device, torch.float32)
+        if flat.numel() != self.blocks * FP8_BLOCK:
+            flat = torch.nn.functional.pad(flat, (0, self.blocks * FP8_BLOCK - flat.numel()))
+        self._master().copy_(flat.view(self.blocks, 16, 2, 4))
+
+    def codes(self, role: str) -> torch.Tensor:
+        """The role's codes, padded to whole blocks, as a contiguous FP8 tensor (FP8Store.q)."""
+        return self._codes(role).reshape(-1).view(_FP8_FORMATS[role][0])
+
+    def set_codes(self, role: str, q: torch.Tensor) -> None:
+        self._codes(role).copy_(q.reshape(-1).view(torch.uint8).view(self.blocks, 16, 8))
+
+    @property
+    def nbytes(self) -> int:
+        return self.rec.nbytes + sum(t.nbytes for t in self.scales.values())
+
+
+class RecordMaster(MomentStore):
+    """The FP32 master held in a :class:`RecordState` (precision 'fp32')."""
+
+    precision = "fp32"
+
+    def __init__(self, records: RecordState):
+        super().__init__(records.numel, records.device)
+        self.packed = records
+
+    @property
+    def data(self) -> torch.Tensor:
+        return self.packed.get("p")
+
+    def write(self, lo, hi, x, seed=None):
+        if lo != 0 or hi != self.numel:
+            raise ValueError("a master in records is written whole")
+        self.packed.set("p", x)
+
+    def to_fp32(self):
+        return self.packed.get("p")
+
+    @property
+    def nbytes(self):
+        return 4 * self.numel   # the master values (the last record's unused slots count with m)
+
+    def state_dict(self):
+        return {"precision": "fp32", "data": self.packed.get("p")}
+
+
+class RecordMoment(MomentStore):
+    """An FP8 moment held in a :class:`RecordState` (precision 'fp8'): its codes in the records,
+    its block scales in the state's scale array for the role."""
+
+    precision = "fp8"
+    block = FP8_BLOCK
+
+    def __init__(self, records: RecordState, role: str):
+        super().__init__(records.numel, records.device)
+        self.packed = records
+        self.role = role
+
+    @property
+    def q(self) -> torch.Tensor:
+        return self.packed.codes(self.role)
+
+    @property
+    def scale(self) -> torch.Tensor:
+        return self.packed.scales[self.role]
+
+    def _store(self) -> "FP8Store":
+        """A separate FP8Store with this moment's codes and scales (a copy)."""
+        st = FP8Store(self.numel, self.role, device=self.device)
+        st.q.copy_(self.q)
+        st.scale.copy_(self.scale)
+        return st
+
+    def adopt(self, store: "FP8Store") -> None:
+        """Take the codes and scales of a separate FP8Store of the same size and role."""
+        if store.block != FP8_BLOCK or store.role != self.role or store.numel != self.numel:
+            raise ValueError("records take 128-element FP8 blocks of the same role and size")
+        self.packed.set_codes(self.role, store.q)
+        self.scale.copy_(store.scale)
+
+    def read(self, lo: int, hi: int) -> torch.Tensor:
+        return self._store().read(lo, hi)
+
+    def write(self, lo, hi, x, seed=None):
+        if lo != 0 or hi != self.numel:
+            raise ValueError("a moment in records is written whole")
+        st = FP8Store(self.numel, self.role, device=self.device)
+        st.write(0, self.numel, x, seed)
+        self.adopt(st)
+
+    def to_fp32(self):
+        return self._store().to_fp32()
+
+    @property
+    def nbytes(self):
+        # 128 code bytes per record and one scale, as a separate FP8Store; m also counts the master
+        # slots of the last record past the end, so that master + m + v is the whole RecordState
+        pad = self.packed.blocks * 512 - 4 * self.numel if self.role == "m" else 0
+        return self.packed.blocks * (FP8_BLOCK + 4) + pad
+
+    def state_dict(self):
+        return {"precision": "fp8", "role": self.role, "block": FP8_BLOCK, "q": self.q, "scale": self.scale}
 
 
 def make_store(precision: str, numel: int, role: str, init: torch.Tensor | None = None, device=None) -> MomentStore:

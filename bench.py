@@ -143,8 +143,9 @@ def gpu_bench(cfg: dict, steps: int, warmup: int, layout: str = "auto", double_b
     elems_per_launch = sum(e for _, _, e in log) / len(log)
     achieved = elems_per_launch * bpp / kernel_s / 1e9
     packed = sum(1 for s in opt._ordered if s.packed is not None)
-    state_layout = ("interleaved, double-buffered" if packed and double_buffer else "interleaved" if packed
-                    else "separate")
+    records = cfg["precision"] == "fp8" and packed
+    state_layout = ("FP8 block records" if records else "interleaved, double-buffered" if packed and double_buffer
+                    else "interleaved" if packed else "separate")
     stats = dict(params=n, tensors=len(params), wall=wall, launches_per_step=launches_per_step, layout=state_layout,
                  state_bytes=opt.memory_report()["total"],
                  kernel_ms=kernel_s * 1e3, kernel_ms_min=min(durs) * 1e3, kernel_ms_max=max(durs) * 1e3,

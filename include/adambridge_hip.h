@@ -38,7 +38,7 @@ extern "C" {
  * Algorithms, kernels.c:75: ALGO_ADAMW 0, ALGO_LION 1.
  * SIMD levels reproduced, kernels.c:74: 0 scalar, 1 AVX2 (8 lanes), 2 AVX-512 (16 lanes). */
 enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, ADAMBRIDGE_DT_FP8 = 3,
-       ADAMBRIDGE_DT_F24 = 4, ADAMBRIDGE_DT_PACKED = 5 };
+       ADAMBRIDGE_DT_F24 = 4, ADAMBRIDGE_DT_PACKED = 5, ADAMBRIDGE_DT_PACKED_FP8 = 6 };
 
 /* ADAMBRIDGE_DT_PACKED (p_dtype; no counterpart in the reference): an HBM layout for
  * AdamW with an FP32 master and BF16 moments (mv_dtype DT_BF16).  p points at 16-byte
@@ -47,6 +47,16 @@ enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, AD
  * aligned.  m and v are unused.  p_lo is NULL (update in place) or a second buffer of
  * the same layout that receives the new state (double buffering).  Same arithmetic,
  * rounding and rounding streams as the separate layout. */
+
+/* ADAMBRIDGE_DT_PACKED_FP8 (p_dtype; no counterpart in the reference): an HBM layout for
+ * AdamW with an FP32 master and FP8 moments (mv_dtype DT_FP8).  p points at one 768-byte
+ * record per 128-element block, ceil(n/128) records, 16-byte aligned.  In the record of
+ * block b, for l = 0 .. 15, elements 128b + 8l + j hold: master (FP32) at byte 16l + 4j
+ * for j < 4 and 256 + 16l + 4(j - 4) for j >= 4; m code (E4M3) at 512 + 16l + j; v code
+ * (E5M2, of sqrt v) at 520 + 16l + j.  Elements past n are padding (codes written as 0,
+ * master left as it is).  m_scale and v_scale are the usual block scales; m, v and p_lo are
+ * unused (p_lo must be NULL).  Same arithmetic, rounding and rounding streams as the
+ * separate FP8 layout. */
 enum { ADAMBRIDGE_ALGO_ADAMW = 0, ADAMBRIDGE_ALGO_LION = 1 };
 
 /* Error codes (kernels.c:1537-1553, 1582-1584, 1620-1621), plus the HIP-side ones. */
@@ -100,7 +110,7 @@ typedef struct adambridge_group {
  * itself is host memory; p .. out are device pointers. */
 typedef struct adambridge_segment {
     void* p;                 /* FP32 master, the FP24 hi plane (uint16) when p_dtype is DT_F24, or the
-                                packed state when p_dtype is DT_PACKED */
+                                packed state when p_dtype is DT_PACKED / DT_PACKED_FP8 */
     uint8_t* p_lo;           /* FP24 lo plane (one byte per element); NULL for FP32; DT_PACKED: the
                                 destination state (NULL: in place) */
     const void* g;           /* gradient, g_dtype */
@@ -118,7 +128,7 @@ typedef struct adambridge_segment {
     int32_t mv_dtype;
     int32_t out_dtype;
     int32_t algorithm;
-    int32_t p_dtype;         /* DT_F32 (or 0), DT_F24, or DT_PACKED */
+    int32_t p_dtype;         /* DT_F32 (or 0), DT_F24, DT_PACKED or DT_PACKED_FP8 */
     int32_t reserved;
 } adambridge_segment;
 

@@ -191,3 +191,89 @@ def run_hip_packed(cases: list[O.Case], width: int = 16, double_buffer: bool = F
         if out is not None:
             c.arrays["out"] = from_device(out, c.arrays["out"])
     return work
+
+
+def pack_records(case: O.Case) -> np.ndarray:
+    """Separate FP32 master + FP8 codes -> ADAMBRIDGE_DT_PACKED_FP8 records (blocks x 768 bytes):
+    per block, lane l's elements 8l .. 8l + 7 have their master at 16l (first four) and 256 + 16l
+    (last four), their m codes at 512 + 16l and v codes at 520 + 16l."""
+    n = case.n
+    nb = max(1, -(-n // 128))
+    p = np.zeros(nb * 128, np.uint32)
+    p[:n] = case.arrays["p"].view(np.uint32)
+    rec = np.zeros((nb, 768), np.uint8)
+    rec[:, :512] = p.reshape(nb, 16, 2, 4).transpose(0, 2, 1, 3).reshape(nb, 128).view(np.uint8)
+    codes = np.zeros((nb, 16, 16), np.uint8)
+    for key, lo in (("m", 0), ("v", 8)):
+        c = np.zeros(nb * 128, np.uint8)
+        src = case.arrays[key]
+        c[:min(src.size, nb * 128)] = src[:nb * 128]
+        codes[:, :, lo:lo + 8] = c.reshape(nb, 16, 8)
+    rec[:, 512:] = codes.reshape(nb, 256)
+    return rec
+
+
+def unpack_records(case: O.Case, rec: np.ndarray) -> None:
+    """ADAMBRIDGE_DT_PACKED_FP8 records -> the case's separate master and code arrays (in place)."""
+    n, nb = case.n, rec.shape[0]
+    p = np.ascontiguousarray(rec[:, :512]).view(np.uint32).reshape(nb, 2, 16, 4).transpose(0, 2, 1, 3).reshape(-1)
+    case.arrays["p"] = p[:n].view(np.float32).copy()
+    codes = np.ascontiguousarray(rec[:, 512:]).reshape(nb, 16, 16)
+    for key, lo in (("m", 0), ("v", 8)):
+        size = case.arrays[key].size
+        case.arrays[key] = codes[:, :, lo:lo + 8].reshape(-1)[:size].copy()
+
+
+def run_hip_records(cases: list[O.Case], width: int = 16, misalign_g: bool = False) -> list[O.Case]:
+    """Like run_hip for AdamW / FP32 master / FP8 moment cases, through the block-record layout
+    (ADAMBRIDGE_DT_PACKED_FP8): pack on the host, one call, unpack the result."""
+    kernels = _hip.load()
+    work = [c.copy() for c in cases]
+    keep, segs = [], []
+    by_group = all(c.group is not None for c in work)
+    for c in work:
+        assert c.algorithm == O.ADAMW and c.mv_dtype == O.DT_FP8 and c.p_dtype == O.DT_F32
+        O.check_sizes(c)
+        rec = torch.from_numpy(pack_records(c)).cuda()
+        g = to_device(c.arrays["g"])
+        if misalign_g:
+            buf = torch.empty(g.numel() + 1, dtype=g.dtype, device=g.device)
+            buf[1:].copy_(g)
+            keep.append(buf)
+            g = buf[1:]
+        ms, vs = to_device(c.arrays["m_scale"]), to_device(c.arrays["v_scale"])
+        out = to_device(c.arrays["out"]) if "out" in c.arrays else None
+        grp = None
+        if by_group:
+            grp = _hip.Group(**{k: c.group[k] for k in ("lr", "beta1", "beta2", "eps", "weight_decay")},
+                             seed=c.group["seed"] & (2**64 - 1), stochastic=int(c.group["stochastic"]))
+        keep += [rec, g, ms, vs, out, grp]
+        segs.append(_hip.Segment(p=rec.data_ptr(), p_lo=None, g=g.data_ptr(), m=None, v=None,
+                                 m_scale=ms.data_ptr(), v_scale=vs.data_ptr(),
+                                 out=out.data_ptr() if out is not None else None,
+                                 group=ctypes.pointer(grp) if grp is not None else None, n=c.n, step=c.step,
+                                 index=c.index, offset=c.offset, g_dtype=c.g_dtype, mv_dtype=O.DT_FP8,
+                                 out_dtype=c.out_dtype, algorithm=0, p_dtype=_hip.DT_PACKED8))
+    arr = kernels.segment_array([ctypes.pointer(s) for s in segs])
+    kernels.set_simd_level(WIDTH_LEVEL[width])
+    try:
+        kernels.set_stream(torch.cuda.current_stream())
+        if by_group:
+            kernels.multi_step(None, arr)
+        else:
+            hps = [_hip.HParams(**{k: c.hparams[k] for k, _ in _hip.HParams._fields_}) for c in work]
+            kernels.multi_apply(None, arr, hps)
+        torch.cuda.synchronize()
+    finally:
+        kernels.set_simd_level(None)
+    it = iter(keep)
+    for c in work:
+        if misalign_g:
+            next(it)
+        rec, g, ms, vs, out, grp = (next(it) for _ in range(6))
+        unpack_records(c, rec.cpu().numpy())
+        c.arrays["m_scale"] = from_device(ms, c.arrays["m_scale"])
+        c.arrays["v_scale"] = from_device(vs, c.arrays["v_scale"])
+        if out is not None:
+            c.arrays["out"] = from_device(out, c.arrays["out"])
+    return work

@@ -24,6 +24,7 @@ import numpy as np
 import pytest
 import torch
 
+from adambridge_amd.precision import RecordState
 from oracle import oracle as O
 
 ROOT = Path(__file__).resolve().parents[1]
@@ -47,7 +48,19 @@ def _u8(t: torch.Tensor) -> np.ndarray:
 def snapshot(opt, slot, lo: int, hi: int) -> dict:
     """The slot's state, gradient and master over elements [lo, hi) as the oracle's arrays."""
     a: dict[str, np.ndarray] = {}
-    if slot.packed is not None:   # interleaved FP32 master + BF16 moments, 16 bytes per pair
+    if isinstance(slot.packed, RecordState):   # FP32 master + FP8 codes in 768-byte block records
+        assert lo % 128 == 0
+        b0, b1 = lo // 128, math.ceil(hi / 128)
+        rec = slot.packed.rec[b0:b1].cpu().numpy()
+        nb = b1 - b0
+        p = np.ascontiguousarray(rec[:, :512]).view(np.uint32).reshape(nb, 2, 16, 4).transpose(0, 2, 1, 3)
+        a["p"] = p.reshape(-1)[: hi - lo].view(np.float32).copy()
+        codes = np.ascontiguousarray(rec[:, 512:]).reshape(nb, 16, 16)
+        a["m"] = codes[:, :, 0:8].reshape(-1).copy()
+        a["v"] = codes[:, :, 8:16].reshape(-1).copy()
+        a["m_scale"] = slot.packed.scales["m"][b0:b1].cpu().numpy().copy()
+        a["v_scale"] = slot.packed.scales["v"][b0:b1].cpu().numpy().copy()
+    elif slot.packed is not None:   # interleaved FP32 master + BF16 moments, 16 bytes per pair
         assert lo % 2 == 0
         rows = slot.packed.current[lo // 2: (hi + 1) // 2].cpu().numpy().view(np.uint32)
         p = np.empty(2 * rows.shape[0], np.uint32)

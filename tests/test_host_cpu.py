@@ -216,6 +216,44 @@ def test_store_from_state_dict_rejects_bad_stores():
                               "lo": torch.zeros(n, dtype=torch.int8)}, n, "master")
 
 
+@pytest.mark.parametrize("n", [1, 127, 128, 300, 4096 + 77])
+def test_fp8_records_layout_offsets_and_views(n):
+    """RecordState puts element 128b + 8l + j's master at byte 16l + 4j (j < 4) or 256 + 16l + 4(j - 4)
+    of record b, its m code at 512 + 16l + j and its v code at 520 + 16l + j (the kernel's
+    ADAMBRIDGE_DT_PACKED_FP8 layout); the master and moment views read back what was stored, and
+    the record-backed FP8 moment decodes like a separate FP8Store with the same codes and scales."""
+    rng = np.random.default_rng(n)
+    master = rng.normal(0, 0.02, n).astype(np.float32)
+    nb = -(-n // 128)
+    mq = rng.integers(0, 256, nb * 128, dtype=np.uint8)
+    vq = rng.integers(0, 0x7c, nb * 128, dtype=np.uint8)   # finite E5M2 codes
+    rs = P.RecordState(n, init=torch.from_numpy(master))
+    rs.set_codes("m", torch.from_numpy(mq).view(torch.float8_e4m3fn))
+    rs.set_codes("v", torch.from_numpy(vq).view(torch.float8_e5m2))
+    rec = rs.rec.numpy()
+    for e in list(range(min(n, 40))) + list(rng.integers(0, n, 40)):
+        b, l, j = e // 128, (e % 128) // 8, e % 8
+        off = 16 * l + 4 * j if j < 4 else 256 + 16 * l + 4 * (j - 4)
+        assert rec[b, off:off + 4].view(np.float32)[0] == master[e]
+        assert rec[b, 512 + 16 * l + j] == mq[e] and rec[b, 520 + 16 * l + j] == vq[e]
+    assert np.array_equal(rs.get("p").numpy(), master)
+    assert np.array_equal(rs.codes("m").view(torch.uint8).numpy(), mq)
+    assert np.array_equal(rs.codes("v").view(torch.uint8).numpy(), vq)
+    scale = torch.from_numpy(rng.uniform(1e-6, 1e-3, nb).astype(np.float32))
+    for role, q in (("m", mq), ("v", vq)):
+        mom = P.RecordMoment(rs, role)
+        mom.scale.copy_(scale)
+        sep = P.FP8Store(n, role)
+        sep.q.copy_(torch.from_numpy(q).view(sep.q.dtype))
+        sep.scale.copy_(scale)
+        assert torch.equal(mom.to_fp32().view(torch.int32), sep.to_fp32().view(torch.int32))   # NaN codes too
+        sd = mom.state_dict()
+        assert sd["precision"] == "fp8" and sd["role"] == role and torch.equal(sd["q"].view(torch.uint8), sep.q.view(torch.uint8))
+    assert P.RecordMaster(rs).nbytes == 4 * n and P.RecordMoment(rs, "v").nbytes == nb * (128 + 4)
+    assert P.RecordMaster(rs).nbytes + P.RecordMoment(rs, "m").nbytes + P.RecordMoment(rs, "v").nbytes == \
+        rs.nbytes == nb * (768 + 8)
+
+
 def test_fp24_master_store_round_trip():
     n = 1000
     x = torch.randn(n) * 3

@@ -226,6 +226,74 @@ def run_hip_packed_unchecked(case):
     k.multi_apply(None, k.segment_array([ctypes.pointer(seg)]), [hp])
 
 
+# ------------------------------------------------------ FP8 block-record layout
+
+from hip_cases import run_hip_records  # noqa: E402
+
+
+def test_fp8_records_match_oracle():
+    """ADAMBRIDGE_DT_PACKED_FP8 (master and both FP8 moments in 768-byte block records) gives the
+    separate layout's bytes: ragged and block-aligned sizes, tails of every reproduced ISA,
+    128-aligned offsets, SR on/off, every grad/out dtype."""
+    rng = np.random.default_rng(31)
+    cases = []
+    for gt, ot, sr, n in itertools.product([O.DT_BF16, O.DT_F32], [O.DT_NONE, O.DT_F32, O.DT_BF16], [True, False],
+                                           [1, 15, 127, 128, 129, 1000, 2048 + 77, 16384 + 300]):
+        cases.append(O.make_case(rng, n, mv_dtype=O.DT_FP8, p_dtype=O.DT_F32, g_dtype=gt, out_dtype=ot,
+                                 stochastic=sr, offset=128 * int(rng.integers(0, 2**24)),
+                                 index=int(rng.integers(0, 999)), step=int(rng.integers(1, 30))))
+    for width in (16, 8, 0):
+        want = O.run_many(cases, "oracle", width)
+        got = run_hip_records(cases, width)
+        for w, g in zip(want, got):
+            check(w, g)
+
+
+def test_fp8_records_misaligned_gradient_and_specials():
+    rng = np.random.default_rng(32)
+    cases = [O.make_case(rng, n, mv_dtype=O.DT_FP8, special=sp) for n in (999, 4096) for sp in (False, True)]
+    want = O.run_many(cases, "oracle", 16)
+    got = run_hip_records(cases, 16, misalign_g=True)
+    for w, g in zip(want, got):
+        bad = O.outputs_equal(w, g, nan_equiv=True)
+        assert not bad, bad
+
+
+def test_fp8_records_multi_step_groups_and_steps():
+    """Several segments per call through the group path, then three consecutive steps of one."""
+    rng = np.random.default_rng(33)
+    cases = [O.make_case(rng, 3000 + 128 * k + 7, mv_dtype=O.DT_FP8, explicit=False, index=k, step=k + 2, seed=3)
+             for k in range(12)]
+    want = O.run_many(cases, "oracle", 16)
+    got = run_hip_records(cases, 16)
+    for w, g in zip(want, got):
+        check(w, g)
+    case = O.make_case(rng, 5000, mv_dtype=O.DT_FP8)
+    grads = [O.make_case(rng, 5000, mv_dtype=O.DT_FP8).arrays["g"] for _ in range(3)]
+    check(run_steps(case, grads, oracle_runner, 16), run_steps(case, grads, run_hip_records, 16))
+
+
+def test_fp8_records_reject_bad_segments():
+    """Lion (-12), a second state buffer (-13), BF16 moments (-4) and a misaligned record (-14)."""
+    import ctypes
+    from adambridge_amd import _hip
+    rng = np.random.default_rng(34)
+    k = _hip.load()
+    case = O.make_case(rng, 300, mv_dtype=O.DT_FP8)
+    rec = torch.zeros(3 * 768 + 16, dtype=torch.uint8, device="cuda")
+    g = torch.zeros(300, dtype=torch.bfloat16, device="cuda")
+    sc = torch.ones(3, dtype=torch.float32, device="cuda")
+    hp = _hip.HParams(**{kk: case.hparams[kk] for kk, _ in _hip.HParams._fields_})
+    base = dict(p=rec.data_ptr(), g=g.data_ptr(), m_scale=sc.data_ptr(), v_scale=sc.data_ptr(), n=300, step=1,
+                mv_dtype=O.DT_FP8, g_dtype=O.DT_BF16, out_dtype=0, algorithm=0, p_dtype=_hip.DT_PACKED8)
+    for change, code in ((dict(algorithm=1), -12), (dict(p_lo=rec.data_ptr()), -13),
+                         (dict(mv_dtype=O.DT_BF16), -4), (dict(p=rec.data_ptr() + 8), -14)):
+        seg = _hip.Segment(**{**base, **change})
+        with pytest.raises(RuntimeError, match=rf"code {code}"):
+            k.multi_apply(None, k.segment_array([ctypes.pointer(seg)]), [hp])
+    assert torch.count_nonzero(rec).item() == 0   # nothing ran
+
+
 # ------------------------------------------------ fused_adamw, pools, streams
 
 @pytest.mark.parametrize("mv", [O.DT_F32, O.DT_BF16])

@@ -745,15 +745,17 @@ def test_multi_tensor_launch_count():
     opt.close()
 
 
+@pytest.mark.parametrize("precision", ["bf16", "fp8"])
 @pytest.mark.parametrize("hooks", [False, True])
-def test_state_layouts_give_identical_bytes(hooks):
-    """The interleaved layout (default), the separate layout and the double-buffered interleaved
-    layout produce the same weights, masters and moments, step after step."""
+def test_state_layouts_give_identical_bytes(hooks, precision):
+    """The interleaved layouts (default: BF16 pairs, FP8 block records), the separate layout and
+    the double-buffered interleaved layout produce the same weights, masters and moments (FP8:
+    codes and scales), step after step."""
     results = []
     for kw in (dict(state_layout="separate"), dict(), dict(double_buffer=True)):
         torch.manual_seed(0)
         model = TinyLM().to(DEV).to(torch.bfloat16)
-        opt = ab.AdamBridge(model.parameters(), lr=3e-3, precision="bf16", small_param_threshold=2000, **kw)
+        opt = ab.AdamBridge(model.parameters(), lr=3e-3, precision=precision, small_param_threshold=2000, **kw)
         if hooks:
             opt.attach_hooks(model)
         assert any(s.packed is not None for s in opt._ordered) or "state_layout" in kw or not opt._ordered[0].initialized
@@ -766,20 +768,25 @@ def test_state_layouts_give_identical_bytes(hooks):
                 opt.zero_grad()
         if "state_layout" not in kw:
             assert all(s.packed is not None for s in opt._ordered)
+        codes = ([s.m.q.view(torch.uint8) for s in opt._ordered] + [s.v.q.view(torch.uint8) for s in opt._ordered]
+                 + [s.m.scale.clone() for s in opt._ordered] + [s.v.scale.clone() for s in opt._ordered]
+                 if precision == "fp8" else [])
         results.append(([p.detach().clone() for p in model.parameters()], [m.clone() for m in opt.master_params()],
-                        [s.m.to_fp32() for s in opt._ordered], [s.v.to_fp32() for s in opt._ordered]))
+                        [s.m.to_fp32() for s in opt._ordered], [s.v.to_fp32() for s in opt._ordered], codes))
         opt.close()
     for other in results[1:]:
         for xs, ys in zip(results[0], other):
             assert all(torch.equal(x, y) for x, y in zip(xs, ys))
 
 
-def test_packed_state_checkpoint_and_set_precision():
-    """Checkpoints of the interleaved layout are the reference format and load into either layout;
-    set_precision leaves and re-enters the interleaved layout without changing values."""
+@pytest.mark.parametrize("precision", ["bf16", "fp8"])
+def test_packed_state_checkpoint_and_set_precision(precision):
+    """Checkpoints of the interleaved layouts are the reference format and load into either layout;
+    set_precision leaves and re-enters the interleaved layout: the values survive the exit exactly
+    and come back as the new precision's encoding of them."""
     torch.manual_seed(0)
     model = TinyLM().to(DEV).to(torch.bfloat16)
-    opt = ab.AdamBridge(model.parameters(), lr=3e-3, precision="bf16")
+    opt = ab.AdamBridge(model.parameters(), lr=3e-3, precision=precision)
     for step in range(3):
         lm_loss(model, step).backward()
         opt.step()
@@ -787,10 +794,16 @@ def test_packed_state_checkpoint_and_set_precision():
     sd = opt.state_dict()
     st = sd["state"][0]
     assert isinstance(st["master"], torch.Tensor) and st["master"].dtype == torch.float32
-    assert st["exp_avg"]["precision"] == "bf16" and st["exp_avg"]["data"].dtype == torch.bfloat16
+    if precision == "bf16":
+        assert st["exp_avg"]["precision"] == "bf16" and st["exp_avg"]["data"].dtype == torch.bfloat16
+    else:
+        assert st["exp_avg"]["precision"] == "fp8" and st["exp_avg"]["q"].dtype == torch.float8_e4m3fn
+        assert st["exp_avg_sq"]["q"].dtype == torch.float8_e5m2 and st["exp_avg_sq"]["scale"].dtype == torch.float32
+        n = opt._ordered[0].numel
+        assert st["exp_avg"]["q"].numel() == -(-n // 128) * 128 and st["exp_avg"]["scale"].numel() == -(-n // 128)
     masters = [m.clone() for m in opt.master_params()]
     for layout in ("separate", "auto"):
-        other = ab.AdamBridge(TinyLM().to(DEV).to(torch.bfloat16).parameters(), lr=3e-3, precision="bf16",
+        other = ab.AdamBridge(TinyLM().to(DEV).to(torch.bfloat16).parameters(), lr=3e-3, precision=precision,
                               state_layout=layout)
         other.load_state_dict(sd)
         for x, y in zip(masters, other.master_params()):
@@ -803,10 +816,11 @@ def test_packed_state_checkpoint_and_set_precision():
     assert all(s.packed is None for s in opt._ordered)
     for s, m in zip(opt._ordered, m_before):
         assert torch.equal(s.m.to_fp32(), m)
-    opt.set_precision("bf16")
+    opt.set_precision(precision)
     assert all(s.packed is not None for s in opt._ordered)
+    from adambridge_amd import precision as P
     for s, m in zip(opt._ordered, m_before):
-        assert torch.equal(s.m.to_fp32(), m)
+        assert torch.equal(s.m.to_fp32(), P.make_store(precision, s.numel, "m", init=m, device=DEV).to_fp32())
     for x, y in zip(masters, opt.master_params()):
         assert torch.equal(x, y)
     opt.close()
