@@ -106,16 +106,18 @@ def windows(numel: int) -> list[tuple[int, int]]:
 
 
 def run_config(name: str, warm: int = 2, tensors: int = 6, cfg: dict | None = None,
-               windows_of=None) -> None:
+               windows_of=None, layout: str = "auto") -> None:
     cfg = cfg or bench.CONFIGS[name]
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    opt, params = bench.build(cfg, dev)
+    opt, params = bench.build(cfg, dev, layout=layout)
     windows_of = windows_of or windows
     try:
         for _ in range(warm):
             opt.step()
         torch.cuda.synchronize()
+        if layout == "separate":
+            assert all(s.packed is None for s in opt._ordered)
         lion = cfg["algo"] == "lion"
         mv = {"fp32": O.DT_F32, "bf16": O.DT_BF16, "fp8": O.DT_FP8}[cfg["precision"]]
         # the largest tensors (first, middle, last windows) and the first window of every tensor
@@ -162,6 +164,13 @@ def run_config(name: str, warm: int = 2, tensors: int = 6, cfg: dict | None = No
 @pytest.mark.parametrize("name", ["c3p", "c3", "c4", "c2", "c1"])
 def test_full_size_config_sampled_parity(name):
     run_config(name)
+
+
+@pytest.mark.parametrize("name", ["c3p", "c3"])
+def test_full_size_separate_layout_sampled_parity(name):
+    """The reference's separate state arrays at the 7B list (the default keeps BF16 moments
+    interleaved and FP8 moments in block records)."""
+    run_config(name, layout="separate")
 
 
 # one tensor past 2^31 elements: 64-bit element indices, and the rounding stream's 32-bit element
