@@ -18,8 +18,10 @@
 // MI355X: a 1:1 read/write stream goes from 5.4 to 6.5 TB/s).
 //
 // FP8 moments are handled 128-element block by block: 16 lanes x 8 elements
-// per block, the two block maxima reduced with cross-lane shuffles, codes and
-// scales written by the same lanes (kernels.c:1034-1059).
+// per block (one DPP row), the two block maxima reduced by DPP row maxima, codes and
+// scales written by the same lanes (kernels.c:1034-1059).  In the block-record layout
+// (DT_PACKED8) a block's master and both code arrays are one 768-byte record, read
+// and written with three 16-byte accesses per lane.
 //
 // Segment descriptors travel in the kernel arguments when a call has at most
 // kInline segments (the per-parameter hook path: no copy at all), otherwise in
@@ -594,9 +596,9 @@ __device__ __forceinline__ float block_scale(float amax)
 }
 
 // One 128-element block, 16 lanes x 8 elements (this lane: e0 .. e0 + 7): decode both moments,
-// update, store master and output, block maxima by shuffles within the 16 lanes, scales, codes.
+// update, store master and output, block maxima by DPP within the 16 lanes, scales, codes.
 // FULL: the whole block lies inside the segment, takes the fused form and allows vector access --
-// straight-line code.  FULL is the same for the 16 lanes of a block, so the shuffles below always
+// straight-line code.  FULL is the same for the 16 lanes of a block, so the DPP maxima below always
 // run with the whole group active.
 template <int ALGO, int PT, int GT, int OT, bool SR, bool FULL>
 __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_t b0, int lane)
