@@ -612,8 +612,12 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     const int64_t e0 = b0 + lane * 8;
     const uint32_t idx = s.idx0 + (uint32_t)e0;
     const bool full = FULL || (vec && e0 + 8 <= n);
-    const float sm = ld(s.m_scale + blk);
-    const float sv = kLion ? 0.0f : ld(s.v_scale + blk);
+    // Block scales: ordinary (cached) accesses.  A wavefront reads and writes 16 bytes of each
+    // scale array, four blocks' worth; through L2 the four wavefronts of a workgroup share whole
+    // lines, where non-temporal accesses sent each 16-byte piece to HBM on its own (measured: the
+    // launch 3-4% slower, reads and writes 1.4% above the algorithmic bytes).
+    const float sm = *(const ABH_GLOBAL float*)(s.m_scale + blk);
+    const float sv = kLion ? 0.0f : *(const ABH_GLOBAL float*)(s.v_scale + blk);
     // codes are stored padded to whole blocks, so all 8 of this lane's exist
     u32x2 cm, cv = {0u, 0u};
     if constexpr (PT == DT_PACKED8) {   // AdamW only
@@ -749,8 +753,8 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
         if constexpr (!kLion) store_codes8(vq + e0, qv);
     }
     if (lane == 0) {
-        st(s.m_scale + blk, scm);
-        if constexpr (!kLion) st(s.v_scale + blk, scu);
+        *(ABH_GLOBAL float*)(s.m_scale + blk) = scm;
+        if constexpr (!kLion) *(ABH_GLOBAL float*)(s.v_scale + blk) = scu;
     }
 }
 
