@@ -732,6 +732,43 @@ def test_api_updates_are_bit_exact_against_the_oracle(precision, master, lion, h
     opt.close()
 
 
+@pytest.mark.parametrize("precision", ["bf16", "fp8"])
+def test_back_to_back_table_launches_reuse_staging_slots(precision):
+    """24 steps of 20 parameters with no host synchronisation between them: every launch carries
+    its descriptors in a device table (more than 7 segments), so the 16 staging slots are reused
+    while earlier launches may still be queued, and the uploads run on the queue's copy stream.
+    The final state equals the oracle's after the same 24 steps."""
+    torch.manual_seed(1)
+    shapes = [(97 + 13 * k, 31 + k) for k in range(20)]
+    params = [torch.nn.Parameter((torch.randn(s, device=DEV) * 0.02).to(torch.bfloat16)) for s in shapes]
+    init = [p.detach().clone() for p in params]
+    lr, wd, betas, seed = 2e-3, 0.01, (0.9, 0.999), 9
+    opt = ab.AdamBridge(params, lr=lr, betas=betas, weight_decay=wd, precision=precision, seed=seed,
+                        small_param_threshold=0)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    grads_seq = [[(torch.randn(s, device=DEV, generator=g) * 1e-2).to(torch.bfloat16) for s in shapes]
+                 for _ in range(24)]
+    log = []
+    opt._engine.launch_log = log
+    for grads in grads_seq:
+        for p, gr in zip(params, grads):
+            p.grad = gr
+        opt.step()
+    torch.cuda.synchronize()
+    assert len(log) == 24 and all(e == sum(p.numel() for p in params) for _, _, e in log)
+    want = _oracle_state_after(init, grads_seq, precision, "fp32", lr, wd, betas, seed)
+    for k, (p, c) in enumerate(zip(params, want)):
+        slot = opt._ordered[k]
+        assert slot.step == 24
+        got_p = p.detach().reshape(-1).cpu().view(torch.int16).numpy().view(np.uint16)
+        assert np.array_equal(got_p, c.arrays["out"]), f"param {k} weights"
+        assert np.array_equal(slot.master.data.cpu().numpy().view(np.uint32), c.arrays["p"].view(np.uint32))
+        m_data = (slot.m.q if hasattr(slot.m, "q") else slot.m.data).detach().cpu()
+        assert np.array_equal(m_data.view(torch.uint8).numpy().view(c.arrays["m"].dtype).reshape(-1),
+                              c.arrays["m"].reshape(-1)), f"param {k} m"
+    opt.close()
+
+
 def test_multi_tensor_launch_count():
     """step() updates every parameter in one kernel launch."""
     model = TinyLM().to(DEV).to(torch.bfloat16)
