@@ -398,7 +398,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
-              "the update shards by element ranges, see DESIGN.md", file=sys.stderr)
+              "sharded, each rank would update its 128-aligned element ranges of every state buffer "
+              "between a reduce-scatter of the gradients and an all-gather of the weights", file=sys.stderr)
         return 2
     if args.steps < 1 or args.warmup < 0 or args.rebuilds < 1:
         ap.error("--steps and --rebuilds must be >= 1 and --warmup >= 0")
