@@ -768,9 +768,19 @@ __device__ __forceinline__ void update_tile_fp8(const DevSeg& s, int64_t tile, i
     const bool vec = (s.flags & kVec) != 0;
     // blocks wholly in the fused range (AdamW's scalar tail, if any, is the segment's last n mod W)
     const int64_t full_end = kLion ? s.n : s.n_main;
+    // The smallest tile (the default) holds one 128-element block per 16-lane group: no loop and
+    // no loop-carried addresses (measured 1.3% faster on the 7B FP8 step in a fast HBM placement,
+    // equal in a slow one)
+    if (T == kFp8Quantum) {
+        const int64_t b0 = (tile - s.tile_begin) * kFp8Quantum + group * kFp8Block;
+        if (b0 >= s.n) return;
+        if (vec && b0 + kFp8Block <= full_end) fp8_block<ALGO, PT, GT, OT, SR, true>(s, c, b0, lane);
+        else fp8_block<ALGO, PT, GT, OT, SR, false>(s, c, b0, lane);
+        return;
+    }
     const int64_t lo = (tile - s.tile_begin) * T;
     const int64_t hi = lo + T < s.n ? lo + T : s.n;
-    // one 128-element block per 16-lane group
+    // larger tiles (ADAMBRIDGE_TILE_FP8): each 16-lane group walks every 16th block of the tile
     for (int64_t b0 = lo + group * kFp8Block; b0 < hi; b0 += (kThreads / 16) * kFp8Block) {
         if (vec && b0 + kFp8Block <= full_end) fp8_block<ALGO, PT, GT, OT, SR, true>(s, c, b0, lane);
         else fp8_block<ALGO, PT, GT, OT, SR, false>(s, c, b0, lane);

@@ -388,3 +388,45 @@ def test_pools_on_two_streams_from_two_threads():
     finally:
         for p in pools:
             k.destroy_pool(p)
+
+
+_LARGER_FP8_TILE = r"""
+import itertools, sys
+import numpy as np
+sys.path[:0] = sys.argv[1:3]
+from oracle import oracle as O
+from hip_cases import run_hip, run_hip_records
+rng = np.random.default_rng(41)
+cases = [O.make_case(rng, n, algorithm=algo, mv_dtype=O.DT_FP8, p_dtype=pt, stochastic=sr,
+                     offset=128 * int(rng.integers(0, 2**20)), index=int(rng.integers(0, 999)), step=3)
+         for algo, pt, sr, n in itertools.product([O.ADAMW, O.LION], [O.DT_F32, O.DT_F24], [True, False],
+                                                  [129, 4096 + 77, 3 * 4096, 20000 + 5])]
+records = [c for c in cases if c.algorithm == O.ADAMW and c.p_dtype == O.DT_F32]
+bad = 0
+for runner, subset in ((run_hip, cases), (run_hip_records, records)):
+    for w, g in zip(O.run_many(subset, "oracle", 16), runner(subset, 16)):
+        diff = O.outputs_equal(w, g)
+        if diff:
+            print("differ:", w.n, w.algorithm, w.p_dtype, diff, flush=True)
+            bad += 1
+print("cases", len(cases) + len(records), "bad", bad, flush=True)
+sys.exit(1 if bad else 0)
+"""
+
+
+def test_fp8_larger_tile_matches_oracle():
+    """The FP8 kernel's loop over several blocks per 16-lane group, taken only when
+    ADAMBRIDGE_TILE_FP8 asks for a tile above 2048 elements (read once per process, hence a child
+    process): separate and block-record layouts, AdamW and Lion, FP32 and FP24 masters."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    env = dict(os.environ, ADAMBRIDGE_TILE_FP8="4096")
+    print("child process: ADAMBRIDGE_TILE_FP8=4096", flush=True)
+    run = subprocess.run([sys.executable, "-c", _LARGER_FP8_TILE, str(root), str(root / "tests")], env=env,
+                         capture_output=True, text=True, timeout=110)
+    print(run.stdout, flush=True)
+    assert run.returncode == 0, run.stdout + run.stderr[-3000:]
