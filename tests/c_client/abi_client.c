@@ -12,9 +12,11 @@
  *                                  switch, argument checks (nothing reaches a device)
  *   abi_client gpu ORACLE.so       three segments (AdamW BF16 moments; AdamW FP8 moments
  *                                  with an FP24 master at a non-zero offset; Lion), three
- *                                  steps, each compared byte for byte with the same update
- *                                  computed by the CPU oracle (oracle/liboracle.so, the
- *                                  checker: abo_multi_step over host copies)
+ *                                  multi_step steps, one multi_apply with explicit
+ *                                  coefficients, then one fused_adamw on the first tensor;
+ *                                  after each, every buffer compared byte for byte with the
+ *                                  same update computed by the CPU oracle (oracle/liboracle.so,
+ *                                  the checker: abo_multi_step / abo_multi_apply on host copies)
  *
  * Exit status 0 when every check passes; the failing check is printed.
  */
@@ -109,6 +111,8 @@ static int run_abi(void)
 /* ---------------------------------------------------------------- with GPU */
 
 typedef int (*oracle_multi_step_fn)(adambridge_segment* const*, int32_t, int64_t, int32_t);
+typedef int (*oracle_multi_apply_fn)(adambridge_segment* const*, const adambridge_hparams*, int32_t, int64_t,
+                                     int32_t);
 
 static uint64_t rng_state = 0x243F6A8885A308D3ull;
 
@@ -210,8 +214,10 @@ static int run_gpu(const char* oracle_path)
     void* lib = dlopen(oracle_path, RTLD_NOW | RTLD_LOCAL);
     if (!lib) { fprintf(stderr, "dlopen %s: %s\n", oracle_path, dlerror()); return 2; }
     oracle_multi_step_fn oracle_step = (oracle_multi_step_fn)(uintptr_t)dlsym(lib, "abo_multi_step");
+    oracle_multi_apply_fn oracle_apply = (oracle_multi_apply_fn)(uintptr_t)dlsym(lib, "abo_multi_apply");
     int (*oracle_segment_size)(void) = (int (*)(void))(uintptr_t)dlsym(lib, "abo_segment_size");
-    if (!oracle_step || !oracle_segment_size || oracle_segment_size() != (int)sizeof(adambridge_segment)) {
+    if (!oracle_step || !oracle_apply || !oracle_segment_size ||
+        oracle_segment_size() != (int)sizeof(adambridge_segment)) {
         fprintf(stderr, "oracle library does not match the segment layout\n");
         return 2;
     }
@@ -323,6 +329,49 @@ static int run_gpu(const char* oracle_path)
         bad.offset = 100;   /* FP8 chunks start at multiples of 128 */
         adambridge_segment* mixed[2] = {&segs[0].dev, &bad};
         CHECK(adambridge_multi_step(pool, mixed, 2, 0) == ADAMBRIDGE_EOFFSET, "FP8 offset 100 accepted");
+    }
+    /* multi_apply: explicit coefficients per segment (kernels.c:1630-1641), as the reference's
+     * benches and tests call it */
+    {
+        adambridge_hparams hps[3];
+        for (int k = 0; k < 3; ++k) {
+            const adambridge_hparams h = {0.85f, 0.98f, 0.15f, 0.02f, 0.999f, 2e-3f * (float)(k + 1), 1.25f, 1e-7f,
+                                          0x9e3779b9u * (uint32_t)(k + 11), k != 1};
+            hps[k] = h;
+        }
+        fill_gradient(&segs[0], 0.0f);
+        fill_gradient(&segs[1], 0.0f);
+        fill_gradient(&segs[2], 0.0f);
+        for (int k = 0; k < 3; ++k) {
+            if (upload(segs[k].g)) { fprintf(stderr, "gradient upload failed\n"); return 2; }
+        }
+        int rc = adambridge_multi_apply(pool, dev, hps, 3, 0);
+        CHECK(rc == 0, "multi_apply returned %d (%s)", rc, adambridge_last_error());
+        CHECK(adambridge_pool_sync(pool) == 0, "pool_sync after multi_apply");
+        CHECK(oracle_apply(host, hps, 3, width, 1) == 0, "oracle multi_apply");
+        int same = 1;
+        for (int b = 0; b < nbufs; ++b) same &= compare(&bufs[b], 4);
+        printf("multi_apply: %d buffers %s\n", nbufs, same ? "identical to the oracle" : "DIFFER");
+        fflush(stdout);
+    }
+    /* fused_adamw: one FP32-master tensor with BF16 moments, synchronous (kernels.c:1518-1535);
+     * segment 0's buffers at element offset 4099 of a parameter, nearest rounding */
+    {
+        const adambridge_hparams h = {0.9f, 0.995f, 0.1f, 0.005f, 0.9995f, 1e-3f, 1.5f, 1e-8f, 77u, 0};
+        fill_gradient(&segs[0], 0.0f);
+        if (upload(segs[0].g)) { fprintf(stderr, "gradient upload failed\n"); return 2; }
+        const adambridge_segment* d = &segs[0].dev;
+        const int rc = adambridge_fused_adamw((float*)d->p, d->g, d->g_dtype, d->m, d->v, d->mv_dtype, d->out,
+                                              d->out_dtype, d->n, 4099, &h);
+        CHECK(rc == 0, "fused_adamw returned %d (%s)", rc, adambridge_last_error());
+        adambridge_segment o = segs[0].host;
+        o.offset = 4099; o.index = 0; o.step = 0; o.group = NULL;
+        adambridge_segment* one[1] = {&o};
+        CHECK(oracle_apply(one, &h, 1, width, 1) == 0, "oracle fused update");
+        int same = 1;
+        for (int b = 0; b < nbufs; ++b) same &= compare(&bufs[b], 5);
+        printf("fused_adamw: %d buffers %s\n", nbufs, same ? "identical to the oracle" : "DIFFER");
+        fflush(stdout);
     }
     CHECK(adambridge_pool_sync(pool) == 0, "final pool_sync");
     adambridge_pool_destroy(pool);

@@ -8,9 +8,10 @@ GPU: the program built by build() (tests/c_client/Makefile) allocates device buf
 hipMalloc, creates a pool bound to its own HIP stream, and calls adambridge_multi_step for three
 steps over three segments at once: AdamW with BF16 moments and a scalar tail; AdamW with FP8
 moments, an FP24 master and stochastic rounding at element offset 384; Lion with zero
-gradients.  After every step every buffer must equal, byte for byte, the same update computed
-by the CPU oracle (oracle/liboracle.so) on host copies, and a call with one invalid segment
-must change nothing.
+gradients.  Then one adambridge_multi_apply with explicit coefficients, and one
+adambridge_fused_adamw on the first tensor at an element offset.  After every call every buffer
+must equal, byte for byte, the same update computed by the CPU oracle (oracle/liboracle.so) on
+host copies, and a call with one invalid segment must change nothing.
 """
 
 import subprocess
@@ -37,11 +38,11 @@ def test_c_client_compiles_and_checks_arguments(tmp_path):
 
 
 @pytest.mark.gpu
-def test_c_client_multi_step_matches_oracle():
+def test_c_client_updates_match_oracle():
     assert CLIENT.exists(), "tests/c_client/abi_client is not built: run __graft_entry__.build()"
     assert ORACLE.exists(), "oracle/liboracle.so is not built: run __graft_entry__.build()"
     print(f"running {CLIENT} gpu {ORACLE}", flush=True)
     run = subprocess.run([str(CLIENT), "gpu", str(ORACLE)], capture_output=True, text=True, timeout=120)
     print(run.stdout, flush=True)
     assert run.returncode == 0, run.stdout + run.stderr
-    assert run.stdout.count("identical to the oracle") == 3
+    assert run.stdout.count("identical to the oracle") == 5   # 3 x multi_step, multi_apply, fused_adamw
