@@ -20,12 +20,13 @@ from pathlib import Path
 import torch
 
 __all__ = ["HipKernels", "HParams", "Group", "Segment", "load", "LIB_PATH", "DT_NONE", "DT_F32", "DT_BF16",
-           "DT_FP8", "DT_F24", "DT_PACKED", "DT_PACKED8", "MOMENT_CODES", "MASTER_CODES", "ALGORITHMS", "SIMD_NAMES"]
+           "DT_FP8", "DT_F24", "DT_PACKED", "DT_PACKED8", "DT_PACKED_LION", "MOMENT_CODES", "MASTER_CODES",
+           "ALGORITHMS", "SIMD_NAMES"]
 
 LIB_PATH = Path(__file__).resolve().with_name("libadambridge_hip.so")
 ABI_VERSION = 5
 
-DT_NONE, DT_F32, DT_BF16, DT_FP8, DT_F24, DT_PACKED, DT_PACKED8 = 0, 1, 2, 3, 4, 5, 6
+DT_NONE, DT_F32, DT_BF16, DT_FP8, DT_F24, DT_PACKED, DT_PACKED8, DT_PACKED_LION = 0, 1, 2, 3, 4, 5, 6, 7
 _DTYPE_CODES = {torch.float32: DT_F32, torch.bfloat16: DT_BF16}
 MOMENT_CODES = {"fp32": DT_F32, "bf16": DT_BF16, "fp8": DT_FP8}
 MASTER_CODES = {"fp32": DT_F32, "fp24": DT_F24}
@@ -69,7 +70,7 @@ EXPORTS = (
     "adambridge_fused_adamw", "adambridge_pool_create", "adambridge_pool_destroy", "adambridge_pool_threads",
     "adambridge_pool_set_spin", "adambridge_multi_step", "adambridge_multi_apply", "adambridge_pool_set_stream",
     "adambridge_pool_sync", "adambridge_set_stream", "adambridge_last_error", "adambridge_backend",
-    "adambridge_check_conversions", "adambridge_convert",
+    "adambridge_check_conversions", "adambridge_convert", "adambridge_plan_launches",
 )
 
 
@@ -103,6 +104,7 @@ def open_library(path: Path = LIB_PATH) -> ctypes.CDLL:
         "adambridge_backend": (ctypes.c_char_p, []),
         "adambridge_check_conversions": (ctypes.c_int, [ctypes.c_uint32, ctypes.POINTER(u64), i32]),
         "adambridge_convert": (ctypes.c_int, [vp, vp, i32, vp, vp, i32, i64, i32]),
+        "adambridge_plan_launches": (ctypes.c_int, [_SegArray, i32, ctypes.POINTER(i64), i32]),
     }
     for name in EXPORTS:
         fn = getattr(lib, name)
@@ -210,6 +212,19 @@ class HipKernels:
         self._check(self._lib.adambridge_multi_apply(pool, segments, hps, len(segments), threads),
                     "adambridge_multi_apply")
 
+    def plan_launches(self, segments: ctypes.Array) -> list[tuple[int, int, int, int]]:
+        """(launch, kernel variant, first tile, launch tiles) of every entry of the launches a
+        multi_apply / multi_step call over ``segments`` would make (adambridge_plan_launches); no
+        device work."""
+        count = self._lib.adambridge_plan_launches(segments, len(segments), None, 0)
+        if count < 0:
+            self._check(count, "adambridge_plan_launches")
+        rows = (ctypes.c_int64 * (4 * max(count, 1)))()
+        got = self._lib.adambridge_plan_launches(segments, len(segments), rows, count)
+        if got != count:
+            raise RuntimeError(f"adambridge_plan_launches returned {got}, then {count}")
+        return [tuple(rows[4 * k: 4 * k + 4]) for k in range(count)]
+
     _CONVERT_DTYPES = {torch.float32: DT_F32, torch.bfloat16: DT_BF16, torch.float8_e4m3fn: DT_FP8,
                        torch.float8_e5m2: DT_FP8, torch.uint8: DT_FP8}
 
@@ -286,7 +301,7 @@ class HipKernels:
 
     def _check(self, rc: int, what: str) -> None:
         if rc != 0:
-            detail = self.last_error() if rc == -20 else ""
+            detail = self.last_error() if rc in (-20, -22) else ""   # codes that set the error text
             raise RuntimeError(f"{what} rejected the update (code {rc}){': ' + detail if detail else ''}")
 
 

@@ -886,6 +886,70 @@ __global__ __launch_bounds__(kThreads) void k_update_packed(Launch L)
     else update_tile_packed<GT, OT, false>(s, tile, L.tile);
 }
 
+// ------------------------------------------------------ Lion record state kernel
+//
+// Lion with an FP32 master and a BF16 moment in one 768-byte record per 128
+// elements: elements 2l and 2l + 1 of a record (l < 64) keep their two masters
+// at byte 8l and their two m values (BF16 bits, the first in the low half) at
+// 512 + 4l.  A wavefront's 64 lanes take one record per pass, so each of its
+// two state accesses covers one contiguous span (512 and 256 bytes) in place of
+// the separate layout's four master and moment streams.  Lion fuses every
+// element (kernels.c:1093-1106), so there is no scalar tail; a record's slots
+// past n are padding and are written back unchanged.
+
+constexpr int64_t kLionRecordBytes = 768;
+
+template <int GT, int OT, bool SR>
+__device__ __forceinline__ void update_tile_lion_rec(const DevSeg& s, int64_t tile, int64_t T)
+{
+    const int64_t n = s.n;
+    const Coef c = s.c;
+    const uint8_t* __restrict__ src = static_cast<const uint8_t*>(s.p);
+    uint8_t* __restrict__ dst = s.p_lo;
+    const bool vec = (s.flags & kVec) != 0;   // g and out allow 2-element access
+    const int64_t lo = (tile - s.tile_begin) * T;
+    const int64_t hi = lo + T < n ? lo + T : n;
+    for (int64_t i = lo + threadIdx.x * 2; i < hi; i += kThreads * 2) {
+        // i is even: record i / 128, pair (i % 128) / 2 -> master at 4 (i % 128), m at 512 + 2 (i % 128)
+        const int64_t at = (i >> 7) * kLionRecordBytes + (i & 127) * 4;
+        const int64_t at_m = (i >> 7) * kLionRecordBytes + 512 + (i & 127) * 2;
+        const uint32_t idx = s.idx0 + (uint32_t)i;
+        const u32x2 pw = ld(reinterpret_cast<const u32x2*>(src + at));
+        const uint32_t mw = ld(reinterpret_cast<const uint32_t*>(src + at_m));
+        const bool both = i + 2 <= n;
+        float g0 = 0.0f, g1 = 0.0f;
+        if (vec && both) load2<GT>(s.g, i, g0, g1);
+        else {
+            g0 = load1<GT>(s.g, i);
+            if (both) g1 = load1<GT>(s.g, i + 1);
+        }
+        float m0 = bitsf(mw << 16), m1 = bitsf(mw & 0xffff0000u);
+        const float p0 = lion(bitsf(pw.x), g0, m0, c);
+        const float p1 = lion(bitsf(pw.y), g1, m1, c);
+        const uint32_t h0 = bf16_store<SR>(m0, SR ? hash32(idx ^ s.seed_m) : 0u);
+        uint32_t w_p1 = fbits(p1), w_m = h0 | (mw & 0xffff0000u);
+        if (both) w_m = h0 | (bf16_store<SR>(m1, SR ? hash32((idx + 1) ^ s.seed_m) : 0u) << 16);
+        else w_p1 = pw.y;   // padding keeps its bits
+        st(reinterpret_cast<u32x2*>(dst + at), u32x2{fbits(p0), w_p1});
+        st(reinterpret_cast<uint32_t*>(dst + at_m), w_m);
+        if (vec && both) store_out2<OT>(s.out, i, p0, p1);
+        else {
+            store_out1<OT>(s.out, i, p0);
+            if (both) store_out1<OT>(s.out, i + 1, p1);
+        }
+    }
+}
+
+template <int GT, int OT>
+__global__ __launch_bounds__(kThreads) void k_update_lion_rec(Launch L)
+{
+    const int64_t tile = block_tile(L);
+    if (tile >= L.ntiles) return;
+    const DevSeg s = find_segment(L, tile);
+    if (s.flags & kSR) update_tile_lion_rec<GT, OT, true>(s, tile, L.tile);
+    else update_tile_lion_rec<GT, OT, false>(s, tile, L.tile);
+}
+
 // ------------------------------------------------------------ kernel table
 
 using KernelFn = void (*)(Launch);
@@ -947,21 +1011,38 @@ constexpr auto make_packed8_table(std::integer_sequence<int, I...>)
     return std::array<KernelFn, sizeof...(I)>{packed8_entry<I>()...};
 }
 
+// Lion-record kernels follow: index kNumKernels + 2 * kNumPacked + gt * 3 + ot.
+template <int I>
+constexpr KernelFn lion_rec_entry()
+{
+    constexpr int ot = I % 3, gt = I / 3;
+    return &k_update_lion_rec<gt ? DT_BF16 : DT_F32, ot == 0 ? DT_NONE : ot == 1 ? DT_F32 : DT_BF16>;
+}
+
+template <int... I>
+constexpr auto make_lion_rec_table(std::integer_sequence<int, I...>)
+{
+    return std::array<KernelFn, sizeof...(I)>{lion_rec_entry<I>()...};
+}
+
 static const auto kKernels = make_table(std::make_integer_sequence<int, kNumKernels>{});
 static const auto kPacked = make_packed_table(std::make_integer_sequence<int, kNumPacked>{});
 static const auto kPacked8 = make_packed8_table(std::make_integer_sequence<int, kNumPacked>{});
+static const auto kLionRec = make_lion_rec_table(std::make_integer_sequence<int, kNumPacked>{});
 
 // Kernel family of a table index: the FP8 block kernel, or a two-element-per-lane kernel.
 inline bool kernel_is_fp8(int index)
 {
-    return index < kNumKernels ? (index / 12) % 3 == 2 : index >= kNumKernels + kNumPacked;
+    if (index < kNumKernels) return (index / 12) % 3 == 2;
+    return index >= kNumKernels + kNumPacked && index < kNumKernels + 2 * kNumPacked;
 }
 
 inline KernelFn kernel_at(int index)
 {
     if (index < kNumKernels) return kKernels[index];
     if (index < kNumKernels + kNumPacked) return kPacked[index - kNumKernels];
-    return kPacked8[index - kNumKernels - kNumPacked];
+    if (index < kNumKernels + 2 * kNumPacked) return kPacked8[index - kNumKernels - kNumPacked];
+    return kLionRec[index - kNumKernels - 2 * kNumPacked];
 }
 
 inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
@@ -970,6 +1051,8 @@ inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
         return kNumKernels + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
     if (pt == DT_PACKED8)
         return kNumKernels + kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
+    if (pt == DT_PACKED_LION)
+        return kNumKernels + 2 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
     const int mvi = mv == DT_F32 ? 0 : mv == DT_BF16 ? 1 : 2;
     const int pti = pt == DT_F24 ? 1 : 0;
     const int gti = gt == DT_BF16 ? 1 : 0;

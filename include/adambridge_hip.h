@@ -38,7 +38,8 @@ extern "C" {
  * Algorithms, kernels.c:75: ALGO_ADAMW 0, ALGO_LION 1.
  * SIMD levels reproduced, kernels.c:74: 0 scalar, 1 AVX2 (8 lanes), 2 AVX-512 (16 lanes). */
 enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, ADAMBRIDGE_DT_FP8 = 3,
-       ADAMBRIDGE_DT_F24 = 4, ADAMBRIDGE_DT_PACKED = 5, ADAMBRIDGE_DT_PACKED_FP8 = 6 };
+       ADAMBRIDGE_DT_F24 = 4, ADAMBRIDGE_DT_PACKED = 5, ADAMBRIDGE_DT_PACKED_FP8 = 6,
+       ADAMBRIDGE_DT_PACKED_LION = 7 };
 
 /* ADAMBRIDGE_DT_PACKED (p_dtype; no counterpart in the reference): an HBM layout for
  * AdamW with an FP32 master and BF16 moments (mv_dtype DT_BF16).  p points at 16-byte
@@ -57,6 +58,15 @@ enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, AD
  * master left as it is).  m_scale and v_scale are the usual block scales; m, v and p_lo are
  * unused (p_lo must be NULL).  Same arithmetic, rounding and rounding streams as the
  * separate FP8 layout. */
+
+/* ADAMBRIDGE_DT_PACKED_LION (p_dtype; no counterpart in the reference): an HBM layout for
+ * Lion with an FP32 master and a BF16 moment (mv_dtype DT_BF16).  p points at one 768-byte
+ * record per 128 elements, ceil(n/128) records, 16-byte aligned.  In the record of elements
+ * 128r .. 128r + 127, for l = 0 .. 63, elements 128r + 2l and 128r + 2l + 1 keep their FP32
+ * masters at bytes 8l and 8l + 4 and their m values (BF16 bits) at 512 + 4l and 512 + 4l + 2.
+ * Slots past n are padding, written back unchanged.  p_lo is NULL (update in place) or a
+ * second buffer of the same layout that receives the new state; m, v and the scales are
+ * unused.  Same arithmetic, rounding and rounding stream as the separate layout. */
 enum { ADAMBRIDGE_ALGO_ADAMW = 0, ADAMBRIDGE_ALGO_LION = 1 };
 
 /* Error codes (kernels.c:1537-1553, 1582-1584, 1620-1621), plus the HIP-side ones. */
@@ -77,7 +87,9 @@ enum {
     ADAMBRIDGE_EPDTYPE = -13,
     ADAMBRIDGE_EALIGN = -14,       /* a packed state buffer is not 16-byte aligned */
     ADAMBRIDGE_EHIP = -20,         /* a HIP runtime call failed; see adambridge_last_error() */
-    ADAMBRIDGE_EDEVICE = -21       /* the pool belongs to another device than the current one */
+    ADAMBRIDGE_EDEVICE = -21,      /* the pool belongs to another device than the current one */
+    ADAMBRIDGE_ECAPTURE = -22      /* a pooled call whose launch needs a staged segment table (more than
+                                      7 segments of one kernel variant) on a stream under graph capture */
 };
 
 /* Per-segment step coefficients: kernels.c:77-88 (40 bytes). */
@@ -110,9 +122,9 @@ typedef struct adambridge_group {
  * itself is host memory; p .. out are device pointers. */
 typedef struct adambridge_segment {
     void* p;                 /* FP32 master, the FP24 hi plane (uint16) when p_dtype is DT_F24, or the
-                                packed state when p_dtype is DT_PACKED / DT_PACKED_FP8 */
-    uint8_t* p_lo;           /* FP24 lo plane (one byte per element); NULL for FP32; DT_PACKED: the
-                                destination state (NULL: in place) */
+                                packed state when p_dtype is DT_PACKED / DT_PACKED_FP8 / DT_PACKED_LION */
+    uint8_t* p_lo;           /* FP24 lo plane (one byte per element); NULL for FP32; DT_PACKED and
+                                DT_PACKED_LION: the destination state (NULL: in place) */
     const void* g;           /* gradient, g_dtype */
     void* m;                 /* first moment, mv_dtype (FP8: E4M3 codes, padded to 128 per block) */
     void* v;                 /* second moment (FP8: E5M2 codes of sqrt(v)); unused by Lion */
@@ -128,7 +140,7 @@ typedef struct adambridge_segment {
     int32_t mv_dtype;
     int32_t out_dtype;
     int32_t algorithm;
-    int32_t p_dtype;         /* DT_F32 (or 0), DT_F24, DT_PACKED or DT_PACKED_FP8 */
+    int32_t p_dtype;         /* DT_F32 (or 0), DT_F24, DT_PACKED, DT_PACKED_FP8 or DT_PACKED_LION */
     int32_t reserved;
 } adambridge_segment;
 
@@ -162,7 +174,8 @@ ADAMBRIDGE_API int adambridge_fused_adamw(float* p, const void* g, int g_dtype, 
 /* kernels.c:1427-1487.  A launch queue on the current HIP device, initially on
  * the null stream.  nthreads, cpus and ncpus are accepted and ignored (the
  * device schedules its own compute units).  NULL on failure.  pool_threads
- * returns the device's compute-unit count; pool_set_spin is a no-op. */
+ * returns the device's compute-unit count (1 for a NULL pool, as the
+ * reference's); pool_set_spin is a no-op. */
 ADAMBRIDGE_API void* adambridge_pool_create(int32_t nthreads, const int32_t* cpus, int32_t ncpus);
 ADAMBRIDGE_API void adambridge_pool_destroy(void* pool);
 ADAMBRIDGE_API int32_t adambridge_pool_threads(void* pool);
@@ -172,7 +185,13 @@ ADAMBRIDGE_API void adambridge_pool_set_spin(void* pool, int32_t spin);
  * step, computed on the host in double as the reference does.  Validates every
  * segment before enqueueing anything (first bad segment's code).  pool NULL:
  * the current device's default queue on the calling thread's stream.
- * threads is ignored.  Asynchronous: ordered on the pool's stream. */
+ * threads is ignored.  Asynchronous: ordered on the pool's stream.  Launches
+ * are planned in full first (one per kernel variant, split where a variant has
+ * more segments than a staging slot holds or more tiles than one dispatch
+ * takes), so no size limit is met after something was enqueued.  A launch of
+ * more than 7 segments stages its segment table through a reused pinned host
+ * slot: on a stream under graph capture such a call returns ADAMBRIDGE_ECAPTURE
+ * before enqueueing anything. */
 ADAMBRIDGE_API int adambridge_multi_step(void* pool, adambridge_segment* const* segs, int32_t nsegs,
                                          int32_t threads);
 
@@ -198,6 +217,17 @@ ADAMBRIDGE_API const char* adambridge_last_error(void);
 
 /* Name of the device code this library carries, e.g. "hip/gfx950". */
 ADAMBRIDGE_API const char* adambridge_backend(void);
+
+/* The launches a multi_apply / multi_step call over these segments would make, without
+ * launching anything or touching the device (a diagnostic for bindings and tests).  Segments are
+ * validated as multi_apply validates them.  For each entry of each launch, in launch order, writes
+ * four values to rows[4k .. 4k + 3] while k < cap: the launch's number, its kernel variant, the
+ * entry's first tile (negative where a segment continues from the previous launch) and the
+ * launch's tile count.  A segment appears once, or once per launch its tiles are spread over when
+ * they exceed one dispatch (2^32 - 1 work-items).  Returns the number of entries (which may
+ * exceed cap), or a negative code. */
+ADAMBRIDGE_API int adambridge_plan_launches(adambridge_segment* const* segs, int32_t nsegs, int64_t* rows,
+                                            int32_t cap);
 
 /* Re-encodes n values of one moment (role 0: m, FP8 as E4M3FN; role 1: v, FP8 as E5M2 of
  * sqrt(v)) or of an FP32 master (role 0) from src_dtype to dst_dtype (ADAMBRIDGE_DT_F32, _BF16 or

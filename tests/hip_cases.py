@@ -41,41 +41,59 @@ def hip_segment(case: O.Case, tensors: dict, group: _hip.Group | None) -> _hip.S
                         out_dtype=case.out_dtype, algorithm=case.algorithm, p_dtype=case.p_dtype)
 
 
+class Prepared:
+    """Device copies of cases, their segments and coefficients, ready for one library call."""
+
+    def __init__(self, cases: list[O.Case], tensors_hook=None):
+        self.work = [c.copy() for c in cases]
+        for c in self.work:
+            O.check_sizes(c)   # every buffer covers what the launch will touch, before anything runs
+        self.dev = [{k: to_device(a) for k, a in c.arrays.items()} for c in self.work]
+        if tensors_hook is not None:
+            for i, t in enumerate(self.dev):
+                tensors_hook(i, t)
+        self.by_group = all(c.group is not None for c in self.work)
+        self.groups = [_hip.Group(**{k: c.group[k] for k in ("lr", "beta1", "beta2", "eps", "weight_decay")},
+                                  seed=c.group["seed"] & (2**64 - 1), stochastic=int(c.group["stochastic"]))
+                       if self.by_group else None for c in self.work]
+        self.segs = [hip_segment(c, t, g) for c, t, g in zip(self.work, self.dev, self.groups)]
+        self.arr = _hip.load().segment_array([ctypes.pointer(s) for s in self.segs])
+        self.hps = None if self.by_group else [
+            _hip.HParams(**{k: c.hparams[k] for k, _ in _hip.HParams._fields_}) for c in self.work]
+
+    def call(self, pool: int | None = None) -> None:
+        """multi_step (cases with groups) or multi_apply, on the current stream."""
+        kernels = _hip.load()
+        kernels.set_stream(torch.cuda.current_stream())
+        if self.by_group:
+            kernels.multi_step(pool, self.arr)
+        else:
+            kernels.multi_apply(pool, self.arr, self.hps)
+
+    def collect(self) -> list[O.Case]:
+        """The device state copied back into the cases (after a synchronisation)."""
+        out = [c.copy() for c in self.work]
+        for c, t in zip(out, self.dev):
+            for k in list(c.arrays):
+                if k in t:
+                    c.arrays[k] = from_device(t[k], c.arrays[k])
+        return out
+
+
 def run_hip(cases: list[O.Case], width: int = 16, pool: int | None = None,
             tensors_hook=None) -> list[O.Case]:
     """Update copies of ``cases`` in one call of the HIP library; returns them.
 
     ``tensors_hook(i, tensors)`` may replace device tensors before the call (misalignment tests)."""
+    prep = Prepared(cases, tensors_hook)
     kernels = _hip.load()
-    work = [c.copy() for c in cases]
-    for c in work:
-        O.check_sizes(c)   # every buffer covers what the launch will touch, before anything runs
-    dev = [{k: to_device(a) for k, a in c.arrays.items()} for c in work]
-    if tensors_hook is not None:
-        for i, t in enumerate(dev):
-            tensors_hook(i, t)
-    by_group = all(c.group is not None for c in work)
-    groups = [_hip.Group(**{k: c.group[k] for k in ("lr", "beta1", "beta2", "eps", "weight_decay")},
-                         seed=c.group["seed"] & (2**64 - 1), stochastic=int(c.group["stochastic"]))
-              if by_group else None for c in work]
-    segs = [hip_segment(c, t, g) for c, t, g in zip(work, dev, groups)]
-    arr = kernels.segment_array([ctypes.pointer(s) for s in segs])
     kernels.set_simd_level(WIDTH_LEVEL[width])
     try:
-        kernels.set_stream(torch.cuda.current_stream())
-        if by_group:
-            kernels.multi_step(pool, arr)
-        else:
-            hps = [_hip.HParams(**{k: c.hparams[k] for k, _ in _hip.HParams._fields_}) for c in work]
-            kernels.multi_apply(pool, arr, hps)
+        prep.call(pool)
         torch.cuda.synchronize()
     finally:
         kernels.set_simd_level(None)
-    for c, t in zip(work, dev):
-        for k in list(c.arrays):
-            if k in t:
-                c.arrays[k] = from_device(t[k], c.arrays[k])
-    return work
+    return prep.collect()
 
 
 def golden_cases():
@@ -274,6 +292,87 @@ def run_hip_records(cases: list[O.Case], width: int = 16, misalign_g: bool = Fal
         unpack_records(c, rec.cpu().numpy())
         c.arrays["m_scale"] = from_device(ms, c.arrays["m_scale"])
         c.arrays["v_scale"] = from_device(vs, c.arrays["v_scale"])
+        if out is not None:
+            c.arrays["out"] = from_device(out, c.arrays["out"])
+    return work
+
+
+def pack_lion_records(case: O.Case) -> np.ndarray:
+    """Separate FP32 master + BF16 m -> ADAMBRIDGE_DT_PACKED_LION records (records x 768 bytes):
+    per 128 elements, elements 2l and 2l + 1 keep their masters at byte 8l and their m bits at
+    512 + 4l (first element in the low half).  Padding slots are set to a fixed pattern so that
+    a test can see the kernel leave them unchanged."""
+    n = case.n
+    nr = max(1, -(-n // 128))
+    p = np.full(nr * 128, 0x7FA5A5A5, np.uint32)   # a NaN pattern: any arithmetic on it would show
+    p[:n] = case.arrays["p"].view(np.uint32)
+    m = np.full(nr * 128, 0xA5A5, np.uint16)
+    m[:n] = case.arrays["m"]
+    rec = np.zeros((nr, 768), np.uint8)
+    rec[:, :512] = p.reshape(nr, 128).view(np.uint8)
+    rec[:, 512:] = m.reshape(nr, 128).view(np.uint8)
+    return rec
+
+
+def unpack_lion_records(case: O.Case, rec: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """ADAMBRIDGE_DT_PACKED_LION records -> the case's separate master and m (in place); returns
+    the padding slots' (master bits, m bits) past n."""
+    n = case.n
+    p = np.ascontiguousarray(rec[:, :512]).view(np.uint32).reshape(-1)
+    m = np.ascontiguousarray(rec[:, 512:]).view(np.uint16).reshape(-1)
+    case.arrays["p"] = p[:n].view(np.float32).copy()
+    case.arrays["m"] = m[:n].copy()
+    return p[n:].copy(), m[n:].copy()
+
+
+def run_hip_lion_records(cases: list[O.Case], width: int = 16, double_buffer: bool = False,
+                         misalign_g: bool = False, padding: list | None = None) -> list[O.Case]:
+    """Like run_hip for Lion / FP32 master / BF16 moment cases, through the record layout
+    (ADAMBRIDGE_DT_PACKED_LION): pack on the host, one call, unpack the result.  ``padding``
+    receives each case's padding slots after the call."""
+    kernels = _hip.load()
+    work = [c.copy() for c in cases]
+    keep, segs = [], []
+    by_group = all(c.group is not None for c in work)
+    for c in work:
+        assert c.algorithm == O.LION and c.mv_dtype == O.DT_BF16 and c.p_dtype == O.DT_F32
+        O.check_sizes(c)
+        rec = torch.from_numpy(pack_lion_records(c)).cuda()
+        dst = torch.full_like(rec, 0x5A) if double_buffer else None
+        g = to_device(c.arrays["g"])
+        if misalign_g:
+            buf = torch.empty(g.numel() + 1, dtype=g.dtype, device=g.device)
+            buf[1:].copy_(g)
+            keep.append(buf)
+            g = buf[1:]
+        out = to_device(c.arrays["out"]) if "out" in c.arrays else None
+        grp = None
+        if by_group:
+            grp = _hip.Group(**{k: c.group[k] for k in ("lr", "beta1", "beta2", "eps", "weight_decay")},
+                             seed=c.group["seed"] & (2**64 - 1), stochastic=int(c.group["stochastic"]))
+        keep.append((rec, dst, g, out, grp))
+        segs.append(_hip.Segment(p=rec.data_ptr(), p_lo=dst.data_ptr() if dst is not None else None,
+                                 g=g.data_ptr(), m=None, v=None, out=out.data_ptr() if out is not None else None,
+                                 group=ctypes.pointer(grp) if grp is not None else None, n=c.n, step=c.step,
+                                 index=c.index, offset=c.offset, g_dtype=c.g_dtype, mv_dtype=O.DT_BF16,
+                                 out_dtype=c.out_dtype, algorithm=O.LION, p_dtype=_hip.DT_PACKED_LION))
+    arr = kernels.segment_array([ctypes.pointer(s) for s in segs])
+    kernels.set_simd_level(WIDTH_LEVEL[width])
+    try:
+        kernels.set_stream(torch.cuda.current_stream())
+        if by_group:
+            kernels.multi_step(None, arr)
+        else:
+            hps = [_hip.HParams(**{k: c.hparams[k] for k, _ in _hip.HParams._fields_}) for c in work]
+            kernels.multi_apply(None, arr, hps)
+        torch.cuda.synchronize()
+    finally:
+        kernels.set_simd_level(None)
+    entries = [e for e in keep if isinstance(e, tuple)]
+    for c, (rec, dst, g, out, grp) in zip(work, entries):
+        pad = unpack_lion_records(c, (dst if dst is not None else rec).cpu().numpy())
+        if padding is not None:
+            padding.append(pad)
         if out is not None:
             c.arrays["out"] = from_device(out, c.arrays["out"])
     return work

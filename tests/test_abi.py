@@ -84,7 +84,7 @@ def _segment_variants():
     return [
         ("negative n", m(n=-1), -1),
         ("unknown algorithm", m(algorithm=5), -12),
-        ("unknown master format", m(p_dtype=7), -13),
+        ("unknown master format", m(p_dtype=9), -13),
         ("no master", m(p=None), -2),
         ("no gradient", m(g=None), -2),
         ("no first moment", m(m=None), -2),
@@ -173,3 +173,69 @@ def test_convert_argument_codes():
     assert lib.adambridge_convert(p, None, F32, None, None, BF16, 8, 0) == -2
     assert lib.adambridge_convert(p, None, FP8, p, None, F32, 8, 0) == -7
     assert lib.adambridge_convert(p, None, F32, p, None, FP8, 8, 1) == -7
+
+
+def test_pool_threads_without_a_pool():
+    """kernels.c:1484: adambridge_pool_threads(NULL) is 1."""
+    lib = _hip.open_library()
+    assert lib.adambridge_pool_threads(None) == 1
+
+
+# ----------------------------------------------------------- the launch plan
+
+MAX_TILES = (0xFFFFFFFF // 256) // 8 * 8   # workgroups of one dispatch: 2^32 - 1 lanes, whole rounds of 8 XCDs
+
+
+def _fake_segments(specs):
+    """Segments over fake 16-byte-aligned device addresses: planning reads no buffer and launches nothing."""
+    segs = []
+    for k, (n, algo, p_dtype) in enumerate(specs):
+        segs.append(_hip.Segment(p=0x10000000, g=0x20000000, out=0x30000000, n=n, step=1, index=k,
+                                 g_dtype=_hip.DT_BF16, mv_dtype=_hip.DT_BF16, out_dtype=_hip.DT_BF16,
+                                 algorithm=algo, p_dtype=p_dtype))
+    k = _hip.HipKernels()
+    return k, segs, k.segment_array([ctypes.pointer(s) for s in segs])
+
+
+def test_launch_plan_splits_a_segment_at_the_dispatch_limit():
+    """A segment whose tiles overflow one dispatch continues in the next launch from the tile where
+    the first launch stopped (its entry's first tile moved back by the tiles already taken)."""
+    big = MAX_TILES * 1024 + 5000   # 1024-element tiles: MAX_TILES + 5 tiles
+    k, segs, arr = _fake_segments([(3000, 0, _hip.DT_PACKED), (big, 0, _hip.DT_PACKED), (100, 0, _hip.DT_PACKED)])
+    rows = k.plan_launches(arr)
+    variant = rows[0][1]
+    assert rows == [(0, variant, 0, MAX_TILES), (0, variant, 3, MAX_TILES),
+                    (1, variant, -(MAX_TILES - 3), 9), (1, variant, 8, 9)]
+    # every tile of every segment in exactly one launch
+    launch_tiles = {launch: tiles for launch, _, _, tiles in rows}
+    assert sum(launch_tiles.values()) == 3 + (MAX_TILES + 5) + 1
+
+
+def test_launch_plan_batches_by_variant_and_staging_slot():
+    """One launch per kernel variant, split where a variant has more segments than a staging slot
+    holds (128 KiB of 152-byte entries: 862); variants in index order, segments in call order."""
+    specs = [(1000 + k, 1 if k % 3 == 0 else 0, _hip.DT_PACKED_LION if k % 3 == 0 else _hip.DT_PACKED)
+             for k in range(2400)]
+    k, segs, arr = _fake_segments(specs)
+    rows = k.plan_launches(arr)
+    assert len(rows) == 2400
+    by_launch: dict = {}
+    for launch, variant, first, tiles in rows:
+        by_launch.setdefault(launch, []).append((variant, first, tiles))
+    sizes = [len(v) for _, v in sorted(by_launch.items())]
+    assert sizes == [862, 738, 800]   # AdamW pairs (1600: 862 + 738), then Lion records (800)
+    # expected: per variant, segments in call order, each starting where the previous one's tiles end
+    order = [n for n, algo, _ in specs if algo == 0] + [n for n, algo, _ in specs if algo == 1]
+    chunks = [order[:862], order[862:1600], order[1600:]]
+    for (_, entries), ns in zip(sorted(by_launch.items()), chunks):
+        assert len({v for v, _, _ in entries}) == 1
+        tiles = [-(-n // 1024) for n in ns]
+        assert [f for _, f, _ in entries] == [sum(tiles[:j]) for j in range(len(tiles))]
+        assert entries[0][2] == sum(tiles)
+
+
+def test_launch_plan_validates_first():
+    k, segs, arr = _fake_segments([(100, 0, _hip.DT_PACKED), (100, 0, _hip.DT_PACKED)])
+    segs[1].g = None
+    with pytest.raises(RuntimeError, match="code -2"):
+        k.plan_launches(arr)

@@ -103,6 +103,43 @@ def test_many_segments_use_the_device_table():
         check(w, g)
 
 
+def test_graph_capture_inline_launches_and_staged_table_refusal():
+    """Under stream capture: a call of at most 7 segments (descriptors in the kernel arguments) is
+    captured, and every replay applies the update again -- each checked against the oracle on the
+    previous state, with eager work and synchronisations between replays; a call of 8 segments of
+    one variant, whose launch would stage its table through a reused host slot, returns -22
+    before enqueueing anything."""
+    from hip_cases import Prepared
+    rng = np.random.default_rng(15)
+    seven = [O.make_case(rng, 3000 + 100 * k, mv_dtype=MVS[k % 3], index=k) for k in range(7)]
+    eight = [O.make_case(rng, 1000, mv_dtype=O.DT_BF16, index=k) for k in range(8)]
+    run_hip(seven, 16)   # eager first: the default launch queue exists before the capture
+    small, large = Prepared(seven), Prepared(eight)
+    before = large.collect()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.zeros(1024, device="cuda")
+    with torch.cuda.graph(graph):
+        small.call()
+        with pytest.raises(RuntimeError, match="code -22"):
+            large.call()
+        side.add_(1.0)
+    torch.cuda.synchronize()
+    for w, g in zip(before, large.collect()):
+        check(w, g)   # the refused call changed nothing
+    state = small.collect()   # capturing ran nothing
+    for w, g in zip(seven, state):
+        check(w, g)
+    for replay in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        want = O.run_many(state, "oracle", 16)
+        state = small.collect()
+        for w, g in zip(want, state):
+            check(w, g)
+        side.mul_(0.5)   # eager work on the same tensors' stream between replays
+        torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("mv", MVS)
 def test_misaligned_buffers_take_the_scalar_path(mv):
     """Device views that start one element into their allocation: no 16-byte access is legal."""
@@ -288,6 +325,88 @@ def test_fp8_records_reject_bad_segments():
                 mv_dtype=O.DT_FP8, g_dtype=O.DT_BF16, out_dtype=0, algorithm=0, p_dtype=_hip.DT_PACKED8)
     for change, code in ((dict(algorithm=1), -12), (dict(p_lo=rec.data_ptr()), -13),
                          (dict(mv_dtype=O.DT_BF16), -4), (dict(p=rec.data_ptr() + 8), -14)):
+        seg = _hip.Segment(**{**base, **change})
+        with pytest.raises(RuntimeError, match=rf"code {code}"):
+            k.multi_apply(None, k.segment_array([ctypes.pointer(seg)]), [hp])
+    assert torch.count_nonzero(rec).item() == 0   # nothing ran
+
+
+# ------------------------------------------------------------ Lion record layout
+
+from hip_cases import run_hip_lion_records  # noqa: E402
+
+
+@pytest.mark.parametrize("double_buffer", [False, True])
+def test_lion_records_match_oracle(double_buffer):
+    """ADAMBRIDGE_DT_PACKED_LION (master + BF16 m in 768-byte records) gives the separate layout's
+    bytes: sizes around the record and the pair, offsets, SR on/off, every grad/out dtype; in place,
+    the padding slots of the last record keep their bits."""
+    rng = np.random.default_rng(41)
+    cases = []
+    for gt, ot, sr, n in itertools.product([O.DT_BF16, O.DT_F32], [O.DT_NONE, O.DT_F32, O.DT_BF16], [True, False],
+                                           [1, 2, 3, 127, 128, 129, 1000, 2048 + 77, 5001]):
+        cases.append(O.make_case(rng, n, algorithm=O.LION, mv_dtype=O.DT_BF16, g_dtype=gt, out_dtype=ot,
+                                 stochastic=sr, offset=int(rng.integers(0, 2**32)), index=int(rng.integers(0, 999)),
+                                 step=int(rng.integers(1, 30)), lr=1e-4, betas=(0.9, 0.99), weight_decay=0.1))
+    want = O.run_many(cases, "oracle", 16)
+    pads: list = []
+    got = run_hip_lion_records(cases, 16, double_buffer=double_buffer, padding=pads)
+    for w, g in zip(want, got):
+        check(w, g)
+    if not double_buffer:
+        for (pp, pm), c in zip(pads, cases):
+            assert (pp == 0x7FA5A5A5).all() and (pm == 0xA5A5).all(), f"padding changed at n={c.n}"
+
+
+def test_lion_records_zero_gradients_misaligned_and_specials():
+    """Exact-zero gradients at 1% (sign(0) = 0, kernels.c:1107-1124), a misaligned gradient (the
+    element-wise path) and non-finite inputs."""
+    rng = np.random.default_rng(42)
+    cases = []
+    for n, sp in ((999, False), (4096, False), (4096, True), (5001, True)):
+        c = O.make_case(rng, n, algorithm=O.LION, mv_dtype=O.DT_BF16, special=sp, lr=3e-6, betas=(0.9, 0.99),
+                        weight_decay=0.1)
+        if not sp:
+            zero = rng.random(n) < 0.01
+            c.arrays["g"][zero] = 0
+            c.arrays["m"][zero] = 0   # c = 0 exactly where m and g are both zero: u = 0
+            assert zero.any()
+        cases.append(c)
+    want = O.run_many(cases, "oracle", 16)
+    got = run_hip_lion_records(cases, 16, misalign_g=True)
+    for w, g in zip(want, got):
+        bad = O.outputs_equal(w, g, nan_equiv=True)
+        assert not bad, bad
+
+
+def test_lion_records_multi_step_groups_and_steps():
+    """Several segments per call through the group path, then three consecutive steps of one."""
+    rng = np.random.default_rng(43)
+    cases = [O.make_case(rng, 3000 + 64 * k + 3, algorithm=O.LION, mv_dtype=O.DT_BF16, explicit=False, index=k,
+                         step=k + 2, seed=5) for k in range(12)]
+    want = O.run_many(cases, "oracle", 16)
+    got = run_hip_lion_records(cases, 16)
+    for w, g in zip(want, got):
+        check(w, g)
+    case = O.make_case(rng, 5000, algorithm=O.LION, mv_dtype=O.DT_BF16)
+    grads = [O.make_case(rng, 5000, algorithm=O.LION, mv_dtype=O.DT_BF16).arrays["g"] for _ in range(3)]
+    check(run_steps(case, grads, oracle_runner, 16), run_steps(case, grads, run_hip_lion_records, 16))
+
+
+def test_lion_records_reject_bad_segments():
+    """AdamW (-12), FP8 moments (-4) and misaligned records (-14), before anything runs."""
+    import ctypes
+    from adambridge_amd import _hip
+    rng = np.random.default_rng(44)
+    k = _hip.load()
+    case = O.make_case(rng, 300, algorithm=O.LION, mv_dtype=O.DT_BF16)
+    rec = torch.zeros(3 * 768 + 16, dtype=torch.uint8, device="cuda")
+    g = torch.zeros(300, dtype=torch.bfloat16, device="cuda")
+    hp = _hip.HParams(**{kk: case.hparams[kk] for kk, _ in _hip.HParams._fields_})
+    base = dict(p=rec.data_ptr(), g=g.data_ptr(), n=300, step=1, mv_dtype=O.DT_BF16, g_dtype=O.DT_BF16,
+                out_dtype=0, algorithm=1, p_dtype=_hip.DT_PACKED_LION)
+    for change, code in ((dict(algorithm=0), -12), (dict(mv_dtype=O.DT_FP8), -4), (dict(p=rec.data_ptr() + 8), -14),
+                         (dict(p_lo=rec.data_ptr() + 4), -14)):
         seg = _hip.Segment(**{**base, **change})
         with pytest.raises(RuntimeError, match=rf"code {code}"):
             k.multi_apply(None, k.segment_array([ctypes.pointer(seg)]), [hp])
