@@ -71,6 +71,7 @@ EXPORTS = (
     "adambridge_pool_set_spin", "adambridge_multi_step", "adambridge_multi_apply", "adambridge_pool_set_stream",
     "adambridge_pool_sync", "adambridge_set_stream", "adambridge_last_error", "adambridge_backend",
     "adambridge_check_conversions", "adambridge_convert", "adambridge_plan_launches",
+    "adambridge_multi_step_noalloc",
 )
 
 
@@ -105,6 +106,7 @@ def open_library(path: Path = LIB_PATH) -> ctypes.CDLL:
         "adambridge_check_conversions": (ctypes.c_int, [ctypes.c_uint32, ctypes.POINTER(u64), i32]),
         "adambridge_convert": (ctypes.c_int, [vp, vp, i32, vp, vp, i32, i64, i32]),
         "adambridge_plan_launches": (ctypes.c_int, [_SegArray, i32, ctypes.POINTER(i64), i32]),
+        "adambridge_multi_step_noalloc": (ctypes.c_int, [vp, _SegArray, i32]),
     }
     for name in EXPORTS:
         fn = getattr(lib, name)
@@ -205,6 +207,14 @@ class HipKernels:
     def multi_step(self, pool: int | None, segments: ctypes.Array, threads: int = 0) -> None:
         """Enqueue an update of every segment; coefficients from each segment's group and step."""
         self._check(self._lib.adambridge_multi_step(pool, segments, len(segments), threads), "adambridge_multi_step")
+
+    def multi_step_noalloc(self, stream: torch.cuda.Stream | int | None, segments: ctypes.Array) -> None:
+        """multi_step on ``stream`` without any allocation (adambridge_multi_step_noalloc): segment
+        tables in the library's static device array, at most 1024 segments per call; calls that
+        overlap on one GPU race."""
+        rc = self._lib.adambridge_multi_step_noalloc(_stream_handle(stream), segments, len(segments))
+        if rc != 0:
+            raise RuntimeError(f"adambridge_multi_step_noalloc rejected the update (code {rc}): {self.last_error()}")
 
     def multi_apply(self, pool: int | None, segments: ctypes.Array, hparams: list, threads: int = 0) -> None:
         """Like multi_step with explicit coefficients, one ``HParams`` per segment."""

@@ -950,6 +950,33 @@ __global__ __launch_bounds__(kThreads) void k_update_lion_rec(Launch L)
     else update_tile_lion_rec<GT, OT, false>(s, tile, L.tile);
 }
 
+// ------------------------------------------------------- segment-table writer
+//
+// The allocation-free entry point keeps its segment tables in a device array
+// of the library (no staging buffer, no copy from host memory): each table is
+// written by launches of this kernel, the descriptors travelling in its
+// kernel arguments, ordered on the stream before the update that reads them.
+
+constexpr int kWriteSegs = 20;   // descriptors per writer launch: 20 x 144 + 24 bytes of arguments
+
+struct TableChunk {
+    DevSeg* table;        // destination: table entries [0, count)
+    int64_t* starts;      // destination: first tile of each entry
+    int32_t count;
+    int32_t pad;
+    DevSeg segs[kWriteSegs];
+};
+static_assert(sizeof(TableChunk) <= 4096 - 256, "kernel argument block");
+
+__global__ __launch_bounds__(64) void k_write_table(TableChunk C)
+{
+    constexpr int kWords = sizeof(DevSeg) / 8;
+    const uint64_t* src = reinterpret_cast<const uint64_t*>(&C.segs[0]);
+    uint64_t* dst = reinterpret_cast<uint64_t*>(C.table);
+    for (int w = threadIdx.x; w < C.count * kWords; w += 64) dst[w] = src[w];
+    for (int i = threadIdx.x; i < C.count; i += 64) C.starts[i] = C.segs[i].tile_begin;
+}
+
 // ------------------------------------------------------------ kernel table
 
 using KernelFn = void (*)(Launch);

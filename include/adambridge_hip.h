@@ -218,6 +218,21 @@ ADAMBRIDGE_API const char* adambridge_last_error(void);
 /* Name of the device code this library carries, e.g. "hip/gfx950". */
 ADAMBRIDGE_API const char* adambridge_backend(void);
 
+/* adambridge_multi_step with no allocation in the call, for callers that cannot allocate
+ * device or pinned memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  No counterpart in the reference.  Same segments, validation, coefficients and
+ * results as adambridge_multi_step, enqueued on `stream` (a hipStream_t of the current device;
+ * NULL: the null stream).  Instead of a pool's staging buffers it uses one static device array of
+ * the library, 152 KiB per GPU, held until the process ends: launches of more than 7 segments of
+ * one kernel variant find their segment table there, written by small kernels whose arguments
+ * carry the descriptors (no copy from host memory).  Limit: 1024 segments per call (more:
+ * ADAMBRIDGE_ETOOMANY, with the reason in adambridge_last_error(), before anything is enqueued).
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (other streams,
+ * other threads, or replays of graphs holding such calls) race and must be ordered by the caller;
+ * calls from several host threads are serialised on the host.  ADAMBRIDGE_EDEVICE if the stream
+ * belongs to another device. */
+ADAMBRIDGE_API int adambridge_multi_step_noalloc(void* stream, adambridge_segment* const* segs, int32_t nsegs);
+
 /* The launches a multi_apply / multi_step call over these segments would make, without
  * launching anything or touching the device (a diagnostic for bindings and tests).  Segments are
  * validated as multi_apply validates them.  For each entry of each launch, in launch order, writes

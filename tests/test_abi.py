@@ -239,3 +239,19 @@ def test_launch_plan_validates_first():
     segs[1].g = None
     with pytest.raises(RuntimeError, match="code -2"):
         k.plan_launches(arr)
+
+
+def test_noalloc_refuses_more_segments_than_its_array_holds():
+    """adambridge_multi_step_noalloc: 1025 valid segments are refused (-9) with the reason, before
+    any device call; invalid segments get the validation code first."""
+    k, segs, arr = _fake_segments([(100, 0, _hip.DT_PACKED)] * 1025)
+    group = _hip.Group(1e-3, 0.9, 0.999, 1e-8, 0.01, 0, 1, 0)
+    for s in segs:
+        s.group = ctypes.pointer(group)
+    with pytest.raises(RuntimeError, match=r"code -9\): .*at most 1024"):
+        k.multi_step_noalloc(None, arr)
+    segs[3].group = None
+    with pytest.raises(RuntimeError, match=r"code -8"):
+        k.multi_step_noalloc(None, arr)
+    assert k._lib.adambridge_multi_step_noalloc(None, None, 5) == -1
+    assert k._lib.adambridge_multi_step_noalloc(None, None, 0) == 0
