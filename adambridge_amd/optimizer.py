@@ -1,22 +1,32 @@
 """AdamBridge / OptiComputeAdamW / LionBridge with the optimizer state in HBM.
 
-Same constructor, methods and checkpoint format as the reference's
-``adambridge/optimizer.py`` (cited per method); what differs is where the
-state lives and what updates it.  The FP32 (or FP24) master weights, the
-moments and the FP8 block scales are device tensors next to each parameter,
-and one fused HIP kernel launch (libadambridge_hip.so) updates a whole batch of
+The constructor, methods, checkpoint format and error behaviour are the
+reference's (adambridge/optimizer.py, cited per method).  The implementation is
+built around where the state lives here: each parameter's FP32 (or FP24)
+master, moments and FP8 block scales are a
+:class:`~adambridge_amd.state.ParamState` in device memory, and one launch of
+the fused HIP kernel (libadambridge_hip.so) updates a whole batch of
 parameters in a single pass over HBM, writing the new working weights into
 ``p.data``.
 
 Numerically this is torch.optim.AdamW (decoupled weight decay, bias
-correction, the same operation order) with the reference kernel's exact
-rounding: results are bit-identical to the reference's native CPU kernel on
-the same inputs (AVX-512 rounding by default, see ``HipKernels.set_simd_level``).
+correction, the same operation order), or Lion, with the reference kernel's
+exact rounding: results are bit-identical to the reference's native CPU kernel
+on the same inputs.
 
-Host-side knobs of the reference that have nothing to act on here -- NUMA
-placement, thread counts, PyTorch-kernel chunk size, the pinned transfer ring,
-the GPU state budget, the CPU thread auto-tuner -- are accepted and validated
-as the reference validates them, and otherwise ignored.
+The parts:
+
+* ``_Registry`` -- the parameters in index order (the index selects the
+  rounding stream), their slots, and the small ones batched at step_sync;
+* ``_StepWindow`` -- what the gradient hooks may do in the current step:
+  ``no_sync`` nesting, gradient-accumulation micro-batches;
+* ``_HookSet`` -- the post-accumulate-grad hooks;
+* ``_CheckpointReader`` -- validates a whole checkpoint before anything changes.
+
+Host-side knobs of the reference with nothing to act on here -- NUMA
+placement, thread counts, the PyTorch-kernel chunk size, the pinned transfer
+ring, the GPU state budget, the CPU thread auto-tuner -- are accepted and
+validated as the reference validates them, and otherwise ignored.
 """
 
 from __future__ import annotations
@@ -28,10 +38,9 @@ from typing import Any, Callable, Iterable
 
 import torch
 
-from . import _hip
 from .engine import ParamSlot, SmallGroup, StepStats, UpdateEngine
-from .precision import (FP32Store, PackedMaster, RecordMaster, _checked, bytes_per_param, canonical_master_precision,
-                        canonical_precision, check_master_state, load_master_, make_store, store_from_state_dict)
+from .precision import (_checked, bytes_per_param, canonical_master_precision, canonical_precision,
+                        check_master_state, make_store, store_from_state_dict)
 
 __all__ = ["AdamBridge", "LionBridge", "OptiComputeAdamW", "AutoTuneConfig"]
 
@@ -51,6 +60,150 @@ class AutoTuneConfig:
         self.min_precision = canonical_precision(min_precision)
         self.tune_threads = tune_threads
 
+
+# ------------------------------------------------------------- validation
+
+def _check_arguments(algorithm: str, lr, betas, eps, weight_decay, delay_warmup_steps, accumulation_steps,
+                     chunk_size, transfer_buffer_mb, gpu_state_budget, backend) -> None:
+    """The reference's argument checks and messages (optimizer.py:152-170), then this build's own."""
+    rules = [
+        (0.0 <= lr, f"invalid learning rate: {lr}"),
+        (delay_warmup_steps >= 0 and accumulation_steps >= 1,
+         "delay_warmup_steps must be >= 0 and accumulation_steps >= 1"),
+        (0.0 <= eps, f"invalid epsilon: {eps}"),
+        (0.0 <= betas[0] < 1.0 and 0.0 <= betas[1] < 1.0, f"invalid betas: {betas}"),
+        (0.0 <= weight_decay, f"invalid weight_decay: {weight_decay}"),
+        (chunk_size is None or (chunk_size > 0 and chunk_size % 128 == 0),
+         "chunk_size must be a positive multiple of 128"),
+        (transfer_buffer_mb is None or transfer_buffer_mb >= 0, "transfer_buffer_mb must be >= 0"),
+        (gpu_state_budget is None or gpu_state_budget == "auto"
+         or (isinstance(gpu_state_budget, int) and gpu_state_budget >= 0),
+         "gpu_state_budget must be None, 'auto' or a number of bytes >= 0"),
+        (not gpu_state_budget or algorithm == "adamw", "gpu_state_budget is only available for AdamW"),
+        (backend in ("auto", "native", "torch"), "backend must be 'auto', 'native' or 'torch'"),
+        (backend != "torch", "backend='torch' is not available: the update runs only as the fused HIP kernel"),
+    ]
+    for ok, message in rules:
+        if not ok:
+            raise ValueError(message)
+
+
+# ------------------------------------------------------------------ parts
+
+class _Registry:
+    """Parameters in index order, the slot of each, and the small-parameter batches."""
+
+    def __init__(self):
+        self.ordered: list[ParamSlot] = []
+        self.by_param: dict[torch.Tensor, ParamSlot] = {}
+        self.small: list[SmallGroup] = []
+
+    def register(self, p: torch.Tensor, group: dict) -> ParamSlot:
+        if p.is_sparse:
+            raise ValueError("AdamBridge does not support sparse parameters")
+        slot = ParamSlot(len(self.ordered), p, group)
+        self.ordered.append(slot)
+        self.by_param[p] = slot
+        return slot
+
+    def batch_small(self, threshold: int) -> None:
+        """Device parameters under ``threshold`` elements: one batch per device, no hooks."""
+        per_device: dict[torch.device, list[ParamSlot]] = {}
+        for slot in self.ordered:
+            p = slot.param
+            if p.is_cuda and p.requires_grad and slot.numel < threshold and slot.small is None:
+                per_device.setdefault(p.device, []).append(slot)
+        self.small += [SmallGroup(members) for members in per_device.values()]
+
+    def pending(self, *, include_small: bool = True) -> list[ParamSlot]:
+        """Slots with a gradient and no update yet in this step."""
+        return [s for s in self.ordered if not s.submitted and s.param.grad is not None
+                and (include_small or s.small is None)]
+
+
+class _StepWindow:
+    """What the gradient hooks may do in the current step (optimizer.py:285-304): nothing inside
+    ``no_sync``; with gradient accumulation, update only on the window's last backward pass, counted
+    by a callback at the end of each backward."""
+
+    def __init__(self, every: int):
+        self.every = every
+        self.suppressed = 0      # no_sync nesting depth
+        self.backwards = 0       # backward passes finished since the last step
+        self.counting = False    # an end-of-backward callback is queued
+
+    def hook_may_update(self) -> bool:
+        if self.suppressed:
+            return False
+        if self.every == 1:
+            return True
+        if not self.counting:
+            self.counting = True
+            torch.autograd.Variable._execution_engine.queue_callback(self._backward_finished)
+        return self.backwards + 1 >= self.every
+
+    def _backward_finished(self) -> None:
+        self.backwards += 1
+        self.counting = False
+
+    def restart(self) -> None:
+        self.backwards = 0
+
+
+class _HookSet:
+    """Post-accumulate-grad hooks calling one function, kept opaque to TorchDynamo so that compiled
+    autograd calls it instead of tracing the launches inside (optimizer.py:271-274)."""
+
+    def __init__(self, fn: Callable[[torch.Tensor], None]):
+        self._fn = torch.compiler.disable(fn)
+        self._handles: list = []
+        self.active = False
+
+    def add(self, params: Iterable[torch.Tensor]) -> None:
+        self._handles += [p.register_post_accumulate_grad_hook(self._fn) for p in params]
+
+    def clear(self) -> None:
+        while self._handles:
+            self._handles.pop().remove()
+        self.active = False
+
+
+class _CheckpointReader:
+    """A checkpoint's per-parameter entries, validated as a whole before anything is changed (a
+    checkpoint may come from another model, another version or an untrusted source)."""
+
+    def __init__(self, state_dict: dict[str, Any], slots: list[ParamSlot], lion: bool):
+        entries = {}
+        for key, entry in state_dict["state"].items():
+            index = int(key) if isinstance(key, str) and key.isdigit() else key
+            if type(index) is not int or not 0 <= index < len(slots):
+                raise ValueError(f"checkpoint state for parameter {index!r}: this optimizer has parameters "
+                                 f"0..{len(slots) - 1}")
+            entries[index] = entry
+        for index, entry in entries.items():
+            numel = slots[index].numel
+            if entry.get("master") is not None:
+                check_master_state(entry["master"], numel, f"master weights of parameter {index}")
+            for key in ("exp_avg", "exp_avg_sq"):
+                if isinstance(entry.get(key), torch.Tensor):
+                    _checked(entry[key], numel, f"{key} of parameter {index}")
+            if not lion and "exp_avg_sq" not in entry:
+                raise ValueError("checkpoint has no exp_avg_sq (saved by LionBridge?); AdamW needs both moments")
+        self.entries = entries
+
+    @staticmethod
+    def moment(saved: Any, numel: int, role: str, precision: str, device):
+        """A saved moment as a store of ``precision``: the torch.optim.AdamW layout (a plain tensor)
+        converted, a store dictionary rebuilt and converted if its precision differs."""
+        if isinstance(saved, torch.Tensor):
+            return make_store(precision, numel, role, init=saved.to(device, torch.float32), device=device)
+        store = store_from_state_dict(saved, numel, role, device=device)
+        if store.precision == precision:
+            return store
+        return make_store(precision, numel, role, init=store.to_fp32(), device=device)
+
+
+# -------------------------------------------------------------- the optimizer
 
 class AdamBridge(torch.optim.Optimizer):
     r"""AdamW whose state lives in GPU memory and is updated by one fused HIP kernel.
@@ -82,15 +235,15 @@ class AdamBridge(torch.optim.Optimizer):
     ``backend``: 'auto' or 'native' (both the HIP kernel); 'torch' is refused --
     there is no second implementation to switch to.
 
-    HIP-specific: ``state_layout`` -- 'auto' (default) keeps an FP32 master and BF16
-    moments interleaved, 16 bytes per pair of elements, and an FP32 master and FP8
-    moments in one 768-byte record per 128-element block (block scales apart), which
-    stream faster from HBM than separate arrays; 'separate' keeps the reference's layout;
-    values, rounding and checkpoints are identical either way.  ``double_buffer`` -- the
-    BF16 interleaved state alternates between two buffers (reads and writes go to
-    different memory), at 8 more bytes per parameter; measured at the 7B list it is as
-    fast as one buffer (20.8 ms), and 3% faster only where the single buffer landed in
-    slow HBM (FP8 records are updated in place).
+    HIP-specific: ``state_layout`` -- 'auto' (default) keeps each parameter's master and
+    moments interleaved where a layout for its precision exists (AdamW with BF16 moments:
+    16 bytes per pair of elements; AdamW with FP8 moments: one 768-byte record per
+    128-element block, block scales apart; Lion with a BF16 moment: one 768-byte record per
+    128 elements), which stream faster from HBM than separate arrays; 'separate' keeps the
+    reference's arrays; values, rounding and checkpoints are identical either way.
+    ``double_buffer`` -- interleaved BF16 state alternates between two buffers (reads and
+    writes go to different memory), at 8 (Lion 6) more bytes per parameter; FP8 records are
+    updated in place.
     """
 
     _algorithm = "adamw"
@@ -123,49 +276,24 @@ class AdamBridge(torch.optim.Optimizer):
         state_layout: str = "auto",
         double_buffer: bool = False,
     ):
-        # validation as optimizer.py:152-170
-        if not 0.0 <= lr:
-            raise ValueError(f"invalid learning rate: {lr}")
-        if delay_warmup_steps < 0 or accumulation_steps < 1:
-            raise ValueError("delay_warmup_steps must be >= 0 and accumulation_steps >= 1")
-        if not 0.0 <= eps:
-            raise ValueError(f"invalid epsilon: {eps}")
-        if not 0.0 <= betas[0] < 1.0 or not 0.0 <= betas[1] < 1.0:
-            raise ValueError(f"invalid betas: {betas}")
-        if not 0.0 <= weight_decay:
-            raise ValueError(f"invalid weight_decay: {weight_decay}")
-        if chunk_size is not None and (chunk_size <= 0 or chunk_size % 128):
-            raise ValueError("chunk_size must be a positive multiple of 128")
-        if transfer_buffer_mb is not None and transfer_buffer_mb < 0:
-            raise ValueError("transfer_buffer_mb must be >= 0")
-        if not (gpu_state_budget is None or gpu_state_budget == "auto"
-                or (isinstance(gpu_state_budget, int) and gpu_state_budget >= 0)):
-            raise ValueError("gpu_state_budget must be None, 'auto' or a number of bytes >= 0")
-        if gpu_state_budget and self._algorithm != "adamw":
-            raise ValueError("gpu_state_budget is only available for AdamW")
-        if backend not in ("auto", "native", "torch"):
-            raise ValueError("backend must be 'auto', 'native' or 'torch'")
-        if backend == "torch":
-            raise ValueError("backend='torch' is not available: the update runs only as the fused HIP kernel")
-        self.gpu_state_budget = gpu_state_budget or None   # everything is on the GPU already
+        _check_arguments(self._algorithm, lr, betas, eps, weight_decay, delay_warmup_steps, accumulation_steps,
+                         chunk_size, transfer_buffer_mb, gpu_state_budget, backend)
         self.precision = canonical_precision(precision)
         self.master_precision = canonical_master_precision(master_precision)
+        self.gpu_state_budget = gpu_state_budget or None   # every byte of state is on the GPU already
         self.release_grads = release_grads
         self.small_param_threshold = small_param_threshold
-        self._slots: dict[torch.Tensor, ParamSlot] = {}
-        self._ordered: list[ParamSlot] = []
-        self._hooks: list[torch.utils.hooks.RemovableHandle] = []
-        self._hooked = False
-        self._accumulating = 0
         self.accumulation_steps = accumulation_steps
-        self._micro = 0
-        self._backward_counted = False
         self.delay_updates = delay_updates
         self.delay_warmup_steps = delay_warmup_steps
-        self._steps_synced = 0
         self.last_step_stats: StepStats | None = None
-        self._autotune = autotune
+        self._registry = _Registry()
+        self._window = _StepWindow(accumulation_steps)
+        self._hooks = _HookSet(self._on_grad_ready)
+        self._steps_synced = 0
         self._autotune_log: list[str] = []
+        if autotune:
+            self._autotune_log.append("autotune: nothing to tune on the GPU (no host threads, one kernel launch)")
 
         super().__init__(params, dict(lr=lr, betas=betas, eps=eps, weight_decay=weight_decay))
 
@@ -176,139 +304,113 @@ class AdamBridge(torch.optim.Optimizer):
             double_buffer=double_buffer)
         self._engine.delay = delay_updates and delay_warmup_steps == 0
         self._finalizer = weakref.finalize(self, UpdateEngine.close, self._engine)
-        self._small_groups = self._build_small_groups()
-        if autotune:
-            self._autotune_log.append("autotune: nothing to tune on the GPU (no host threads, one kernel launch)")
+        self._registry.batch_small(small_param_threshold)
+
+    # Slots in index order and by parameter (names the tests and tools read).
+    @property
+    def _ordered(self) -> list[ParamSlot]:
+        return self._registry.ordered
+
+    @property
+    def _slots(self) -> dict[torch.Tensor, ParamSlot]:
+        return self._registry.by_param
+
+    @property
+    def _small_groups(self) -> list[SmallGroup]:
+        return self._registry.small
 
     # ---------------------------------------------------------------- groups
 
     def add_param_group(self, param_group: dict[str, Any]) -> None:
-        """optimizer.py:221-237: every parameter gets the next index (its rounding stream)."""
+        """Every new parameter takes the next index, its rounding stream (optimizer.py:221-237)."""
         super().add_param_group(param_group)
         group = self.param_groups[-1]
-        for p in group["params"]:
-            if p.is_sparse:
-                raise ValueError("AdamBridge does not support sparse parameters")
-            slot = ParamSlot(len(self._ordered), p, group)
-            self._slots[p] = slot
-            self._ordered.append(slot)
-            if self._hooked and p.requires_grad:
-                self._hooks.append(p.register_post_accumulate_grad_hook(self._hook()))
+        added = [self._registry.register(p, group) for p in group["params"]]
+        if self._hooks.active:
+            self._hooks.add(s.param for s in added if s.param.requires_grad)
 
-    def _build_small_groups(self) -> list[SmallGroup]:
-        """Small GPU parameters, by device: no hook, one batched launch at step_sync (optimizer.py:239-246)."""
-        by_dev: dict[torch.device, list[ParamSlot]] = {}
-        for slot in self._ordered:
-            p = slot.param
-            if p.is_cuda and p.requires_grad and slot.numel < self.small_param_threshold:
-                by_dev.setdefault(p.device, []).append(slot)
-        return [SmallGroup(slots) for slots in by_dev.values()]
-
-    def _rebind_groups(self) -> None:
+    def _regroup(self) -> None:
+        """Point every slot at its group dict again (load_state_dict replaces the dicts)."""
         for group in self.param_groups:
             for p in group["params"]:
-                self._slots[p].group = group
+                self._registry.by_param[p].group = group
 
     # ------------------------------------------------------------ async mode
 
     def attach_hooks(self, model: torch.nn.Module | None = None) -> "AdamBridge":
-        """Update each parameter as soon as its gradient is ready (optimizer.py:255-269)."""
-        if self._hooked:
-            return self
-        wanted = None if model is None else {id(p) for p in model.parameters()}
-        hook = self._hook()
-        for slot in self._ordered:
-            p = slot.param
-            if p.requires_grad and slot.small is None and (wanted is None or id(p) in wanted):
-                self._hooks.append(p.register_post_accumulate_grad_hook(hook))
-        self._hooked = True
+        """Update each parameter as soon as its gradient is ready (optimizer.py:255-269): the
+        parameters of ``model`` (default: all) that require gradients and are not small."""
+        if not self._hooks.active:
+            keep = None if model is None else {id(p) for p in model.parameters()}
+            self._hooks.add(s.param for s in self._ordered
+                            if s.param.requires_grad and s.small is None and (keep is None or id(s.param) in keep))
+            self._hooks.active = True
         return self
 
-    def _hook(self):
-        """Opaque to TorchDynamo, like the reference (optimizer.py:271-274)."""
-        return torch.compiler.disable(self._on_grad_ready)
-
     def detach_hooks(self) -> None:
-        for h in self._hooks:
-            h.remove()
         self._hooks.clear()
-        self._hooked = False
+
+    @property
+    def _hooked(self) -> bool:
+        return self._hooks.active
 
     @contextlib.contextmanager
     def no_sync(self):
-        """Accumulate gradients without updating (all but the last micro-batch)."""
-        self._accumulating += 1
+        """Accumulate gradients without updating (every micro-batch but the last)."""
+        self._window.suppressed += 1
         try:
             yield
         finally:
-            self._accumulating -= 1
+            self._window.suppressed -= 1
 
     def _on_grad_ready(self, p: torch.Tensor) -> None:
-        """optimizer.py:291-304."""
-        if self._accumulating or p.grad is None:
-            return
-        if self.accumulation_steps > 1:
-            if not self._backward_counted:
-                self._backward_counted = True
-                torch.autograd.Variable._execution_engine.queue_callback(self._end_of_backward)
-            if self._micro + 1 < self.accumulation_steps:
-                return
-        self._submit([self._slots[p]], [p.grad], hooked=True, release=self.release_grads)
-
-    def _end_of_backward(self) -> None:
-        self._micro += 1
-        self._backward_counted = False
+        """The hook (optimizer.py:291-304): update ``p`` now, unless the step window says otherwise."""
+        if p.grad is not None and self._window.hook_may_update():
+            self._submit([self._registry.by_param[p]], [p.grad], hooked=True, release=self.release_grads)
 
     def _submit(self, slots: list[ParamSlot], grads: list[torch.Tensor], hooked: bool, release: bool) -> None:
-        """optimizer.py:310-321, batched: one launch for ``slots``."""
-        for slot, grad in zip(slots, grads):
-            if slot.submitted:
-                raise RuntimeError(
-                    "AdamBridge: parameter received a second gradient before step_sync(); "
-                    "run extra backward passes inside optimizer.no_sync() to accumulate gradients")
-            if grad.is_sparse:
-                raise RuntimeError("AdamBridge does not support sparse gradients")
+        """One launch for ``slots`` (optimizer.py:310-321, batched)."""
+        if any(s.submitted for s in slots):
+            raise RuntimeError(
+                "AdamBridge: parameter received a second gradient before step_sync(); "
+                "run extra backward passes inside optimizer.no_sync() to accumulate gradients")
+        if any(g.is_sparse for g in grads):
+            raise RuntimeError("AdamBridge does not support sparse gradients")
         try:
             self._engine.update(slots, grads, hooked=hooked, grads_kept=not release)
-        except Exception as exc:   # surfaced like the reference's worker errors (engine.py:1150-1158)
+        except Exception as exc:   # surfaced as the reference surfaces its workers' errors (engine.py:1150-1158)
             raise RuntimeError(f"adambridge update failed: {exc}") from exc
         for slot in slots:
             slot.submitted = True
             if release:
                 slot.param.grad = None
 
-    def _flush_small(self, release: bool) -> None:
-        """The small parameters' updates, one launch per device (optimizer.py:323-330)."""
-        for group in self._small_groups:
-            live = [s for s in group.slots if not s.submitted and s.param.grad is not None]
-            if live:
-                self._submit(live, [s.param.grad for s in live], hooked=self._hooked, release=release)
-
     def step_sync(self) -> StepStats:
-        """Update the small parameters and order every update of this step before subsequent
-        work on the current stream -- a stream wait, not a host wait.  With delayed updates, only
-        the write-backs are ordered (optimizer.py:332-355)."""
+        """Close the step (optimizer.py:332-355): update what the hooks left -- the small parameters,
+        and with gradient accumulation any parameter whose window the step cut short -- then order
+        every update before subsequent work on the current stream (a stream wait, not a host wait;
+        with delayed updates, only the write-backs)."""
         try:
-            if not self._accumulating:
+            if not self._window.suppressed:
                 if self.accumulation_steps > 1:
-                    self._submit_remaining()  # a window cut short: hooks have not fired
-                self._flush_small(release=self.release_grads and self._hooked)
+                    late = self._registry.pending(include_small=False)
+                    if late:
+                        self._submit(late, [s.param.grad for s in late], hooked=False, release=False)
+                release = self.release_grads and self._hooks.active
+                for batch in self._registry.small:
+                    live = [s for s in batch.slots if not s.submitted and s.param.grad is not None]
+                    if live:
+                        self._submit(live, [s.param.grad for s in live], hooked=self._hooks.active, release=release)
             stats = self._engine.finish_step()
         finally:
             for slot in self._ordered:
                 slot.submitted = False
-            self._micro = 0
+            self._window.restart()
         self.last_step_stats = stats
         self._steps_synced += 1
         if self.delay_updates and self._steps_synced >= self.delay_warmup_steps:
             self._engine.delay = True
         return stats
-
-    def _submit_remaining(self, release: bool = False) -> None:
-        todo = [s for s in self._ordered
-                if not s.submitted and s.small is None and s.param.grad is not None]
-        if todo:
-            self._submit(todo, [s.param.grad for s in todo], hooked=False, release=release)
 
     def flush(self) -> None:
         """Apply every pending (delayed) update to the parameters (optimizer.py:432-436)."""
@@ -318,13 +420,13 @@ class AdamBridge(torch.optim.Optimizer):
 
     @torch.no_grad()
     def step(self, closure: Callable[[], torch.Tensor] | None = None):
-        """Update every parameter that has a gradient and was not updated by a hook this iteration
-        -- all of them in one kernel launch -- then :meth:`step_sync` (optimizer.py:440-451)."""
+        """Update every parameter that has a gradient and no update yet this step -- all of them in one
+        launch per device -- then :meth:`step_sync` (optimizer.py:440-451)."""
         loss = None
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
-        todo = [s for s in self._ordered if not s.submitted and s.param.grad is not None]
+        todo = self._registry.pending()
         if todo:
             self._submit(todo, [s.param.grad for s in todo], hooked=False, release=False)
         self.step_sync()
@@ -338,11 +440,8 @@ class AdamBridge(torch.optim.Optimizer):
         self._engine.wait()
         if precision == self.precision:
             return
-        self._engine.precision = precision
-        for slot in self._ordered:
-            if slot.initialized:
-                self._engine.convert_moments(slot, precision)
-        self.precision = precision
+        self._engine.rebuild([s for s in self._ordered if s.initialized], precision)
+        self._engine.precision = self.precision = precision
 
     @property
     def autotune_log(self) -> list[str]:
@@ -361,107 +460,66 @@ class AdamBridge(torch.optim.Optimizer):
 
     def memory_report(self) -> dict[str, int]:
         """Device bytes held by the optimizer, by category (optimizer.py:496-513)."""
-        report = {"master": 0, "moments": 0, "staging": 0}
+        master = moments = staging = 0
         for slot in self._ordered:
-            if not slot.initialized:
+            if slot.state is None:
                 continue
-            if not slot.in_place:
-                report["master"] += slot.master.nbytes
-            report["moments"] += slot.m.nbytes + (slot.v.nbytes if slot.v is not None else 0)
-            if slot.out is not None:
-                report["staging"] += slot.out.nbytes
-        report["total"] = sum(report.values())
-        report["gpu_state"] = report["total"]   # all of it is on the GPU
-        return report
+            a, b = slot.state.footprint()
+            master, moments = master + a, moments + b
+            staging += 0 if slot.out is None else slot.out.nbytes
+        total = master + moments + staging
+        return {"master": master, "moments": moments, "staging": staging, "total": total, "gpu_state": total}
 
     def expected_bytes_per_param(self) -> float:
         return bytes_per_param(self.precision, 1 if self._algorithm == "lion" else 2, master=self.master_precision)
 
     def master_params(self) -> list[torch.Tensor | None]:
-        """FP32 master copies (``None`` before a parameter's first update; decoded for FP24 and
-        the interleaved layout).  Waits for enqueued updates."""
+        """FP32 master copies (``None`` before a parameter's first update; decoded for FP24 and the
+        interleaved layouts).  Waits for enqueued updates."""
         self._engine.wait()
-        out = []
-        for slot in self._ordered:
-            if not slot.initialized:
-                out.append(None)
-            elif isinstance(slot.master, FP32Store):
-                out.append(slot.master.data)
-            else:
-                out.append(slot.master.to_fp32())
-        return out
+        return [None if s.state is None else s.state.master_fp32() for s in self._ordered]
 
     # ------------------------------------------------------------ checkpoint
 
     def state_dict(self) -> dict[str, Any]:
-        """Applies pending delayed updates first; the reference's layout (optimizer.py:525-544)."""
+        """The reference's checkpoint (optimizer.py:525-544), after applying pending delayed updates so
+        that the model's weights match the saved masters."""
         self._engine.flush()
         self._engine.wait()
-        sd = super().state_dict()
-        sd["state"] = {}
-        for slot in self._ordered:
-            if not slot.initialized:
-                continue
-            if isinstance(slot.master, (FP32Store, PackedMaster, RecordMaster)):
-                master = slot.master.data   # a plain FP32 tensor (interleaved layouts: a contiguous copy)
-            else:
-                master = slot.master.state_dict()
-            st = sd["state"][slot.index] = {"step": slot.step, "master": master, "exp_avg": slot.m.state_dict()}
-            if slot.v is not None:
-                st["exp_avg_sq"] = slot.v.state_dict()
-        sd["adambridge"] = {"precision": self.precision, "master_precision": self.master_precision, "format": 1,
-                            "algorithm": self._algorithm}
-        return sd
+        out = super().state_dict()
+        out["state"] = {s.index: {"step": s.step, **s.state.export()} for s in self._ordered if s.state is not None}
+        out["adambridge"] = {"precision": self.precision, "master_precision": self.master_precision, "format": 1,
+                             "algorithm": self._algorithm}
+        return out
 
     def load_state_dict(self, state_dict: dict[str, Any]) -> None:
-        """An AdamBridge / LionBridge checkpoint, or a torch.optim.AdamW one (moments converted to this
-        optimizer's precision).  Everything is validated before anything changes (optimizer.py:546-602)."""
+        """An AdamBridge / LionBridge checkpoint, or a torch.optim.AdamW one, moments converted to this
+        optimizer's precision (optimizer.py:546-602).  Nothing changes unless all of it is valid."""
         self._engine.discard_pending()
-        saved = {int(k) if isinstance(k, str) and k.isdigit() else k: v for k, v in state_dict["state"].items()}
-        lion = self._algorithm == "lion"
-        for index, st in saved.items():
-            if isinstance(index, bool) or not isinstance(index, int) or not 0 <= index < len(self._ordered):
-                raise ValueError(f"checkpoint state for parameter {index!r}: this optimizer has parameters "
-                                 f"0..{len(self._ordered) - 1}")
-            numel = self._ordered[index].numel
-            if st.get("master") is not None:
-                check_master_state(st["master"], numel, f"master weights of parameter {index}")
-            for key in ("exp_avg", "exp_avg_sq"):
-                if isinstance(st.get(key), torch.Tensor):
-                    _checked(st[key], numel, f"{key} of parameter {index}")
-            if not lion and "exp_avg_sq" not in st:
-                raise ValueError("checkpoint has no exp_avg_sq (saved by LionBridge?); AdamW needs both moments")
+        reader = _CheckpointReader(state_dict, self._ordered, self._algorithm == "lion")
         super().load_state_dict({"state": {}, "param_groups": state_dict["param_groups"]})
-        self._rebind_groups()
+        self._regroup()
+        keys = (("m", "exp_avg"),) if self._algorithm == "lion" else (("m", "exp_avg"), ("v", "exp_avg_sq"))
+        slots, masters, moments = [], [], []
         with torch.no_grad():
-            for index, st in saved.items():
+            for index, entry in reader.entries.items():
                 slot = self._ordered[index]
-                if not slot.initialized:
-                    self._engine.initialize(slot)
-                slot.step = int(st["step"])
-                if st.get("master") is not None:
-                    load_master_(slot.master, st["master"])
-                dev = slot.param.device
-                self._engine.replace_moments(
-                    slot, self._load_store(st["exp_avg"], slot.numel, "m", dev),
-                    None if lion else self._load_store(st["exp_avg_sq"], slot.numel, "v", dev))
-
-    def _load_store(self, saved, numel: int, role: str, device):
-        if isinstance(saved, torch.Tensor):   # torch.optim.AdamW layout
-            return make_store(self.precision, numel, role, init=saved.to(device, torch.float32), device=device)
-        store = store_from_state_dict(saved, numel, role, device=device)
-        if store.precision != self.precision:
-            store = make_store(self.precision, numel, role, init=store.to_fp32(), device=device)
-        return store
+                slot.step = int(entry["step"])
+                slots.append(slot)
+                masters.append(entry.get("master"))
+                moments.append({role: reader.moment(entry[key], slot.numel, role, self.precision, slot.param.device)
+                                for role, key in keys})
+        self._engine.rebuild(slots, self.precision, masters, moments)
 
     def close(self) -> None:
         """Apply pending delayed updates and release the engine (optimizer.py:604-612)."""
         self.detach_hooks()
-        if self._finalizer.alive:
-            try:
-                self._engine.flush()
-            finally:
-                self._finalizer()
+        if not self._finalizer.alive:
+            return
+        try:
+            self._engine.flush()
+        finally:
+            self._finalizer()
 
 
 OptiComputeAdamW = AdamBridge

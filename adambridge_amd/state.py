@@ -1,0 +1,474 @@
+"""One parameter's optimizer state in HBM, in the layout the fused kernel streams fastest.
+
+A :class:`ParamState` owns every device buffer of one parameter's state --
+master weights, moments, FP8 block scales -- and knows three things about them:
+
+* how the kernel sees them: :meth:`ParamState.bind` fills the state fields of
+  the parameter's ``adambridge_segment``;
+* what they hold, in the reference's terms: :meth:`ParamState.master_fp32`,
+  :meth:`ParamState.moment` (a store of the reference's API), :meth:`ParamState.export`
+  (checkpoint entries) and :meth:`ParamState.window` (the separate arrays of an
+  element range, for inspection and parity checks);
+* how to take values in: :meth:`ParamState.load`.
+
+Layouts (the byte layouts are declared in include/adambridge_hip.h):
+
+==============  =====================================  ======================================
+layout          serves                                 bytes of state per element
+==============  =====================================  ======================================
+separate        anything (the reference's arrays)      master 4 (FP24: 3) + moments
+pairs           AdamW, FP32 master, BF16 moments       16 per 2 elements (x2 double-buffered)
+fp8-records     AdamW, FP32 master, FP8 moments        768 per 128 + two FP32 scales per 128
+lion-records    Lion, FP32 master, BF16 moment         768 per 128 (x2 double-buffered)
+==============  =====================================  ======================================
+
+The interleaved layouts turn the master and moment streams into one stream of
+state per parameter (measured faster on MI355X, see adambridge_hip.hip).  Values,
+roundings and rounding streams are those of the separate arrays, element for
+element, so the layout never shows in results or checkpoints.
+"""
+
+from __future__ import annotations
+
+from typing import Any
+
+import torch
+
+from . import _hip
+from . import formats as F
+from .precision import BF16Store, FP8Store, FP24Store, FP32Store, MomentStore, load_master_, make_master, make_store
+
+__all__ = ["ParamState", "SeparateState", "PairState", "AdamRecordState", "LionRecordState", "choose_layout",
+           "new_state", "new_states", "arena_plan", "LAYOUTS"]
+
+LAYOUTS = ("separate", "pairs", "fp8-records", "lion-records")
+
+
+def choose_layout(algorithm: str, precision: str, master_precision: str, requested: str = "auto",
+                  master_is_param: bool = False) -> str:
+    """The layout of a parameter's state: the interleaved one for its (algorithm, precision) when
+    there is one and the master is an FP32 buffer of the optimizer's own, else 'separate'."""
+    if requested == "separate" or master_is_param or master_precision != "fp32":
+        return "separate"
+    return {("adamw", "bf16"): "pairs", ("adamw", "fp8"): "fp8-records",
+            ("lion", "bf16"): "lion-records"}.get((algorithm, precision), "separate")
+
+
+class ParamState:
+    """Base of the layouts: ``numel`` elements of one parameter on ``device``."""
+
+    layout = ""
+    precision = ""            # moment precision
+    master_precision = "fp32"
+    master_is_param = False   # the master is the FP32 parameter itself, updated in place
+
+    def __init__(self, numel: int, device, roles: tuple[str, ...]):
+        self.numel = int(numel)
+        self.device = torch.device(device)
+        self.roles = roles    # ('m', 'v') for AdamW, ('m',) for Lion
+
+    # -- the kernel's view ---------------------------------------------------
+
+    def bind(self, seg: _hip.Segment) -> None:
+        """Set the state fields of ``seg``: p, p_lo, m, v, m_scale, v_scale, p_dtype, mv_dtype."""
+        raise NotImplementedError
+
+    @property
+    def alternates(self) -> bool:
+        """True if the buffers swap after every update (double buffering): rebind before each launch."""
+        return False
+
+    def advance(self) -> None:
+        """After a launch: the state just written becomes the current one."""
+
+    # -- contents ----------------------------------------------------------------
+
+    def master_fp32(self) -> torch.Tensor:
+        """The master weights as a flat FP32 tensor (a copy unless they are stored as one)."""
+        raise NotImplementedError
+
+    def moment(self, role: str) -> MomentStore:
+        """Moment ``role`` as a store of the reference's API (a copy for interleaved layouts)."""
+        raise NotImplementedError
+
+    def export_master(self) -> Any:
+        """Checkpoint master entry: an FP32 tensor, or an FP24 store dictionary."""
+        return self.master_fp32()
+
+    def export(self) -> dict[str, Any]:
+        """This state's checkpoint entries: ``master``, ``exp_avg`` and (AdamW) ``exp_avg_sq``."""
+        out = {"master": self.export_master()}
+        for role, key in zip(self.roles, ("exp_avg", "exp_avg_sq")):
+            out[key] = self.moment(role).state_dict()
+        return out
+
+    def load(self, master: Any = None, moments: dict[str, MomentStore] | None = None) -> None:
+        """Take validated checkpoint master weights (or FP32 values) and moment stores of this state's
+        precision; anything left out keeps its value."""
+        raise NotImplementedError
+
+    def footprint(self) -> tuple[int, int]:
+        """Device bytes held: (master, moments), every buffer counted once."""
+        raise NotImplementedError
+
+    def window(self, lo: int, hi: int) -> dict[str, torch.Tensor]:
+        """Elements [lo, hi) as the separate arrays the oracle takes: 'p' (FP32, or the FP24 hi plane
+        and 'p_lo'), 'm', 'v' (FP32 values, BF16 bits, or FP8 codes with 'm_scale' / 'v_scale' of the
+        blocks covering the range; FP8 ranges start on a block boundary)."""
+        raise NotImplementedError
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _as_master_values(master: Any, numel: int, device) -> torch.Tensor:
+    """FP32 values from checkpoint master weights (tensor or store dictionary) or plain values."""
+    from .precision import master_to_fp32
+    return master_to_fp32(master, numel, device)
+
+
+# ------------------------------------------------------------------- separate
+
+class SeparateState(ParamState):
+    """The reference's arrays: a master store (FP32 -- possibly the FP32 parameter itself -- or FP24)
+    and one store per moment."""
+
+    layout = "separate"
+
+    def __init__(self, master: MomentStore, moments: dict[str, MomentStore], master_is_param: bool = False):
+        super().__init__(master.numel, master.device, tuple(moments))
+        self.master = master
+        self.stores = dict(moments)
+        self.master_is_param = master_is_param   # instance value over the class default
+        self.precision = next(iter(moments.values())).precision
+        self.master_precision = master.precision
+
+    def bind(self, seg):
+        values, low = self.master.native_buffers
+        seg.p, seg.p_lo = values.data_ptr(), _ptr(low)
+        seg.p_dtype = _hip.MASTER_CODES[self.master_precision]
+        m_values, m_scale = self.stores["m"].native_buffers
+        seg.m, seg.m_scale = m_values.data_ptr(), _ptr(m_scale)
+        seg.v = seg.v_scale = None
+        if "v" in self.stores:
+            v_values, v_scale = self.stores["v"].native_buffers
+            seg.v, seg.v_scale = v_values.data_ptr(), _ptr(v_scale)
+        seg.mv_dtype = _hip.MOMENT_CODES[self.precision]
+
+    def master_fp32(self):
+        return self.master.data if isinstance(self.master, FP32Store) else self.master.to_fp32()
+
+    def export_master(self):
+        return self.master.data if isinstance(self.master, FP32Store) else self.master.state_dict()
+
+    def moment(self, role):
+        return self.stores[role]
+
+    def load(self, master=None, moments=None):
+        if master is not None:
+            load_master_(self.master, master)
+        for role, store in (moments or {}).items():
+            if isinstance(store, FP8Store) and store.block != F.FP8_BLOCK:   # the kernel takes 128-blocks
+                store = FP8Store(self.numel, role, init=store.to_fp32(), device=self.device)
+            self.stores[role] = store if store.device == self.device else _moved(store, self.device)
+
+    def footprint(self):
+        master = 0 if self.master_is_param else self.master.nbytes
+        return master, sum(s.nbytes for s in self.stores.values())
+
+    def window(self, lo, hi):
+        out: dict[str, torch.Tensor] = {}
+        if isinstance(self.master, FP24Store):
+            out["p"], out["p_lo"] = self.master.hi[lo:hi], self.master.lo[lo:hi]
+        else:
+            out["p"] = self.master.data[lo:hi]
+        for role, store in self.stores.items():
+            if isinstance(store, FP8Store):
+                b0, b1 = lo // store.block, -(-hi // store.block)
+                out[role] = store.q[b0 * store.block: b1 * store.block].view(torch.uint8)
+                out[role + "_scale"] = store.scale[b0:b1]
+            else:
+                out[role] = store.data[lo:hi]
+        return out
+
+
+def _moved(store: MomentStore, device) -> MomentStore:
+    """A copy of ``store`` on ``device``."""
+    sd = store.state_dict()
+    from .precision import store_from_state_dict
+    role = getattr(store, "role", "m")
+    return store_from_state_dict({k: v.to(device) if isinstance(v, torch.Tensor) else v for k, v in sd.items()},
+                                 store.numel, role, device=device)
+
+
+# ------------------------------------------------------------ interleaved base
+
+class _Interleaved(ParamState):
+    """State in one buffer (two when double-buffered): ``current`` is read, ``target`` written."""
+
+    def __init__(self, numel, device, roles, buffers: list[torch.Tensor]):
+        super().__init__(numel, device, roles)
+        self.buffers = buffers
+        self.turn = 0
+
+    @property
+    def current(self) -> torch.Tensor:
+        return self.buffers[self.turn]
+
+    @property
+    def target(self) -> torch.Tensor | None:
+        return self.buffers[1 - self.turn] if len(self.buffers) == 2 else None
+
+    @property
+    def alternates(self):
+        return len(self.buffers) == 2
+
+    def advance(self):
+        if len(self.buffers) == 2:
+            self.turn ^= 1
+
+    def _column(self, role: str) -> torch.Tensor:
+        """The strided view of ``role``'s values ('p' the FP32 master, 'm' / 'v' the moments) in
+        ``current``, in element order once flattened (padding included)."""
+        raise NotImplementedError
+
+    def _padded(self) -> int:
+        return self._column("p").numel()
+
+    def _put(self, role: str, values: torch.Tensor) -> None:
+        column = self._column(role)
+        flat = torch.zeros(column.numel(), dtype=column.dtype, device=self.device)
+        flat[: self.numel] = values.reshape(-1)[: self.numel].to(self.device)
+        column.copy_(flat.view(column.shape))
+
+    def master_fp32(self):
+        return self._column("p").reshape(-1)[: self.numel].clone()
+
+    def footprint(self):
+        total = sum(b.nbytes for b in self.buffers)
+        master = 4 * self.numel * len(self.buffers)
+        return master, total - master
+
+
+class PairState(_Interleaved):
+    """AdamW, FP32 master, BF16 moments: 16 bytes per pair of elements {p[2k], p[2k+1], m[2k] | m[2k+1] << 16,
+    v[2k] | v[2k+1] << 16} (ADAMBRIDGE_DT_PACKED)."""
+
+    layout = "pairs"
+    precision = "bf16"
+
+    def __init__(self, numel, device, double_buffer: bool = False, memory: list[torch.Tensor] | None = None):
+        pairs = max(1, (int(numel) + 1) // 2)
+        bufs = [m.view(torch.int32).view(pairs, 4) for m in memory] if memory else \
+            [torch.zeros(pairs, 4, dtype=torch.int32, device=device) for _ in range(2 if double_buffer else 1)]
+        super().__init__(numel, device, ("m", "v"), bufs)
+
+    @staticmethod
+    def buffer_bytes(numel: int) -> int:
+        return max(1, (int(numel) + 1) // 2) * 16
+
+    def bind(self, seg):
+        seg.p, seg.p_lo = self.current.data_ptr(), _ptr(self.target)
+        seg.m = seg.v = seg.m_scale = seg.v_scale = None
+        seg.p_dtype, seg.mv_dtype = _hip.DT_PACKED, _hip.DT_BF16
+
+    def _column(self, role):
+        if role == "p":
+            return self.current.view(torch.float32)[:, 0:2]
+        k = 4 if role == "m" else 6
+        return self.current.view(torch.bfloat16)[:, k:k + 2]
+
+    def moment(self, role):
+        store = BF16Store(self.numel, device=self.device)
+        store.data.copy_(self._column(role).reshape(-1)[: self.numel])
+        return store
+
+    def load(self, master=None, moments=None):
+        if master is not None:
+            self._put("p", _as_master_values(master, self.numel, self.device))
+        for role, store in (moments or {}).items():
+            self._put(role, _bf16_bits(store, self.device))
+
+    def window(self, lo, hi):
+        return {"p": self._column("p").reshape(-1)[lo:hi], "m": self._column("m").reshape(-1)[lo:hi],
+                "v": self._column("v").reshape(-1)[lo:hi]}
+
+
+class LionRecordState(_Interleaved):
+    """Lion, FP32 master, BF16 moment: 768-byte records of 128 elements, the 128 masters then the 128 m
+    values, each in element order (ADAMBRIDGE_DT_PACKED_LION)."""
+
+    layout = "lion-records"
+    precision = "bf16"
+
+    def __init__(self, numel, device, double_buffer: bool = False, memory: list[torch.Tensor] | None = None):
+        records = max(1, -(-int(numel) // 128))
+        bufs = [m.view(records, 768) for m in memory] if memory else \
+            [torch.zeros(records, 768, dtype=torch.uint8, device=device) for _ in range(2 if double_buffer else 1)]
+        super().__init__(numel, device, ("m",), bufs)
+
+    @staticmethod
+    def buffer_bytes(numel: int) -> int:
+        return max(1, -(-int(numel) // 128)) * 768
+
+    def bind(self, seg):
+        seg.p, seg.p_lo = self.current.data_ptr(), _ptr(self.target)
+        seg.m = seg.v = seg.m_scale = seg.v_scale = None
+        seg.p_dtype, seg.mv_dtype = _hip.DT_PACKED_LION, _hip.DT_BF16
+
+    def _column(self, role):
+        if role == "p":
+            return self.current[:, :512].view(torch.float32)
+        return self.current[:, 512:].view(torch.bfloat16)
+
+    def moment(self, role):
+        store = BF16Store(self.numel, device=self.device)
+        store.data.copy_(self._column("m").reshape(-1)[: self.numel])
+        return store
+
+    def load(self, master=None, moments=None):
+        if master is not None:
+            self._put("p", _as_master_values(master, self.numel, self.device))
+        if moments and "m" in moments:
+            self._put("m", _bf16_bits(moments["m"], self.device))
+
+    def window(self, lo, hi):
+        return {"p": self._column("p").reshape(-1)[lo:hi], "m": self._column("m").reshape(-1)[lo:hi]}
+
+
+class AdamRecordState(_Interleaved):
+    """AdamW, FP32 master, FP8 moments: one 768-byte record per 128-element block
+    (ADAMBRIDGE_DT_PACKED_FP8) -- lane l's elements 8l .. 8l + 7 keep their masters at 16l (first
+    four) and 256 + 16l (last four), their m codes at 512 + 16l and v codes at 520 + 16l -- plus an
+    FP32 block-scale array per moment.  Updated in place."""
+
+    layout = "fp8-records"
+    precision = "fp8"
+
+    def __init__(self, numel, device, double_buffer: bool = False, memory: list[torch.Tensor] | None = None):
+        self.blocks = F.fp8_blocks(int(numel))
+        rec = memory[0].view(self.blocks, 768) if memory else \
+            torch.zeros(self.blocks, 768, dtype=torch.uint8, device=device)
+        super().__init__(numel, device, ("m", "v"), [rec])   # updated in place: never double-buffered
+        self.scales = {r: torch.ones(self.blocks, dtype=torch.float32, device=device) for r in ("m", "v")}
+
+    @staticmethod
+    def buffer_bytes(numel: int) -> int:
+        return F.fp8_blocks(int(numel)) * 768
+
+    def bind(self, seg):
+        seg.p, seg.p_lo, seg.m, seg.v = self.current.data_ptr(), None, None, None
+        seg.m_scale, seg.v_scale = self.scales["m"].data_ptr(), self.scales["v"].data_ptr()
+        seg.p_dtype, seg.mv_dtype = _hip.DT_PACKED8, _hip.DT_FP8
+
+    def _column(self, role):
+        if role == "p":   # [block, lane, half, j] = element 128 block + 8 lane + 4 half + j
+            return self.current[:, :512].view(torch.float32).view(self.blocks, 2, 16, 4).permute(0, 2, 1, 3)
+        k = 0 if role == "m" else 8
+        return self.current[:, 512:].view(self.blocks, 16, 16)[:, :, k:k + 8]
+
+    def _codes(self, role: str) -> torch.Tensor:
+        return self._column(role).reshape(-1).view(F.FP8_FORMATS[role].dtype)
+
+    def moment(self, role):
+        store = FP8Store(self.numel, role, device=self.device)
+        store.q.copy_(self._codes(role))
+        store.scale.copy_(self.scales[role])
+        return store
+
+    def load(self, master=None, moments=None):
+        if master is not None:
+            self._put("p", _as_master_values(master, self.numel, self.device))
+        for role, store in (moments or {}).items():
+            if not isinstance(store, FP8Store) or store.role != role or store.block != F.FP8_BLOCK:
+                store = FP8Store(self.numel, role, init=store.to_fp32(), device=self.device)
+            self._column(role).copy_(store.q.to(self.device).view(torch.uint8).view(self.blocks, 16, 8))
+            self.scales[role].copy_(store.scale.to(self.device))
+
+    def footprint(self):
+        return 4 * self.numel, self.current.nbytes - 4 * self.numel + sum(s.nbytes for s in self.scales.values())
+
+    def window(self, lo, hi):
+        b0, b1 = lo // 128, -(-hi // 128)
+        out = {"p": self._column("p").reshape(-1)[lo:hi]}
+        for role in ("m", "v"):
+            out[role] = self._column(role)[b0:b1].reshape(-1)
+            out[role + "_scale"] = self.scales[role][b0:b1]
+        return out
+
+
+def _bf16_bits(store: MomentStore, device) -> torch.Tensor:
+    """A moment's values as BF16 (the store's own bits when it is BF16, nearest-even otherwise)."""
+    if isinstance(store, BF16Store):
+        return store.data.to(device)
+    return F.bf16_encode(store.to_fp32().to(device))
+
+
+# -------------------------------------------------------------------- building
+
+_INTERLEAVED = {"pairs": PairState, "lion-records": LionRecordState, "fp8-records": AdamRecordState}
+ARENA_ALIGN = 2 << 20
+
+
+def arena_plan(layout: str, sizes: list[int], double_buffer: bool = False) -> tuple[list[list[int]], int]:
+    """Byte offsets of each state's buffers in one zeroed arena (every buffer 2 MiB-aligned) and the
+    arena's size, for interleaved states of ``sizes`` elements."""
+    cls = _INTERLEAVED[layout]
+    copies = 2 if double_buffer and layout != "fp8-records" else 1
+    offsets, total = [], 0
+    for n in sizes:
+        mine = []
+        for _ in range(copies):
+            mine.append(total)
+            total += -(-cls.buffer_bytes(n) // ARENA_ALIGN) * ARENA_ALIGN
+        offsets.append(mine)
+    return offsets, total
+
+
+def new_states(layout: str, algorithm: str, precision: str, master_precision: str, device,
+               masters: list[torch.Tensor], double_buffer: bool = False,
+               master_params: list[torch.Tensor | None] | None = None) -> list[ParamState]:
+    """Fresh states for several parameters on one device: master from ``masters[i]`` (any dtype;
+    FP24 rounds to nearest) or, in the separate layout, the FP32 parameter ``master_params[i]`` itself;
+    moments zero, FP8 scales one.
+
+    Interleaved states share one arena: a single zeroed allocation, each buffer at a 2 MiB-aligned
+    offset.  On MI355X the 7B bf16-moment step streams 3-5% faster from one arena allocated after
+    the model's weights and gradients than from one allocation per parameter made at that point
+    (20.8-20.9 against 21.4-21.8 ms per launch, five fresh processes each)."""
+    roles = ("m",) if algorithm == "lion" else ("m", "v")
+    if layout == "separate":
+        out: list[ParamState] = []
+        for i, values in enumerate(masters):
+            param = master_params[i] if master_params else None
+            numel = values.numel()
+            if param is not None:
+                master = FP32Store.wrap(param.data.view(-1))
+            else:
+                master = make_master(master_precision, numel, init=values, device=device)
+            moments = {r: make_store(precision, numel, r, device=device) for r in roles}
+            out.append(SeparateState(master, moments, master_is_param=param is not None))
+        return out
+    if layout not in _INTERLEAVED:
+        raise ValueError(f"unknown state layout {layout!r}; expected one of {LAYOUTS}")
+    cls = _INTERLEAVED[layout]
+    sizes = [t.numel() for t in masters]
+    offsets, total = arena_plan(layout, sizes, double_buffer)
+    arena = torch.zeros(total, dtype=torch.uint8, device=device)
+    states = []
+    for n, offs, values in zip(sizes, offsets, masters):
+        memory = [arena[o: o + cls.buffer_bytes(n)] for o in offs]
+        state = cls(n, device, double_buffer, memory=memory)
+        state.load(master=values.detach().reshape(-1).to(device=device, dtype=torch.float32))
+        states.append(state)
+    return states
+
+
+def new_state(layout: str, algorithm: str, precision: str, master_precision: str, numel: int, device,
+              master_values: torch.Tensor | None = None, master_param: torch.Tensor | None = None,
+              double_buffer: bool = False) -> ParamState:
+    """One fresh state (see :func:`new_states`); without ``master_values`` the master starts at zero."""
+    values = master_values if master_values is not None else torch.zeros(numel, dtype=torch.float32, device=device)
+    return new_states(layout, algorithm, precision, master_precision, device, [values], double_buffer,
+                      [master_param])[0]

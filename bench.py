@@ -142,10 +142,8 @@ def gpu_bench(cfg: dict, steps: int, warmup: int, layout: str = "auto", double_b
     kernel_s = sum(durs) / len(durs)
     elems_per_launch = sum(e for _, _, e in log) / len(log)
     achieved = elems_per_launch * bpp / kernel_s / 1e9
-    packed = sum(1 for s in opt._ordered if s.packed is not None)
-    records = cfg["precision"] == "fp8" and packed
-    state_layout = ("FP8 block records" if records else "interleaved, double-buffered" if packed and double_buffer
-                    else "interleaved" if packed else "separate")
+    layouts = sorted({s.state.layout for s in opt._ordered})
+    state_layout = ", ".join(layouts) + (" (double-buffered)" if double_buffer else "")
     stats = dict(params=n, tensors=len(params), wall=wall, launches_per_step=launches_per_step, layout=state_layout,
                  state_bytes=opt.memory_report()["total"],
                  kernel_ms=kernel_s * 1e3, kernel_ms_min=min(durs) * 1e3, kernel_ms_max=max(durs) * 1e3,

@@ -24,7 +24,6 @@ import numpy as np
 import pytest
 import torch
 
-from adambridge_amd.precision import RecordState
 from oracle import oracle as O
 
 ROOT = Path(__file__).resolve().parents[1]
@@ -46,51 +45,16 @@ def _u8(t: torch.Tensor) -> np.ndarray:
 
 
 def snapshot(opt, slot, lo: int, hi: int) -> dict:
-    """The slot's state, gradient and master over elements [lo, hi) as the oracle's arrays."""
+    """The slot's state, gradient and master over elements [lo, hi) as the oracle's arrays, read
+    through the state's own view of its layout (ParamState.window)."""
     a: dict[str, np.ndarray] = {}
-    if isinstance(slot.packed, RecordState):   # FP32 master + FP8 codes in 768-byte block records
-        assert lo % 128 == 0
-        b0, b1 = lo // 128, math.ceil(hi / 128)
-        rec = slot.packed.rec[b0:b1].cpu().numpy()
-        nb = b1 - b0
-        p = np.ascontiguousarray(rec[:, :512]).view(np.uint32).reshape(nb, 2, 16, 4).transpose(0, 2, 1, 3)
-        a["p"] = p.reshape(-1)[: hi - lo].view(np.float32).copy()
-        codes = np.ascontiguousarray(rec[:, 512:]).reshape(nb, 16, 16)
-        a["m"] = codes[:, :, 0:8].reshape(-1).copy()
-        a["v"] = codes[:, :, 8:16].reshape(-1).copy()
-        a["m_scale"] = slot.packed.scales["m"][b0:b1].cpu().numpy().copy()
-        a["v_scale"] = slot.packed.scales["v"][b0:b1].cpu().numpy().copy()
-    elif slot.packed is not None:   # interleaved FP32 master + BF16 moments, 16 bytes per pair
-        assert lo % 2 == 0
-        rows = slot.packed.current[lo // 2: (hi + 1) // 2].cpu().numpy().view(np.uint32)
-        p = np.empty(2 * rows.shape[0], np.uint32)
-        p[0::2], p[1::2] = rows[:, 0], rows[:, 1]
-        m = np.empty_like(p)
-        m[0::2], m[1::2] = rows[:, 2] & 0xFFFF, rows[:, 2] >> 16
-        v = np.empty_like(p)
-        v[0::2], v[1::2] = rows[:, 3] & 0xFFFF, rows[:, 3] >> 16
-        n = hi - lo
-        a["p"] = p[:n].view(np.float32).copy()
-        a["m"] = m[:n].astype(np.uint16)
-        a["v"] = v[:n].astype(np.uint16)
-    else:
-        master = slot.master
-        if master.precision == "fp24":
-            a["p"], a["p_lo"] = _u16(master.hi[lo:hi]), _u8(master.lo[lo:hi])
+    for key, t in slot.state.window(lo, hi).items():
+        if t.dtype == torch.float32:
+            a[key] = t.detach().contiguous().cpu().numpy().copy()
+        elif t.element_size() == 2:
+            a[key] = _u16(t)
         else:
-            a["p"] = master.data[lo:hi].detach().cpu().numpy().copy()
-        for key, store in (("m", slot.m), ("v", slot.v)):
-            if store is None:
-                continue
-            if store.precision == "fp8":
-                assert lo % 128 == 0
-                b0, b1 = lo // 128, math.ceil(hi / 128)
-                a[key] = _u8(store.q[b0 * 128: b1 * 128])
-                a[key + "_scale"] = store.scale[b0:b1].cpu().numpy().copy()
-            elif store.precision == "bf16":
-                a[key] = _u16(store.data[lo:hi])
-            else:
-                a[key] = store.data[lo:hi].detach().cpu().numpy().copy()
+            a[key] = _u8(t)
     g = slot.param.grad.reshape(-1)[lo:hi]
     a["g"] = _u16(g) if g.dtype == torch.bfloat16 else g.float().cpu().numpy()
     a["out"] = np.zeros(hi - lo, np.uint16)
@@ -117,7 +81,7 @@ def run_config(name: str, warm: int = 2, tensors: int = 6, cfg: dict | None = No
             opt.step()
         torch.cuda.synchronize()
         if layout == "separate":
-            assert all(s.packed is None for s in opt._ordered)
+            assert all(s.state.layout == "separate" for s in opt._ordered)
         lion = cfg["algo"] == "lion"
         mv = {"fp32": O.DT_F32, "bf16": O.DT_BF16, "fp8": O.DT_FP8}[cfg["precision"]]
         # the largest tensors (first, middle, last windows) and the first window of every tensor
@@ -152,7 +116,7 @@ def run_config(name: str, warm: int = 2, tensors: int = 6, cfg: dict | None = No
                         f"{name}: parameter {slot.index} elements [{lo}, {hi}): {key} differs"
         # every element: working weight == bf16 RNE of the stored master
         for slot in opt._ordered:
-            master = slot.master.to_fp32() if slot.packed is None else slot.packed.get("p")
+            master = slot.state.master_fp32()
             assert torch.equal(slot.param.detach().reshape(-1), master.to(torch.bfloat16)), \
                 f"{name}: parameter {slot.index}: bf16 weight != RNE(master)"
     finally:

@@ -218,40 +218,76 @@ def test_store_from_state_dict_rejects_bad_stores():
 
 @pytest.mark.parametrize("n", [1, 127, 128, 300, 4096 + 77])
 def test_fp8_records_layout_offsets_and_views(n):
-    """RecordState puts element 128b + 8l + j's master at byte 16l + 4j (j < 4) or 256 + 16l + 4(j - 4)
+    """AdamRecordState puts element 128b + 8l + j's master at byte 16l + 4j (j < 4) or 256 + 16l + 4(j - 4)
     of record b, its m code at 512 + 16l + j and its v code at 520 + 16l + j (the kernel's
-    ADAMBRIDGE_DT_PACKED_FP8 layout); the master and moment views read back what was stored, and
-    the record-backed FP8 moment decodes like a separate FP8Store with the same codes and scales."""
+    ADAMBRIDGE_DT_PACKED_FP8 layout); loading takes codes as they are, and the moments read back as
+    separate FP8Stores with the same codes and scales."""
+    from adambridge_amd.state import AdamRecordState
     rng = np.random.default_rng(n)
     master = rng.normal(0, 0.02, n).astype(np.float32)
     nb = -(-n // 128)
-    mq = rng.integers(0, 256, nb * 128, dtype=np.uint8)
-    vq = rng.integers(0, 0x7c, nb * 128, dtype=np.uint8)   # finite E5M2 codes
-    rs = P.RecordState(n, init=torch.from_numpy(master))
-    rs.set_codes("m", torch.from_numpy(mq).view(torch.float8_e4m3fn))
-    rs.set_codes("v", torch.from_numpy(vq).view(torch.float8_e5m2))
-    rec = rs.rec.numpy()
+    codes = {"m": rng.integers(0, 256, nb * 128, dtype=np.uint8),
+             "v": rng.integers(0, 0x7c, nb * 128, dtype=np.uint8)}   # finite E5M2 codes
+    scale = torch.from_numpy(rng.uniform(1e-6, 1e-3, nb).astype(np.float32))
+    separate = {}
+    for role, q in codes.items():
+        st = P.FP8Store(n, role)
+        st.q.copy_(torch.from_numpy(q).view(st.q.dtype))
+        st.scale.copy_(scale)
+        separate[role] = st
+    rs = AdamRecordState(n, "cpu")
+    rs.load(master=torch.from_numpy(master), moments=separate)
+    rec = rs.current.numpy()
     for e in list(range(min(n, 40))) + list(rng.integers(0, n, 40)):
         b, l, j = e // 128, (e % 128) // 8, e % 8
         off = 16 * l + 4 * j if j < 4 else 256 + 16 * l + 4 * (j - 4)
         assert rec[b, off:off + 4].view(np.float32)[0] == master[e]
-        assert rec[b, 512 + 16 * l + j] == mq[e] and rec[b, 520 + 16 * l + j] == vq[e]
-    assert np.array_equal(rs.get("p").numpy(), master)
-    assert np.array_equal(rs.codes("m").view(torch.uint8).numpy(), mq)
-    assert np.array_equal(rs.codes("v").view(torch.uint8).numpy(), vq)
-    scale = torch.from_numpy(rng.uniform(1e-6, 1e-3, nb).astype(np.float32))
-    for role, q in (("m", mq), ("v", vq)):
-        mom = P.RecordMoment(rs, role)
-        mom.scale.copy_(scale)
-        sep = P.FP8Store(n, role)
-        sep.q.copy_(torch.from_numpy(q).view(sep.q.dtype))
-        sep.scale.copy_(scale)
+        assert rec[b, 512 + 16 * l + j] == codes["m"][e] and rec[b, 520 + 16 * l + j] == codes["v"][e]
+    assert np.array_equal(rs.master_fp32().numpy(), master)
+    for role, sep in separate.items():
+        mom = rs.moment(role)
+        assert np.array_equal(mom.q.view(torch.uint8).numpy(), codes[role])
         assert torch.equal(mom.to_fp32().view(torch.int32), sep.to_fp32().view(torch.int32))   # NaN codes too
         sd = mom.state_dict()
-        assert sd["precision"] == "fp8" and sd["role"] == role and torch.equal(sd["q"].view(torch.uint8), sep.q.view(torch.uint8))
-    assert P.RecordMaster(rs).nbytes == 4 * n and P.RecordMoment(rs, "v").nbytes == nb * (128 + 4)
-    assert P.RecordMaster(rs).nbytes + P.RecordMoment(rs, "m").nbytes + P.RecordMoment(rs, "v").nbytes == \
-        rs.nbytes == nb * (768 + 8)
+        assert sd["precision"] == "fp8" and sd["role"] == role and torch.equal(sd["scale"], scale)
+    window = rs.window(128 * (nb - 1), n)
+    assert np.array_equal(window["m"].numpy(), codes["m"][128 * (nb - 1):])
+    assert rs.footprint() == (4 * n, nb * (768 + 8) - 4 * n)
+
+
+@pytest.mark.parametrize("n", [1, 2, 127, 128, 301])
+def test_lion_and_pair_layout_offsets(n):
+    """LionRecordState: element 128r + i (i < 128) keeps its master at byte 4i of record r and its m
+    bits at 512 + 2i (ADAMBRIDGE_DT_PACKED_LION).  PairState: elements 2k, 2k + 1 at words 0, 1 of
+    row k, their m and v bits in the halves of words 2 and 3 (ADAMBRIDGE_DT_PACKED)."""
+    from adambridge_amd.state import LionRecordState, PairState
+    rng = np.random.default_rng(n + 7)
+    master = rng.normal(0, 0.02, n).astype(np.float32)
+    m = rng.integers(0, 0x7f00, n).astype(np.int16)
+    v = rng.integers(0, 0x7f00, n).astype(np.int16)
+    stores = {}
+    for role, bits in (("m", m), ("v", v)):
+        st = P.BF16Store(n)
+        st.data.copy_(torch.from_numpy(bits).view(torch.bfloat16))
+        stores[role] = st
+    lion = LionRecordState(n, "cpu")
+    lion.load(master=torch.from_numpy(master), moments={"m": stores["m"]})
+    rec = lion.current.numpy()
+    for e in range(n):
+        r, i = divmod(e, 128)
+        assert rec[r, 4 * i:4 * i + 4].view(np.float32)[0] == master[e]
+        assert rec[r, 512 + 2 * i:514 + 2 * i].view(np.int16)[0] == m[e]
+    assert np.array_equal(lion.moment("m").data.view(torch.int16).numpy(), m)
+    pairs = PairState(n, "cpu", double_buffer=True)
+    pairs.load(master=torch.from_numpy(master), moments=stores)
+    rows = pairs.current.numpy().view(np.uint32)
+    for e in range(n):
+        k, h = divmod(e, 2)
+        assert rows[k, h] == master[e:e + 1].view(np.uint32)[0]
+        assert (rows[k, 2] >> (16 * h)) & 0xFFFF == np.uint16(m[e]) and (rows[k, 3] >> (16 * h)) & 0xFFFF == np.uint16(v[e])
+    assert np.array_equal(pairs.master_fp32().numpy(), master)
+    pairs.advance()   # double-buffered: the other buffer is current now
+    assert pairs.current.data_ptr() != pairs.buffers[0].data_ptr() and pairs.target is pairs.buffers[0]
 
 
 def test_fp24_master_store_round_trip():

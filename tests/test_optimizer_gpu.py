@@ -227,7 +227,7 @@ def test_delayed_updates_state_dict_close_and_unused_params():
     opt.step_sync()
     torch.cuda.synchronize()
     assert not torch.equal(head, before)
-    assert torch.equal(head.detach().reshape(-1), opt._slots[head].master.to_fp32())
+    assert torch.equal(head.detach().reshape(-1), opt._slots[head].state.master_fp32())
     head.requires_grad_(True)
     lm_loss(model, 4).backward()
     opt.step_sync()
@@ -724,11 +724,11 @@ def test_api_updates_are_bit_exact_against_the_oracle(precision, master, lion, h
         assert np.array_equal(m_data.view(torch.uint8).numpy().view(want_m.dtype).reshape(want_m.shape), want_m), \
             f"param {k} m"
         if master == "fp24":
-            hi, lo = slot.master.native_buffers
+            hi, lo = slot.state.master.native_buffers
             assert np.array_equal(hi.cpu().view(torch.int16).numpy().view(np.uint16), c.arrays["p"])
             assert np.array_equal(lo.cpu().numpy(), c.arrays["p_lo"])
         else:
-            assert np.array_equal(slot.master.data.cpu().numpy().view(np.uint32), c.arrays["p"].view(np.uint32))
+            assert np.array_equal(slot.state.master_fp32().cpu().numpy().view(np.uint32), c.arrays["p"].view(np.uint32))
     opt.close()
 
 
@@ -762,7 +762,7 @@ def test_back_to_back_table_launches_reuse_staging_slots(precision):
         assert slot.step == 24
         got_p = p.detach().reshape(-1).cpu().view(torch.int16).numpy().view(np.uint16)
         assert np.array_equal(got_p, c.arrays["out"]), f"param {k} weights"
-        assert np.array_equal(slot.master.data.cpu().numpy().view(np.uint32), c.arrays["p"].view(np.uint32))
+        assert np.array_equal(slot.state.master_fp32().cpu().numpy().view(np.uint32), c.arrays["p"].view(np.uint32))
         m_data = (slot.m.q if hasattr(slot.m, "q") else slot.m.data).detach().cpu()
         assert np.array_equal(m_data.view(torch.uint8).numpy().view(c.arrays["m"].dtype).reshape(-1),
                               c.arrays["m"].reshape(-1)), f"param {k} m"
@@ -795,7 +795,7 @@ def test_state_layouts_give_identical_bytes(hooks, precision):
         opt = ab.AdamBridge(model.parameters(), lr=3e-3, precision=precision, small_param_threshold=2000, **kw)
         if hooks:
             opt.attach_hooks(model)
-        assert any(s.packed is not None for s in opt._ordered) or "state_layout" in kw or not opt._ordered[0].initialized
+        assert any(s.initialized and s.state.layout != "separate" for s in opt._ordered) or "state_layout" in kw or not opt._ordered[0].initialized
         for step in range(4):
             lm_loss(model, step).backward()
             if hooks:
@@ -804,7 +804,7 @@ def test_state_layouts_give_identical_bytes(hooks, precision):
                 opt.step()
                 opt.zero_grad()
         if "state_layout" not in kw:
-            assert all(s.packed is not None for s in opt._ordered)
+            assert all(s.state.layout != "separate" for s in opt._ordered)
         codes = ([s.m.q.view(torch.uint8) for s in opt._ordered] + [s.v.q.view(torch.uint8) for s in opt._ordered]
                  + [s.m.scale.clone() for s in opt._ordered] + [s.v.scale.clone() for s in opt._ordered]
                  if precision == "fp8" else [])
@@ -850,11 +850,11 @@ def test_packed_state_checkpoint_and_set_precision(precision):
         other.close()
     m_before = [s.m.to_fp32() for s in opt._ordered]
     opt.set_precision("fp32")
-    assert all(s.packed is None for s in opt._ordered)
+    assert all(s.state.layout == "separate" for s in opt._ordered)
     for s, m in zip(opt._ordered, m_before):
         assert torch.equal(s.m.to_fp32(), m)
     opt.set_precision(precision)
-    assert all(s.packed is not None for s in opt._ordered)
+    assert all(s.state.layout != "separate" for s in opt._ordered)
     from adambridge_amd import precision as P
     for s, m in zip(opt._ordered, m_before):
         assert torch.equal(s.m.to_fp32(), P.make_store(precision, s.numel, "m", init=m, device=DEV).to_fp32())
