@@ -37,6 +37,8 @@ import weakref
 from typing import Any, Callable, Iterable
 
 import torch
+import torch._dynamo  # noqa: F401 -- imported here, not by the first torch.compiler.disable() call: that import
+#                       keeps the frames on the stack alive, which would pin the optimizer being built
 
 from .engine import ParamSlot, SmallGroup, StepStats, UpdateEngine
 from .precision import (_checked, bytes_per_param, canonical_master_precision, canonical_precision,
@@ -151,11 +153,21 @@ class _StepWindow:
 
 
 class _HookSet:
-    """Post-accumulate-grad hooks calling one function, kept opaque to TorchDynamo so that compiled
-    autograd calls it instead of tracing the launches inside (optimizer.py:271-274)."""
+    """Post-accumulate-grad hooks calling one method of the optimizer, kept opaque to TorchDynamo so
+    that compiled autograd calls it instead of tracing the launches inside (optimizer.py:271-274).
+    The hooks reach the optimizer through a weak reference: parameters (which hold their hooks) and
+    the optimizer's own attributes then form no cycle, and dropping the last reference to the
+    optimizer frees its device state at once, without waiting for the garbage collector."""
 
-    def __init__(self, fn: Callable[[torch.Tensor], None]):
-        self._fn = torch.compiler.disable(fn)
+    def __init__(self, method: Callable[[torch.Tensor], None]):
+        target = weakref.WeakMethod(method)
+
+        def on_grad_ready(p: torch.Tensor) -> None:
+            bound = target()
+            if bound is not None:
+                bound(p)
+
+        self._fn = torch.compiler.disable(on_grad_ready)
         self._handles: list = []
         self.active = False
 

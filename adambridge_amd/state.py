@@ -19,7 +19,7 @@ layout          serves                                 bytes of state per elemen
 separate        anything (the reference's arrays)      master 4 (FP24: 3) + moments
 pairs           AdamW, FP32 master, BF16 moments       16 per 2 elements (x2 double-buffered)
 fp8-records     AdamW, FP32 master, FP8 moments        768 per 128 + two FP32 scales per 128
-lion-records    Lion, FP32 master, BF16 moment         768 per 128 (x2 double-buffered)
+lion-records    Lion, FP32 master, BF16 moment         1536 per 256 (x2 double-buffered)
 ==============  =====================================  ======================================
 
 The interleaved layouts turn the master and moment streams into one stream of
@@ -296,21 +296,21 @@ class PairState(_Interleaved):
 
 
 class LionRecordState(_Interleaved):
-    """Lion, FP32 master, BF16 moment: 768-byte records of 128 elements, the 128 masters then the 128 m
+    """Lion, FP32 master, BF16 moment: 1536-byte records of 256 elements, the 256 masters then the 256 m
     values, each in element order (ADAMBRIDGE_DT_PACKED_LION)."""
 
     layout = "lion-records"
     precision = "bf16"
 
     def __init__(self, numel, device, double_buffer: bool = False, memory: list[torch.Tensor] | None = None):
-        records = max(1, -(-int(numel) // 128))
-        bufs = [m.view(records, 768) for m in memory] if memory else \
-            [torch.zeros(records, 768, dtype=torch.uint8, device=device) for _ in range(2 if double_buffer else 1)]
+        records = max(1, -(-int(numel) // 256))
+        bufs = [m.view(records, 1536) for m in memory] if memory else \
+            [torch.zeros(records, 1536, dtype=torch.uint8, device=device) for _ in range(2 if double_buffer else 1)]
         super().__init__(numel, device, ("m",), bufs)
 
     @staticmethod
     def buffer_bytes(numel: int) -> int:
-        return max(1, -(-int(numel) // 128)) * 768
+        return max(1, -(-int(numel) // 256)) * 1536
 
     def bind(self, seg):
         seg.p, seg.p_lo = self.current.data_ptr(), _ptr(self.target)
@@ -319,8 +319,8 @@ class LionRecordState(_Interleaved):
 
     def _column(self, role):
         if role == "p":
-            return self.current[:, :512].view(torch.float32)
-        return self.current[:, 512:].view(torch.bfloat16)
+            return self.current[:, :1024].view(torch.float32)
+        return self.current[:, 1024:].view(torch.bfloat16)
 
     def moment(self, role):
         store = BF16Store(self.numel, device=self.device)

@@ -72,17 +72,20 @@ def llama7b() -> list[tuple[str, tuple]]:
 
 CONFIGS = {
     "c1": dict(desc="AdamW, FP32 moments, one flat tensor of 16,777,216 params", shapes=lambda: [("flat", (1 << 24,))],
-               algo="adamw", precision="fp32", lr=1e-4, betas=(0.9, 0.999), wd=0.01, gscale=(1e-3, 1e-3)),
+               algo="adamw", precision="fp32", lr=1e-4, betas=(0.9, 0.999), wd=0.01, gscale=(1e-3, 1e-3),
+               warm_steps=5),
     "c2": dict(desc="AdamW, bf16 moments, Qwen2.5-0.5B parameter list",
                shapes=lambda: qwen_like(151936, 896, 4864, 24, 128),
-               algo="adamw", precision="bf16", lr=2e-5, betas=(0.9, 0.999), wd=0.01, gscale=(1e-5, 1e-2)),
+               algo="adamw", precision="bf16", lr=2e-5, betas=(0.9, 0.999), wd=0.01, gscale=(1e-5, 1e-2),
+               warm_steps=10),
     "c3": dict(desc="AdamW, FP8 moments, Llama-7B parameter list", shapes=llama7b,
                algo="adamw", precision="fp8", lr=1e-5, betas=(0.9, 0.999), wd=0.01, gscale=(1e-5, 1e-2)),
     "c3p": dict(desc="AdamW, bf16 moments, Llama-7B parameter list", shapes=llama7b,
                 algo="adamw", precision="bf16", lr=1e-5, betas=(0.9, 0.999), wd=0.01, gscale=(1e-5, 1e-2)),
     "c4": dict(desc="Lion, bf16 moment, Qwen2.5-1.5B parameter list",
                shapes=lambda: qwen_like(151936, 1536, 8960, 28, 256),
-               algo="lion", precision="bf16", lr=3e-6, betas=(0.9, 0.99), wd=0.1, gscale=(1e-6, 1e-2)),
+               algo="lion", precision="bf16", lr=3e-6, betas=(0.9, 0.99), wd=0.1, gscale=(1e-6, 1e-2),
+               grads="elementwise", zeros=0.01),
 }
 
 
@@ -99,22 +102,42 @@ def build(cfg: dict, device, seed: int = 0, layout: str = "auto", double_buffer:
     import torch
     import adambridge_amd as ab
 
+    # Allocated in the order a training job allocates them: every weight when the model is built, the
+    # gradients during the first backward pass (last layer first), the optimizer state at the first
+    # step.  (Allocating each weight next to its gradient instead puts the 7B bf16-moment step at
+    # 20.9-21.5 ms per launch, against 20.7-20.8 in this order.)
     gen = torch.Generator(device=device).manual_seed(seed)
-    lo, hi = cfg["gscale"]
-    params, grads = [], []
-    for k, (_, shape) in enumerate(cfg["shapes"]()):
-        p = torch.nn.Parameter(torch.randn(shape, generator=gen, device=device, dtype=torch.bfloat16).mul_(0.02))
-        u = (k * 0.6180339887) % 1.0
-        scale = math.exp(math.log(lo) + u * (math.log(hi) - math.log(lo)))
-        g = torch.randn(shape, generator=gen, device=device, dtype=torch.bfloat16).mul_(scale)
-        params.append(p)
-        grads.append(g)
+    shapes = [shape for _, shape in cfg["shapes"]()]
+    params = [torch.nn.Parameter(torch.randn(shape, generator=gen, device=device, dtype=torch.bfloat16).mul_(0.02))
+              for shape in shapes]
+    grads = [None] * len(shapes)
+    for k in reversed(range(len(shapes))):
+        grads[k] = synthetic_grad(cfg, k, shapes[k], gen, device)
     kw = dict(lr=cfg["lr"], betas=cfg["betas"], weight_decay=cfg["wd"], precision=cfg["precision"],
               state_layout=layout, double_buffer=double_buffer)
     opt = ab.LionBridge(params, **kw) if cfg["algo"] == "lion" else ab.AdamBridge(params, **kw)
     for p, g in zip(params, grads):
         p.grad = g
     return opt, params
+
+
+def synthetic_grad(cfg: dict, k: int, shape, gen, device):
+    """Tensor k's bf16 gradient.  Default: N(0, 1) times one scale per tensor, log-uniform over
+    cfg['gscale'] (c2, c3).  grads='elementwise' (c4): every element's magnitude log-uniform over
+    cfg['gscale'], a random sign, and exact zeros at density cfg['zeros'] (sign(0) = 0 in Lion)."""
+    import torch
+
+    lo, hi = cfg["gscale"]
+    if cfg.get("grads") == "elementwise":
+        u = torch.rand(shape, generator=gen, device=device)
+        g = torch.exp(u.mul_(math.log(hi) - math.log(lo)).add_(math.log(lo)))
+        sign = torch.rand(shape, generator=gen, device=device) < 0.5
+        g = torch.where(sign, -g, g)
+        g[torch.rand(shape, generator=gen, device=device) < cfg.get("zeros", 0.0)] = 0.0
+        return g.to(torch.bfloat16)
+    u = (k * 0.6180339887) % 1.0
+    scale = math.exp(math.log(lo) + u * (math.log(hi) - math.log(lo)))
+    return torch.randn(shape, generator=gen, device=device, dtype=torch.bfloat16).mul_(scale)
 
 
 def gpu_bench(cfg: dict, steps: int, warmup: int, layout: str = "auto", double_buffer: bool = False) -> dict:
@@ -137,6 +160,10 @@ def gpu_bench(cfg: dict, steps: int, warmup: int, layout: str = "auto", double_b
     wall = time.perf_counter() - t0
     opt._engine.launch_log = None
     durs = [a.elapsed_time(b) / 1e3 for a, b, _ in log]
+    if os.environ.get("ADAMBRIDGE_BENCH_TRACE"):   # diagnostic: launch durations in order, 10 per line
+        for k in range(0, len(durs), 10):
+            print(f"[bench] launches {k}..: " + " ".join(f"{d * 1e3:.2f}" for d in durs[k:k + 10]), file=sys.stderr,
+                  flush=True)
     launches_per_step = len(log) / steps
     bpp = min_bytes(cfg["precision"], cfg["algo"])
     kernel_s = sum(durs) / len(durs)
@@ -281,11 +308,51 @@ def pipeline_bench(steps: int, warmup: int) -> dict:
 
 # ----------------------------------------------------------------- CPU side
 
+def host_cpus() -> dict:
+    """The CPUs this process may run on: logical count, physical cores among them, model and the
+    widest x86 vector ISA (from /proc/cpuinfo)."""
+    try:
+        allowed = sorted(os.sched_getaffinity(0))
+    except AttributeError:
+        allowed = list(range(os.cpu_count() or 1))
+    cores, model, flags = set(), "unknown", set()
+    try:
+        proc = None
+        phys = core = None
+        for line in Path("/proc/cpuinfo").read_text().splitlines() + [""]:
+            key, _, val = line.partition(":")
+            key, val = key.strip(), val.strip()
+            if key == "processor":
+                proc = int(val)
+            elif key == "physical id":
+                phys = val
+            elif key == "core id":
+                core = val
+            elif key == "model name":
+                model = val
+            elif key == "flags":
+                flags = set(val.split())
+            elif not line and proc is not None:
+                if proc in allowed:
+                    cores.add((phys, core) if core is not None else proc)
+                proc = phys = core = None
+    except OSError:
+        pass
+    isa = "avx512" if "avx512f" in flags else "avx2" if "avx2" in flags else "sse"
+    return dict(logical=len(allowed), physical=len(cores) or len(allowed), model=model, isa=isa)
+
+
+# The GPU box gives a one-GPU job a share of 16 CPUs, whatever the machine has in all.
+CPU_SHARE = 16
+
+
 def cpu_bench(cfg: dict, budget_params: int, steps: int) -> dict:
     """The reference's native kernel (oracle/_ref, compiled from its C source) over the first tensors
-    of the same list, up to ``budget_params`` parameters, on this host's CPU share.  Where that
-    library was not built (no reference tree at build time), the oracle's C restatement of the same
-    algorithm (oracle/liboracle.so, OpenMP) is timed instead and reported as kind "port"."""
+    of the same list, up to ``budget_params`` parameters, timed at the reference's default thread
+    count -- min(32, 2/3 of the CPUs, engine.py:635), the CPUs being this job's share of the host --
+    and on every physical core of that share.  Where the reference library was not built (no
+    reference tree at build time), the oracle's C restatement of the same algorithm
+    (oracle/liboracle.so, OpenMP) is timed instead, kind "port"."""
     import ctypes
 
     import numpy as np
@@ -293,11 +360,9 @@ def cpu_bench(cfg: dict, budget_params: int, steps: int) -> dict:
 
     use_ref = O.reference_available()
     lib = O.load_reference() if use_ref else O.load_oracle()
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:
-        cores = os.cpu_count() or 1
-    threads = max(1, min(16, cores))
+    host = host_cpus()
+    share = max(1, min(CPU_SHARE, host["logical"]))
+    plans = {"default": max(1, min(32, (2 * share) // 3)), "all_cores": max(1, min(share, host["physical"]))}
     shapes, total = [], 0
     for name, shape in cfg["shapes"]():
         numel = math.prod(shape)
@@ -324,48 +389,55 @@ def cpu_bench(cfg: dict, budget_params: int, steps: int) -> dict:
         else:
             dt = np.float32 if mv_dt == O.DT_F32 else np.uint16
             m, v, ms, vs = np.zeros(numel, dt), np.zeros(numel, dt), None, None
-        arrs = dict(p=p, g=g, m=m, v=None if lion else v, m_scale=ms, v_scale=None if lion else vs, out=out)
-        keep.append(arrs)
-        seg = O.Segment(p=p.ctypes.data, g=g.ctypes.data, m=m.ctypes.data,
-                        v=None if lion else v.ctypes.data, m_scale=None if ms is None else ms.ctypes.data,
-                        v_scale=None if (lion or vs is None) else vs.ctypes.data, out=out.ctypes.data,
-                        group=ctypes.pointer(group), n=numel, step=1, index=k, offset=0, g_dtype=O.DT_BF16,
-                        mv_dtype=mv_dt, out_dtype=O.DT_BF16, algorithm=1 if lion else 0, p_dtype=O.DT_F32)
-        segs.append(seg)
+        keep.append(dict(p=p, g=g, m=m, v=None if lion else v, m_scale=ms, v_scale=None if lion else vs, out=out))
+        segs.append(O.Segment(p=p.ctypes.data, g=g.ctypes.data, m=m.ctypes.data,
+                              v=None if lion else v.ctypes.data, m_scale=None if ms is None else ms.ctypes.data,
+                              v_scale=None if (lion or vs is None) else vs.ctypes.data, out=out.ctypes.data,
+                              group=ctypes.pointer(group), n=numel, step=1, index=k, offset=0, g_dtype=O.DT_BF16,
+                              mv_dtype=mv_dt, out_dtype=O.DT_BF16, algorithm=1 if lion else 0, p_dtype=O.DT_F32))
     arr = (ctypes.POINTER(O.Segment) * len(segs))(*[ctypes.pointer(s) for s in segs])
+    bpp = min_bytes(cfg["precision"], cfg["algo"])
+    level = None
     if use_ref:
         lib.adambridge_set_simd_level(-1)
         level = lib.adambridge_simd_level()
-        pool = lib.adambridge_pool_create(threads, None, 0)
-        run = lambda: lib.adambridge_multi_step(pool, arr, len(segs), threads)  # noqa: E731
-        what = f"reference native kernel (oracle/_ref, compiled from adambridge_kernels.c, SIMD level {level})"
-    else:
-        pool = None
-        run = lambda: lib.abo_multi_step(arr, len(segs), 16, threads)  # noqa: E731
-        what = "oracle C restatement of the reference kernel (oracle/liboracle.so, scalar C, OpenMP)"
-    try:
-        def one(step):
-            for s in segs:
-                s.step = step
-            rc = run()
-            if rc:
-                raise RuntimeError(f"CPU multi_step returned {rc}")
-        one(1)
-        times = []
-        for k in range(steps):
-            t0 = time.perf_counter()
-            one(k + 2)
-            times.append(time.perf_counter() - t0)
-    finally:
-        if pool:
-            lib.adambridge_pool_destroy(pool)
-    times.sort()
-    med = times[len(times) // 2]
-    bpp = min_bytes(cfg["precision"], cfg["algo"])
-    return dict(value=total / med, unit="params/s", cores=threads, kind="reference" if use_ref else "port",
-                sample=(f"{what} on the first {len(shapes)} tensors of the same list ({total:,} params), "
-                        f"median of {steps} steps after 1 warm-up, {threads} threads"),
-                ms_per_step=med * 1e3, gbs=total * bpp / med / 1e9)
+    runs = {}
+    step = 1
+    for plan, threads in plans.items():
+        pool = lib.adambridge_pool_create(threads, None, 0) if use_ref else None
+        try:
+            def one():
+                nonlocal step
+                for seg in segs:
+                    seg.step = step
+                step += 1
+                rc = (lib.adambridge_multi_step(pool, arr, len(segs), threads) if use_ref
+                      else lib.abo_multi_step(arr, len(segs), 16, threads))
+                if rc:
+                    raise RuntimeError(f"CPU multi_step returned {rc}")
+            one()   # warm-up (bench_kernels.py:30-37)
+            times = []
+            for _ in range(steps):
+                t0 = time.perf_counter()
+                one()
+                times.append(time.perf_counter() - t0)
+        finally:
+            if pool:
+                lib.adambridge_pool_destroy(pool)
+        med = sorted(times)[len(times) // 2]
+        runs[plan] = dict(threads=threads, value=total / med, ms_per_step=med * 1e3, gbs=total * bpp / med / 1e9)
+    what = (f"reference native kernel (oracle/_ref, compiled from adambridge_kernels.c, SIMD level {level})"
+            if use_ref else "oracle C restatement of the reference kernel (oracle/liboracle.so, scalar C, OpenMP)")
+    d = runs["default"]
+    return dict(value=d["value"], unit="params/s", cores=d["threads"], kind="reference" if use_ref else "port",
+                sample=(f"{what} on the first {len(shapes)} tensors of the same list ({total:,} params), median of "
+                        f"{steps} steps after 1 warm-up, at the reference's default thread count "
+                        f"min(32, 2/3 x {share} CPUs) = {d['threads']} and on all {runs['all_cores']['threads']} "
+                        f"physical cores of this job's {share}-CPU share"),
+                ms_per_step=d["ms_per_step"], gbs=d["gbs"],
+                all_cores=runs["all_cores"],
+                host=dict(model=host["model"], logical_cpus=host["logical"], physical_cores=host["physical"],
+                          cpu_share=share, isa=host["isa"], reference_simd_level=level))
 
 
 # --------------------------------------------------------------------- main
@@ -416,7 +488,8 @@ def main() -> int:
               flush=True)
     cpu = None if args.no_cpu else cpu_bench(cfg, args.cpu_params, args.cpu_steps)
     if cpu is not None:
-        print(f"[bench] CPU reference: {cpu['ms_per_step']:.1f} ms/step on {cpu['cores']} threads",
+        print(f"[bench] CPU reference: {cpu['ms_per_step']:.1f} ms/step on {cpu['cores']} threads, "
+              f"{cpu['all_cores']['ms_per_step']:.1f} ms/step on {cpu['all_cores']['threads']} ({cpu['host']})",
               file=sys.stderr, flush=True)
     ms_per_step = g["wall"] / args.steps * 1e3
     line = {
@@ -442,7 +515,8 @@ def main() -> int:
                      "frac": g["achieved_gbs"] / HBM_PEAK_GBS,
                      "traffic": args.traffic if args.traffic is not None else MEASURED_TRAFFIC.get(args.config),
                      "kernel_ms": g["kernel_ms"]},
-        "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
+        "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample",
+                                                                      "ms_per_step", "gbs", "all_cores", "host")},
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -60,13 +60,13 @@ enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, AD
  * separate FP8 layout. */
 
 /* ADAMBRIDGE_DT_PACKED_LION (p_dtype; no counterpart in the reference): an HBM layout for
- * Lion with an FP32 master and a BF16 moment (mv_dtype DT_BF16).  p points at one 768-byte
- * record per 128 elements, ceil(n/128) records, 16-byte aligned.  In the record of elements
- * 128r .. 128r + 127, for l = 0 .. 63, elements 128r + 2l and 128r + 2l + 1 keep their FP32
- * masters at bytes 8l and 8l + 4 and their m values (BF16 bits) at 512 + 4l and 512 + 4l + 2.
- * Slots past n are padding, written back unchanged.  p_lo is NULL (update in place) or a
- * second buffer of the same layout that receives the new state; m, v and the scales are
- * unused.  Same arithmetic, rounding and rounding stream as the separate layout. */
+ * Lion with an FP32 master and a BF16 moment (mv_dtype DT_BF16).  p points at one 1536-byte
+ * record per 256 elements, ceil(n/256) records, 16-byte aligned.  The record of elements
+ * 256r .. 256r + 255 holds their 256 FP32 masters in element order (bytes 0 .. 1023), then their
+ * 256 m values as BF16 bits in element order (bytes 1024 .. 1535).  Slots past n are padding,
+ * written back unchanged.  p_lo is NULL (update in place) or a second buffer of the same layout
+ * that receives the new state; m, v and the scales are unused.  Same arithmetic, rounding and
+ * rounding stream as the separate layout. */
 enum { ADAMBRIDGE_ALGO_ADAMW = 0, ADAMBRIDGE_ALGO_LION = 1 };
 
 /* Error codes (kernels.c:1537-1553, 1582-1584, 1620-1621), plus the HIP-side ones. */

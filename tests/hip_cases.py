@@ -298,19 +298,18 @@ def run_hip_records(cases: list[O.Case], width: int = 16, misalign_g: bool = Fal
 
 
 def pack_lion_records(case: O.Case) -> np.ndarray:
-    """Separate FP32 master + BF16 m -> ADAMBRIDGE_DT_PACKED_LION records (records x 768 bytes):
-    per 128 elements, elements 2l and 2l + 1 keep their masters at byte 8l and their m bits at
-    512 + 4l (first element in the low half).  Padding slots are set to a fixed pattern so that
-    a test can see the kernel leave them unchanged."""
+    """Separate FP32 master + BF16 m -> ADAMBRIDGE_DT_PACKED_LION records (records x 1536 bytes): per
+    256 elements, the 256 masters then the 256 m values, each in element order.  Padding slots are
+    set to a fixed pattern so that a test can see the kernel leave them unchanged."""
     n = case.n
-    nr = max(1, -(-n // 128))
-    p = np.full(nr * 128, 0x7FA5A5A5, np.uint32)   # a NaN pattern: any arithmetic on it would show
+    nr = max(1, -(-n // 256))
+    p = np.full(nr * 256, 0x7FA5A5A5, np.uint32)   # a NaN pattern: any arithmetic on it would show
     p[:n] = case.arrays["p"].view(np.uint32)
-    m = np.full(nr * 128, 0xA5A5, np.uint16)
+    m = np.full(nr * 256, 0xA5A5, np.uint16)
     m[:n] = case.arrays["m"]
-    rec = np.zeros((nr, 768), np.uint8)
-    rec[:, :512] = p.reshape(nr, 128).view(np.uint8)
-    rec[:, 512:] = m.reshape(nr, 128).view(np.uint8)
+    rec = np.zeros((nr, 1536), np.uint8)
+    rec[:, :1024] = p.reshape(nr, 256).view(np.uint8)
+    rec[:, 1024:] = m.reshape(nr, 256).view(np.uint8)
     return rec
 
 
@@ -318,8 +317,8 @@ def unpack_lion_records(case: O.Case, rec: np.ndarray) -> tuple[np.ndarray, np.n
     """ADAMBRIDGE_DT_PACKED_LION records -> the case's separate master and m (in place); returns
     the padding slots' (master bits, m bits) past n."""
     n = case.n
-    p = np.ascontiguousarray(rec[:, :512]).view(np.uint32).reshape(-1)
-    m = np.ascontiguousarray(rec[:, 512:]).view(np.uint16).reshape(-1)
+    p = np.ascontiguousarray(rec[:, :1024]).view(np.uint32).reshape(-1)
+    m = np.ascontiguousarray(rec[:, 1024:]).view(np.uint16).reshape(-1)
     case.arrays["p"] = p[:n].view(np.float32).copy()
     case.arrays["m"] = m[:n].copy()
     return p[n:].copy(), m[n:].copy()

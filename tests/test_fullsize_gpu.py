@@ -69,9 +69,12 @@ def windows(numel: int) -> list[tuple[int, int]]:
     return [(0, WINDOW), (mid, mid + WINDOW), (last, numel)]
 
 
-def run_config(name: str, warm: int = 2, tensors: int = 6, cfg: dict | None = None,
+def run_config(name: str, warm: int | None = None, tensors: int = 6, cfg: dict | None = None,
                windows_of=None, layout: str = "auto") -> None:
+    """Build the configuration, run its warm-up steps (the configuration's own count: c1 5, c2 10,
+    else 2), then check one more step on sampled windows against the oracle."""
     cfg = cfg or bench.CONFIGS[name]
+    warm = cfg.get("warm_steps", 2) if warm is None else warm
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     opt, params = bench.build(cfg, dev, layout=layout)
@@ -101,6 +104,10 @@ def run_config(name: str, warm: int = 2, tensors: int = 6, cfg: dict | None = No
             case.group = {"lr": group["lr"], "beta1": group["betas"][0], "beta2": group["betas"][1],
                           "eps": group["eps"], "weight_decay": group["weight_decay"], "seed": 0, "stochastic": 1}
             cases.append(case)
+        if cfg.get("zeros"):   # c4: exact-zero gradients at 1% density reach the kernel (sign(0) = 0)
+            zero_grads = sum(int(np.count_nonzero((c.arrays["g"] & 0x7FFF) == 0)) for c in cases)
+            total = sum(c.n for c in cases)
+            assert zero_grads > 0.005 * total, f"{zero_grads} zero gradients in {total} sampled elements"
         want = O.run_many(cases, "oracle", 16, threads=O.threads_default())
         opt.step()
         torch.cuda.synchronize()
@@ -130,10 +137,10 @@ def test_full_size_config_sampled_parity(name):
     run_config(name)
 
 
-@pytest.mark.parametrize("name", ["c3p", "c3"])
+@pytest.mark.parametrize("name", ["c3p", "c3", "c4"])
 def test_full_size_separate_layout_sampled_parity(name):
-    """The reference's separate state arrays at the 7B list (the default keeps BF16 moments
-    interleaved and FP8 moments in block records)."""
+    """The reference's separate state arrays at the 7B list and the Lion list (the default keeps
+    AdamW's BF16 moments in pairs, its FP8 moments in block records and Lion's moment in records)."""
     run_config(name, layout="separate")
 
 

@@ -255,10 +255,10 @@ def test_fp8_records_layout_offsets_and_views(n):
     assert rs.footprint() == (4 * n, nb * (768 + 8) - 4 * n)
 
 
-@pytest.mark.parametrize("n", [1, 2, 127, 128, 301])
+@pytest.mark.parametrize("n", [1, 2, 255, 256, 601])
 def test_lion_and_pair_layout_offsets(n):
-    """LionRecordState: element 128r + i (i < 128) keeps its master at byte 4i of record r and its m
-    bits at 512 + 2i (ADAMBRIDGE_DT_PACKED_LION).  PairState: elements 2k, 2k + 1 at words 0, 1 of
+    """LionRecordState: element 256r + i (i < 256) keeps its master at byte 4i of record r and its m
+    bits at 1024 + 2i (ADAMBRIDGE_DT_PACKED_LION).  PairState: elements 2k, 2k + 1 at words 0, 1 of
     row k, their m and v bits in the halves of words 2 and 3 (ADAMBRIDGE_DT_PACKED)."""
     from adambridge_amd.state import LionRecordState, PairState
     rng = np.random.default_rng(n + 7)
@@ -274,9 +274,9 @@ def test_lion_and_pair_layout_offsets(n):
     lion.load(master=torch.from_numpy(master), moments={"m": stores["m"]})
     rec = lion.current.numpy()
     for e in range(n):
-        r, i = divmod(e, 128)
+        r, i = divmod(e, 256)
         assert rec[r, 4 * i:4 * i + 4].view(np.float32)[0] == master[e]
-        assert rec[r, 512 + 2 * i:514 + 2 * i].view(np.int16)[0] == m[e]
+        assert rec[r, 1024 + 2 * i:1026 + 2 * i].view(np.int16)[0] == m[e]
     assert np.array_equal(lion.moment("m").data.view(torch.int16).numpy(), m)
     pairs = PairState(n, "cpu", double_buffer=True)
     pairs.load(master=torch.from_numpy(master), moments=stores)
@@ -448,3 +448,26 @@ def test_step_coefficients_equal_the_librarys_own(step):
             assert a == b, (field, a, b)
     lion = native.StepCoefficients.for_lion(1e-4, 0.9, 0.99, 0.1)
     assert (lion.step_size, lion.inv_sqrt_bc2, lion.eps) == (1e-4, 1.0, 0.0)
+
+
+def test_optimizer_is_freed_without_the_garbage_collector(monkeypatch):
+    """Nothing the optimizer builds at construction refers back to it (the gradient hooks reach it
+    through a weak reference): dropping the last reference frees it, and with it its device state,
+    at once -- a 7B state is 54 GB of HBM."""
+    import gc
+    import weakref
+
+    import adambridge_amd as ab
+    from adambridge_amd import _hip
+
+    monkeypatch.setattr(_hip, "load", lambda: None)   # no library calls: the engine is never used here
+    params = [torch.nn.Parameter(torch.zeros(4, 4)), torch.nn.Parameter(torch.zeros(4))]
+    gc.disable()
+    try:
+        opt = ab.AdamBridge(params, lr=1e-3)
+        gone = weakref.ref(opt)
+        opt.attach_hooks()
+        del opt
+        assert gone() is None
+    finally:
+        gc.enable()

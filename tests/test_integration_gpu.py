@@ -72,8 +72,14 @@ def _per_block(model):
     return model
 
 
+# The reference's modes (tests/test_compile.py:23-28).  reduce-overhead replays the model's forward and
+# backward as HIP graphs; the optimizer's hooks run eagerly between those replays (the hook is
+# opaque to Dynamo and the post-accumulate-grad hooks fire outside the compiled backward), so no
+# launch of the optimizer is captured.
 COMPILERS = {
     "whole-model": lambda m: torch.compile(m),
+    "reduce-overhead": lambda m: torch.compile(m, mode="reduce-overhead"),
+    "max-autotune": lambda m: torch.compile(m, mode="max-autotune"),
     "per-block": _per_block,
 }
 
@@ -120,12 +126,15 @@ def test_compiled_autograd_calls_the_hook_opaquely(fresh_dynamo):
     opt.close()
 
 
-def test_delayed_updates_under_per_block_compile(fresh_dynamo):
+@pytest.mark.parametrize("how", ["per-block", "reduce-overhead"])
+def test_delayed_updates_under_compile(how, fresh_dynamo):
+    """Delayed updates (one-step-stale weights) under per-block compile and under HIP-graph replay of
+    the model (reference tests/test_compile.py:82-99)."""
     torch.manual_seed(0)
     model = TinyLM().to(DEV)
     want_losses, want = _stale_reference(copy.deepcopy(model), 8, lambda ps: torch.optim.AdamW(ps, lr=3e-3), 0)
     opt = ab.AdamBridge(model.parameters(), lr=3e-3, delay_updates=True).attach_hooks(model)
-    fwd = _per_block(model)
+    fwd = COMPILERS[how](model)
     losses = []
     for k in range(1, 9):
         loss = lm_loss(fwd, k)

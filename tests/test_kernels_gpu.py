@@ -338,13 +338,13 @@ from hip_cases import run_hip_lion_records  # noqa: E402
 
 @pytest.mark.parametrize("double_buffer", [False, True])
 def test_lion_records_match_oracle(double_buffer):
-    """ADAMBRIDGE_DT_PACKED_LION (master + BF16 m in 768-byte records) gives the separate layout's
-    bytes: sizes around the record and the pair, offsets, SR on/off, every grad/out dtype; in place,
-    the padding slots of the last record keep their bits."""
+    """ADAMBRIDGE_DT_PACKED_LION (master + BF16 m in 1536-byte records) gives the separate layout's
+    bytes: sizes around the record and the lane's 4 elements, offsets, SR on/off, every grad/out dtype;
+    in place, the padding slots of the last record keep their bits."""
     rng = np.random.default_rng(41)
     cases = []
     for gt, ot, sr, n in itertools.product([O.DT_BF16, O.DT_F32], [O.DT_NONE, O.DT_F32, O.DT_BF16], [True, False],
-                                           [1, 2, 3, 127, 128, 129, 1000, 2048 + 77, 5001]):
+                                           [1, 2, 3, 5, 255, 256, 257, 1000, 2048 + 77, 5001]):
         cases.append(O.make_case(rng, n, algorithm=O.LION, mv_dtype=O.DT_BF16, g_dtype=gt, out_dtype=ot,
                                  stochastic=sr, offset=int(rng.integers(0, 2**32)), index=int(rng.integers(0, 999)),
                                  step=int(rng.integers(1, 30)), lr=1e-4, betas=(0.9, 0.99), weight_decay=0.1))
@@ -400,7 +400,7 @@ def test_lion_records_reject_bad_segments():
     rng = np.random.default_rng(44)
     k = _hip.load()
     case = O.make_case(rng, 300, algorithm=O.LION, mv_dtype=O.DT_BF16)
-    rec = torch.zeros(3 * 768 + 16, dtype=torch.uint8, device="cuda")
+    rec = torch.zeros(2 * 1536 + 16, dtype=torch.uint8, device="cuda")
     g = torch.zeros(300, dtype=torch.bfloat16, device="cuda")
     hp = _hip.HParams(**{kk: case.hparams[kk] for kk, _ in _hip.HParams._fields_})
     base = dict(p=rec.data_ptr(), g=g.data_ptr(), n=300, step=1, mv_dtype=O.DT_BF16, g_dtype=O.DT_BF16,

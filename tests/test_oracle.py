@@ -283,3 +283,26 @@ def test_segment_validation_codes():
     assert lib.abo_check_segment(seg, 0) == -7
     seg.algorithm = 5
     assert lib.abo_check_segment(seg, 0) == -12
+
+
+@pytest.mark.parametrize("key,short", [("out", 1), ("g", 1), ("p", 7), ("m", 128)])
+@pytest.mark.parametrize("impl", ["oracle", "ref"])
+def test_undersized_case_buffers_are_refused_before_any_call(key, short, impl, monkeypatch):
+    """A case whose host buffer is shorter than its segment needs -- as when a sampled window of a
+    full-size test reaches past the end of its tensor and the slices taken from the tensor come out
+    short -- is refused by oracle.check_sizes with a ValueError before the C oracle or the compiled
+    reference is handed it: either would write its outputs past the numpy buffer's end, corrupting
+    the host heap (glibc then aborts the process)."""
+    if impl == "ref" and not O.reference_available():
+        pytest.skip("the compiled reference (oracle/_ref) is not built")
+    rng = np.random.default_rng(5)
+    case = O.make_case(rng, 1000, mv_dtype=O.DT_FP8 if key == "m" else O.DT_BF16)
+    case.arrays[key] = case.arrays[key][: case.arrays[key].size - short]
+    calls = []
+    lib = O.load_oracle() if impl == "oracle" else O.load_reference()
+    for name in ("abo_multi_apply", "abo_multi_step") if impl == "oracle" else \
+            ("adambridge_multi_apply", "adambridge_multi_step"):
+        monkeypatch.setattr(lib, name, lambda *a, _n=name: calls.append(_n) or 0, raising=False)
+    with pytest.raises(ValueError, match=f"case buffer '{key}' holds"):
+        O.run_many([case], impl, 16)
+    assert not calls
