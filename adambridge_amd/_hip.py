@@ -71,7 +71,7 @@ EXPORTS = (
     "adambridge_pool_set_spin", "adambridge_multi_step", "adambridge_multi_apply", "adambridge_pool_set_stream",
     "adambridge_pool_sync", "adambridge_set_stream", "adambridge_last_error", "adambridge_backend",
     "adambridge_check_conversions", "adambridge_convert", "adambridge_plan_launches",
-    "adambridge_multi_step_noalloc",
+    "adambridge_multi_step_noalloc", "adambridge_stream_copy",
 )
 
 
@@ -107,6 +107,7 @@ def open_library(path: Path = LIB_PATH) -> ctypes.CDLL:
         "adambridge_convert": (ctypes.c_int, [vp, vp, i32, vp, vp, i32, i64, i32]),
         "adambridge_plan_launches": (ctypes.c_int, [_SegArray, i32, ctypes.POINTER(i64), i32]),
         "adambridge_multi_step_noalloc": (ctypes.c_int, [vp, _SegArray, i32]),
+        "adambridge_stream_copy": (ctypes.c_int, [vp, vp, i64]),
     }
     for name in EXPORTS:
         fn = getattr(lib, name)
@@ -234,6 +235,17 @@ class HipKernels:
         if got != count:
             raise RuntimeError(f"adambridge_plan_launches returned {got}, then {count}")
         return [tuple(rows[4 * k: 4 * k + 4]) for k in range(count)]
+
+    def stream_copy(self, src: torch.Tensor, dst: torch.Tensor) -> None:
+        """Copy ``src`` into ``dst`` (same byte size, a multiple of 16) on the current stream with the
+        update kernels' access type (adambridge_stream_copy): the known-size kernel that byte
+        counters are calibrated with."""
+        if src.nbytes != dst.nbytes or not (src.is_cuda and dst.is_cuda and src.is_contiguous() and dst.is_contiguous()):
+            raise ValueError("stream_copy: two contiguous device tensors of the same byte size")
+        with torch.cuda.device(dst.device):
+            self.set_stream(torch.cuda.current_stream(dst.device))
+            self._check(self._lib.adambridge_stream_copy(src.data_ptr(), dst.data_ptr(), dst.nbytes),
+                        "adambridge_stream_copy")
 
     _CONVERT_DTYPES = {torch.float32: DT_F32, torch.bfloat16: DT_BF16, torch.float8_e4m3fn: DT_FP8,
                        torch.float8_e5m2: DT_FP8, torch.uint8: DT_FP8}

@@ -855,8 +855,7 @@ __device__ __forceinline__ void update_tile_packed(const DevSeg& s, int64_t tile
             float p0 = bitsf(x.x), p1 = bitsf(x.y);
             float m0 = bitsf(x.z << 16), m1 = bitsf(x.z & 0xffff0000u);
             float v0 = bitsf(x.w << 16), v1 = bitsf(x.w & 0xffff0000u);
-            p0 = adamw<true>(p0, g0, m0, v0, c);
-            p1 = adamw<true>(p1, g1, m1, v1, c);
+            adamw_pair_fused(p0, p1, g0, g1, m0, m1, v0, v1, c);
             const uint32_t mw = bf16_store<SR>(m0, SR ? hash32(idx ^ s.seed_m) : 0u) |
                                 (bf16_store<SR>(m1, SR ? hash32((idx + 1) ^ s.seed_m) : 0u) << 16);
             const uint32_t vw = bf16_store<SR>(v0, SR ? hash32(idx ^ s.seed_v) : 0u) |
@@ -991,6 +990,26 @@ __global__ __launch_bounds__(64) void k_write_table(TableChunk C)
     uint64_t* dst = reinterpret_cast<uint64_t*>(C.table);
     for (int w = threadIdx.x; w < C.count * kWords; w += 64) dst[w] = src[w];
     for (int i = threadIdx.x; i < C.count; i += 64) C.starts[i] = C.segs[i].tile_begin;
+}
+
+// ------------------------------------------------------------- calibration copy
+//
+// A copy of known size with the update kernels' access type (16-byte non-temporal global loads and
+// stores) and tile order (kCopyTile bytes per workgroup, XCD-contiguous), for calibrating hardware
+// byte counters (FETCH_SIZE, WRITE_SIZE) against the bytes actually moved.
+
+constexpr int64_t kCopyTile = 16 * 1024;
+
+__global__ __launch_bounds__(kThreads) void k_stream_copy(const u32x4* src, u32x4* dst, int64_t n16)
+{
+    const int64_t ntiles = (n16 * 16 + kCopyTile - 1) / kCopyTile;
+    const int64_t b = blockIdx.x;
+    const int64_t per = (ntiles + kXcds - 1) / kXcds;
+    const int64_t tile = (b % kXcds) * per + b / kXcds;
+    if (tile >= ntiles) return;
+    const int64_t lo = tile * (kCopyTile / 16);
+    const int64_t hi = lo + kCopyTile / 16 < n16 ? lo + kCopyTile / 16 : n16;
+    for (int64_t i = lo + threadIdx.x; i < hi; i += kThreads) st(dst + i, ld(src + i));
 }
 
 // ------------------------------------------------------------ kernel table

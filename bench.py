@@ -73,7 +73,7 @@ def llama7b() -> list[tuple[str, tuple]]:
 CONFIGS = {
     "c1": dict(desc="AdamW, FP32 moments, one flat tensor of 16,777,216 params", shapes=lambda: [("flat", (1 << 24,))],
                algo="adamw", precision="fp32", lr=1e-4, betas=(0.9, 0.999), wd=0.01, gscale=(1e-3, 1e-3),
-               warm_steps=5),
+               warm_steps=5, rotate=4),
     "c2": dict(desc="AdamW, bf16 moments, Qwen2.5-0.5B parameter list",
                shapes=lambda: qwen_like(151936, 896, 4864, 24, 128),
                algo="adamw", precision="bf16", lr=2e-5, betas=(0.9, 0.999), wd=0.01, gscale=(1e-5, 1e-2),
@@ -141,24 +141,32 @@ def synthetic_grad(cfg: dict, k: int, shape, gen, device):
 
 
 def gpu_bench(cfg: dict, steps: int, warmup: int, layout: str = "auto", double_buffer: bool = False) -> dict:
+    """Time ``steps`` optimizer steps after ``warmup`` untimed ones.  A configuration with
+    ``rotate`` = R builds R independent copies (weights, gradients, state) and steps them in turn,
+    so that consecutive launches stream from HBM, not from the 256 MB Infinity Cache (c1 moves
+    470 MB per step); each timed step is still one full step of one copy."""
     import torch
 
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
-    opt, params = build(cfg, device, layout=layout, double_buffer=double_buffer)
-    n = sum(p.numel() for p in params)
-    for _ in range(warmup):
-        opt.step()
+    copies = [build(cfg, device, seed=k, layout=layout, double_buffer=double_buffer)
+              for k in range(cfg.get("rotate", 1))]
+    opts = [opt for opt, _ in copies]
+    n = sum(p.numel() for p in copies[0][1])
+    for k in range(warmup * len(opts)):
+        opts[k % len(opts)].step()
     torch.cuda.synchronize()
     log: list = []
-    opt._engine.launch_log = log
+    for opt in opts:
+        opt._engine.launch_log = log
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(steps):
-        opt.step()
+    for k in range(steps):
+        opts[k % len(opts)].step()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    opt._engine.launch_log = None
+    for opt in opts:
+        opt._engine.launch_log = None
     durs = [a.elapsed_time(b) / 1e3 for a, b, _ in log]
     if os.environ.get("ADAMBRIDGE_BENCH_TRACE"):   # diagnostic: launch durations in order, 10 per line
         for k in range(0, len(durs), 10):
@@ -169,28 +177,32 @@ def gpu_bench(cfg: dict, steps: int, warmup: int, layout: str = "auto", double_b
     kernel_s = sum(durs) / len(durs)
     elems_per_launch = sum(e for _, _, e in log) / len(log)
     achieved = elems_per_launch * bpp / kernel_s / 1e9
-    layouts = sorted({s.state.layout for s in opt._ordered})
+    layouts = sorted({s.state.layout for s in opts[0]._ordered})
     state_layout = ", ".join(layouts) + (" (double-buffered)" if double_buffer else "")
-    stats = dict(params=n, tensors=len(params), wall=wall, launches_per_step=launches_per_step, layout=state_layout,
-                 state_bytes=opt.memory_report()["total"],
+    stats = dict(params=n, tensors=len(copies[0][1]), wall=wall, launches_per_step=launches_per_step,
+                 layout=state_layout, state_bytes=opts[0].memory_report()["total"], copies=len(opts),
                  kernel_ms=kernel_s * 1e3, kernel_ms_min=min(durs) * 1e3, kernel_ms_max=max(durs) * 1e3,
                  achieved_gbs=achieved, bytes_per_param=bpp)
-    opt.close()
-    del opt, params
+    for opt in opts:
+        opt.close()
+    del opts, copies
     torch.cuda.empty_cache()
     return stats
 
 
 def calibrate_copy(nbytes: int) -> None:
-    """Three copies of ``nbytes`` between two device buffers: under rocprofv3 --pmc, the copy kernel's
+    """Three copies of ``nbytes`` between two device buffers by the library's k_stream_copy -- the
+    update kernels' 16-byte non-temporal loads and stores and tile order: under rocprofv3 --pmc, its
     FETCH_SIZE and WRITE_SIZE readings against ``nbytes`` give the counters' scale factors."""
     import torch
+    from adambridge_amd import _hip
 
+    nbytes = nbytes // 16 * 16
     src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
     for _ in range(3):
-        dst.copy_(src)
+        _hip.load().stream_copy(src, dst)
     torch.cuda.synchronize()
     print(f"[bench] calibration: 3 copies of {nbytes} bytes", file=sys.stderr, flush=True)
     del src, dst
@@ -505,11 +517,13 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (bf16 weights ~N(0,0.02), bf16 grads ~N(0,1) x log-uniform per-tensor scale)",
+        "data": ("synthetic (bf16 weights ~N(0,0.02); bf16 grads with per-element log-uniform magnitudes in "
+                 f"{cfg['gscale']} and {cfg['zeros']:.0%} exact zeros)" if cfg.get("grads") == "elementwise" else
+                 "synthetic (bf16 weights ~N(0,0.02), bf16 grads ~N(0,1) x log-uniform per-tensor scale)"),
         "config": {"workload": cfg["desc"], "config": args.config, "params": g["params"], "tensors": g["tensors"],
                    "moments": cfg["precision"], "master": "fp32", "grad": "bf16", "out": "bf16",
                    "bytes_per_param": g["bytes_per_param"], "launches_per_step": g["launches_per_step"],
-                   "state_layout": g["layout"], "state_bytes": g["state_bytes"],
+                   "state_layout": g["layout"], "state_bytes": g["state_bytes"], "copies_rotated": g["copies"],
                    "wall_gbs": g["params"] * g["bytes_per_param"] / (ms_per_step / 1e3) / 1e9},
         "roofline": {"bound": "hbm", "achieved": g["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": g["achieved_gbs"] / HBM_PEAK_GBS,

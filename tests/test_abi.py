@@ -255,3 +255,15 @@ def test_noalloc_refuses_more_segments_than_its_array_holds():
         k.multi_step_noalloc(None, arr)
     assert k._lib.adambridge_multi_step_noalloc(None, None, 5) == -1
     assert k._lib.adambridge_multi_step_noalloc(None, None, 0) == 0
+
+
+def test_stream_copy_argument_codes():
+    """adambridge_stream_copy's checks; none reaches the device."""
+    lib = _hip.open_library()
+    buf = (ctypes.c_float * 16)()
+    p = ctypes.addressof(buf) // 16 * 16 + 16
+    assert lib.adambridge_stream_copy(p, p, -16) == -1
+    assert lib.adambridge_stream_copy(p, p, 24) == -1
+    assert lib.adambridge_stream_copy(p, p, 0) == 0
+    assert lib.adambridge_stream_copy(None, p, 16) == -2
+    assert lib.adambridge_stream_copy(p + 4, p, 16) == -14

@@ -549,3 +549,16 @@ def test_fp8_larger_tile_matches_oracle():
                          capture_output=True, text=True, timeout=110)
     print(run.stdout, flush=True)
     assert run.returncode == 0, run.stdout + run.stderr[-3000:]
+
+
+def test_stream_copy_copies_exactly():
+    """adambridge_stream_copy, the counter-calibration copy: every byte, sizes around its tile."""
+    from adambridge_amd import _hip
+    k = _hip.load()
+    g = torch.Generator(device="cuda").manual_seed(3)
+    for nbytes in (16, 16 * 1024 - 16, 16 * 1024, 3 * 16 * 1024 + 48, 1 << 24):
+        src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda", generator=g)
+        dst = torch.zeros_like(src)
+        k.stream_copy(src, dst)
+        torch.cuda.synchronize()
+        assert torch.equal(src, dst), nbytes
