@@ -43,7 +43,7 @@ METRIC = "params updated/sec and achieved HBM GB/s (% roofline), AdamW bf16 mome
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the update kernel, measured with rocprofv3 FETCH_SIZE + WRITE_SIZE, each
 # scaled by its reading for a copy of known size (profiles/*_hbm_traffic.md).
-MEASURED_TRAFFIC = {"c3p": 134.764e9, "c1": 469.84e6, "c2": 9.8808e9, "c3": 108.67e9, "c4": 24.6996e9}
+MEASURED_TRAFFIC = {"c3p": 134.767e9, "c1": 469.84e6, "c2": 9.8808e9, "c3": 108.67e9, "c4": 24.700e9}
 
 
 # ------------------------------------------------------------ parameter lists
