@@ -16,6 +16,8 @@ over the K timed steps, bracketed by device synchronisations); ``roofline``
 for the update kernel = algorithmic bytes per launch (the reference's minimum
 bytes, benchmarks/bench_kernels.py:63-65, times the parameters) divided by its
 mean launch duration, timed with HIP events on the stream the kernel runs on;
+``copy_ceiling`` = a plain copy of the same bytes (half read, half written)
+by the library's k_stream_copy, the rate a 1:1 read/write stream reaches here;
 ``cpu_baseline`` = the reference's own native kernel (oracle/_ref, compiled
 from its C source) timed on this host's cores over a bounded sample of the
 same parameter list.
@@ -207,6 +209,39 @@ def calibrate_copy(nbytes: int) -> None:
     print(f"[bench] calibration: 3 copies of {nbytes} bytes", file=sys.stderr, flush=True)
     del src, dst
     torch.cuda.empty_cache()
+
+
+def copy_ceiling(total_bytes: float, reps: int = 10) -> dict:
+    """The rate of a plain copy moving the update's bytes -- half read, half written -- by the
+    library's k_stream_copy (16-byte non-temporal loads and stores, 4 KiB tiles handed out XCD by
+    XCD), timed with HIP events on the stream it runs on: what a 1:1 read/write stream of the same
+    size reaches on this device.  Copies under 4 GB rotate over four buffer pairs, so that each
+    streams from HBM rather than the 256 MB Infinity Cache.  Median over ``reps`` launches after 3
+    untimed ones."""
+    import statistics
+
+    import torch
+    from adambridge_amd import _hip
+
+    k = _hip.load()
+    half = int(total_bytes / 2) // 16 * 16
+    pairs = [(torch.ones(half, dtype=torch.uint8, device="cuda"), torch.empty(half, dtype=torch.uint8, device="cuda"))
+             for _ in range(4 if 2 * half < 4e9 else 1)]
+    times = []
+    for i in range(3 + reps):
+        src, dst = pairs[i % len(pairs)]
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        k.stream_copy(src, dst)
+        b.record()
+        b.synchronize()
+        if i >= 3:
+            times.append(a.elapsed_time(b) / 1e3)
+    del pairs
+    torch.cuda.empty_cache()
+    t = statistics.median(times)
+    gbs = 2 * half / t / 1e9
+    return dict(kernel="k_stream_copy", bytes=2 * half, ms=t * 1e3, gbs=gbs, frac=gbs / HBM_PEAK_GBS)
 
 
 # ------------------------------------------------------- hooked pipeline (c5)
@@ -464,6 +499,8 @@ def main() -> int:
     ap.add_argument("--cpu-params", type=int, default=1 << 30, help="CPU baseline sample size (parameters)")
     ap.add_argument("--cpu-steps", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-copy-ceiling", action="store_true",
+                    help="skip timing a plain copy of the update's bytes (the copy_ceiling object)")
     ap.add_argument("--layout", default="auto", choices=["auto", "packed", "separate"],
                     help="optimizer state layout in HBM (AdamBridge state_layout)")
     ap.add_argument("--double-buffer", action="store_true", help="AdamBridge double_buffer=True")
@@ -498,6 +535,12 @@ def main() -> int:
         r = gpu_bench(cfg, args.steps, args.warmup, args.layout, args.double_buffer)
         print(f"[bench] rebuild {k}: {r['kernel_ms']:.3f} ms/launch, {r['achieved_gbs']:.0f} GB/s", file=sys.stderr,
               flush=True)
+    ceiling = None
+    if not args.no_copy_ceiling:
+        ceiling = copy_ceiling(g["params"] * g["bytes_per_param"])
+        ceiling["update_vs_copy"] = g["achieved_gbs"] / ceiling["gbs"]
+        print(f"[bench] copy of the same bytes: {ceiling['ms']:.3f} ms, {ceiling['gbs']:.0f} GB/s; "
+              f"update / copy {ceiling['update_vs_copy']:.3f}", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else cpu_bench(cfg, args.cpu_params, args.cpu_steps)
     if cpu is not None:
         print(f"[bench] CPU reference: {cpu['ms_per_step']:.1f} ms/step on {cpu['cores']} threads, "
@@ -529,6 +572,7 @@ def main() -> int:
                      "frac": g["achieved_gbs"] / HBM_PEAK_GBS,
                      "traffic": args.traffic if args.traffic is not None else MEASURED_TRAFFIC.get(args.config),
                      "kernel_ms": g["kernel_ms"]},
+        "copy_ceiling": ceiling,
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample",
                                                                       "ms_per_step", "gbs", "all_cores", "host")},
     }

@@ -257,13 +257,13 @@ ADAMBRIDGE_API int adambridge_plan_launches(adambridge_segment* const* segs, int
 ADAMBRIDGE_API int adambridge_convert(const void* src, const float* src_scale, int32_t src_dtype, void* dst,
                                       float* dst_scale, int32_t dst_dtype, int64_t n, int32_t role);
 
-/* Copies nbytes (a multiple of 16; src and dst 16-byte aligned) on the calling thread's stream with
- * the update kernels' access type -- 16-byte non-temporal global loads and stores, workgroup tiles
- * handed out XCD by XCD (kernel k_stream_copy) -- so that hardware byte counters (rocprofv3
- * FETCH_SIZE / WRITE_SIZE) read for it calibrate the same counters read for the update kernels.
- * Asynchronous.  Returns 0, ADAMBRIDGE_EBADN (negative or not a multiple of 16), _ENULL, _EALIGN,
- * _ETOOMANY (more tiles than one dispatch takes: over 256 GiB) or _EHIP.  No counterpart in the
- * reference: a measurement aid. */
+/* Copies nbytes (a multiple of 16; src and dst 16-byte aligned, not overlapping) on the calling
+ * thread's stream with the update kernels' access type -- 16-byte non-temporal global loads and
+ * stores, 4 KiB workgroup tiles handed out XCD by XCD (kernel k_stream_copy, one launch per 64 GiB)
+ * -- so that hardware byte counters (rocprofv3 FETCH_SIZE / WRITE_SIZE) read for it calibrate the
+ * same counters read for the update kernels, and its time bounds what a 1:1 read/write stream of
+ * the same bytes reaches.  Asynchronous.  Returns 0, ADAMBRIDGE_EBADN (negative or not a multiple of
+ * 16), _ENULL, _EALIGN or _EHIP.  No counterpart in the reference: a measurement aid. */
 ADAMBRIDGE_API int adambridge_stream_copy(const void* src, void* dst, int64_t nbytes);
 
 /* Self-check of the device's conversion, square-root and reciprocal instructions, on the current

@@ -552,13 +552,32 @@ def test_fp8_larger_tile_matches_oracle():
 
 
 def test_stream_copy_copies_exactly():
-    """adambridge_stream_copy, the counter-calibration copy: every byte, sizes around its tile."""
+    """adambridge_stream_copy, the counter-calibration copy: every byte, sizes around its 4 KiB tile."""
     from adambridge_amd import _hip
     k = _hip.load()
     g = torch.Generator(device="cuda").manual_seed(3)
-    for nbytes in (16, 16 * 1024 - 16, 16 * 1024, 3 * 16 * 1024 + 48, 1 << 24):
+    for nbytes in (16, 4096 - 16, 4096, 3 * 4096 + 48, 1 << 24):
         src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda", generator=g)
         dst = torch.zeros_like(src)
         k.stream_copy(src, dst)
         torch.cuda.synchronize()
         assert torch.equal(src, dst), nbytes
+
+
+def test_stream_copy_beyond_one_launch():
+    """A copy of more than 64 GiB goes out as two launches; each byte lands once, the ragged end too."""
+    from adambridge_amd import _hip
+    k = _hip.load()
+    torch.cuda.empty_cache()
+    nbytes = (64 << 30) + 4096 + 48
+    src = torch.empty(nbytes // 8, dtype=torch.int64, device="cuda")
+    torch.arange(src.numel(), out=src)
+    src.mul_(0x5851F42D4C957F2D)   # wraps: every 8-byte word differs
+    dst = torch.zeros_like(src)
+    try:
+        k.stream_copy(src, dst)
+        torch.cuda.synchronize()
+        assert torch.equal(src, dst)
+    finally:
+        del src, dst
+        torch.cuda.empty_cache()
