@@ -325,10 +325,11 @@ def unpack_lion_records(case: O.Case, rec: np.ndarray) -> tuple[np.ndarray, np.n
 
 
 def run_hip_lion_records(cases: list[O.Case], width: int = 16, double_buffer: bool = False,
-                         misalign_g: bool = False, padding: list | None = None) -> list[O.Case]:
+                         misalign_g: int = 0, padding: list | None = None) -> list[O.Case]:
     """Like run_hip for Lion / FP32 master / BF16 moment cases, through the record layout
-    (ADAMBRIDGE_DT_PACKED_LION): pack on the host, one call, unpack the result.  ``padding``
-    receives each case's padding slots after the call."""
+    (ADAMBRIDGE_DT_PACKED_LION): pack on the host, one call, unpack the result.  ``misalign_g``
+    elements shift the gradient off its allocation's alignment; ``padding`` receives each case's
+    padding slots after the call."""
     kernels = _hip.load()
     work = [c.copy() for c in cases]
     keep, segs = [], []
@@ -340,10 +341,11 @@ def run_hip_lion_records(cases: list[O.Case], width: int = 16, double_buffer: bo
         dst = torch.full_like(rec, 0x5A) if double_buffer else None
         g = to_device(c.arrays["g"])
         if misalign_g:
-            buf = torch.empty(g.numel() + 1, dtype=g.dtype, device=g.device)
-            buf[1:].copy_(g)
+            shift = int(misalign_g)
+            buf = torch.empty(g.numel() + shift, dtype=g.dtype, device=g.device)
+            buf[shift:].copy_(g)
             keep.append(buf)
-            g = buf[1:]
+            g = buf[shift:]
         out = to_device(c.arrays["out"]) if "out" in c.arrays else None
         grp = None
         if by_group:

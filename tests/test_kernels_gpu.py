@@ -359,8 +359,9 @@ def test_lion_records_match_oracle(double_buffer):
 
 
 def test_lion_records_zero_gradients_misaligned_and_specials():
-    """Exact-zero gradients at 1% (sign(0) = 0, kernels.c:1107-1124), a misaligned gradient (the
-    element-wise path) and non-finite inputs."""
+    """Exact-zero gradients at 1% (sign(0) = 0, kernels.c:1107-1124), gradients shifted by one
+    element (off the vector path's alignment: the element-wise path) and by two, and non-finite
+    inputs."""
     rng = np.random.default_rng(42)
     cases = []
     for n, sp in ((999, False), (4096, False), (4096, True), (5001, True)):
@@ -373,10 +374,11 @@ def test_lion_records_zero_gradients_misaligned_and_specials():
             assert zero.any()
         cases.append(c)
     want = O.run_many(cases, "oracle", 16)
-    got = run_hip_lion_records(cases, 16, misalign_g=True)
-    for w, g in zip(want, got):
-        bad = O.outputs_equal(w, g, nan_equiv=True)
-        assert not bad, bad
+    for shift in (1, 2):
+        got = run_hip_lion_records(cases, 16, misalign_g=shift)
+        for w, g in zip(want, got):
+            bad = O.outputs_equal(w, g, nan_equiv=True)
+            assert not bad, (shift, bad)
 
 
 def test_lion_records_multi_step_groups_and_steps():
