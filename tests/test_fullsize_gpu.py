@@ -12,6 +12,10 @@ launch per step -- and then checks one more step two ways:
   what the whole-tensor launch must write there;
 * every element: the bf16 working weight written by the step equals the round-to-nearest-even
   bf16 of the stored master (kernels.c:108-112 applied to the value actually stored).
+
+``test_full_size_every_element`` checks every element of every tensor bit for bit: the state
+before the step is cloned on the device, and after the step the oracle updates the clone chunk
+by chunk (host memory bounded by one chunk) for comparison with what the launch wrote.
 """
 
 from __future__ import annotations
@@ -135,6 +139,70 @@ def run_config(name: str, warm: int | None = None, tensors: int = 6, cfg: dict |
 @pytest.mark.parametrize("name", ["c3p", "c3", "c4", "c2", "c1"])
 def test_full_size_config_sampled_parity(name):
     run_config(name)
+
+
+def _host(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().contiguous()
+    if t.dtype == torch.float32:
+        return t.cpu().numpy()
+    return _u16(t) if t.element_size() == 2 else _u8(t)
+
+
+CHUNK = 1 << 28   # elements per oracle call
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c4", "c3p", "c3"])
+def test_full_size_every_element(name):
+    """One step after the configuration's warm-up steps, every element of every tensor against the
+    oracle: master (and its low plane), moments, FP8 block scales and the bf16 working weight."""
+    cfg = bench.CONFIGS[name]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    opt, params = bench.build(cfg, dev)
+    try:
+        for _ in range(cfg.get("warm_steps", 2)):
+            opt.step()
+        torch.cuda.synchronize()
+        before = {s.index: {k: v.clone() for k, v in s.state.window(0, s.numel).items()} for s in opt._ordered}
+        opt.step()
+        torch.cuda.synchronize()
+        lion = cfg["algo"] == "lion"
+        mv = {"fp32": O.DT_F32, "bf16": O.DT_BF16, "fp8": O.DT_FP8}[cfg["precision"]]
+        group = opt.param_groups[0]
+        ogroup = {"lr": group["lr"], "beta1": group["betas"][0], "beta2": group["betas"][1], "eps": group["eps"],
+                  "weight_decay": group["weight_decay"], "seed": 0, "stochastic": 1}
+        slots, checked = list(opt._ordered), 0
+        while slots:
+            chunk, size = [], 0
+            while slots and (not chunk or size + slots[0].numel <= CHUNK):
+                chunk.append(slots.pop(0))
+                size += chunk[-1].numel
+            cases = []
+            for slot in chunk:
+                arrays = {k: _host(v) for k, v in before.pop(slot.index).items()}
+                arrays["g"] = _host(slot.param.grad.reshape(-1))
+                arrays["out"] = np.zeros(slot.numel, np.uint16)
+                case = O.Case(n=slot.numel, algorithm=O.LION if lion else O.ADAMW, mv_dtype=mv,
+                              p_dtype=O.DT_F24 if "p_lo" in arrays else O.DT_F32, g_dtype=O.DT_BF16,
+                              out_dtype=O.DT_BF16, offset=0, index=slot.index, step=slot.step, arrays=arrays)
+                case.group = dict(ogroup)
+                cases.append(case)
+            O.run_many(cases, "oracle", 16, threads=O.threads_default(), in_place=True)
+            for slot, want in zip(chunk, cases):
+                got = {k: _host(v) for k, v in slot.state.window(0, slot.numel).items()}
+                got["out"] = _u16(slot.param.detach().reshape(-1))
+                for key in ("p", "p_lo", "m", "v", "m_scale", "v_scale", "out"):
+                    if key in want.arrays:
+                        assert np.array_equal(want.arrays[key].view(np.uint8), got[key].view(np.uint8)), \
+                            f"{name}: parameter {slot.index}: {key} differs"
+                checked += slot.numel
+            del cases
+        assert checked == sum(p.numel() for p in params)
+    finally:
+        opt.close()
+        del opt, params
+        before = None
+        torch.cuda.empty_cache()
 
 
 @pytest.mark.parametrize("name", ["c3p", "c3", "c4"])
