@@ -28,6 +28,7 @@ from __future__ import annotations
 import ctypes
 import threading
 import time
+import weakref
 from dataclasses import dataclass, field
 
 import torch
@@ -43,7 +44,7 @@ class ParamSlot:
     """One parameter: its index (rounding stream), group, step count, state and kernel descriptor."""
 
     __slots__ = ("index", "param", "group", "numel", "step", "state", "out", "out_view", "submitted", "seg",
-                 "seg_ptr", "bound", "small", "done_ev")
+                 "seg_ptr", "bound", "_small", "done_ev")
 
     def __init__(self, index: int, param: torch.Tensor, group: dict):
         self.index = index
@@ -58,12 +59,24 @@ class ParamSlot:
         self.seg = _hip.Segment(n=self.numel, index=index)
         self.seg_ptr = ctypes.pointer(self.seg)
         self.bound: ParamState | None = None        # the state whose buffers seg points at
-        self.small: SmallGroup | None = None
+        self._small: weakref.ref | None = None
         self.done_ev: torch.cuda.Event | None = None   # recorded after the slot's latest update
 
     @property
     def initialized(self) -> bool:
         return self.state is not None
+
+    @property
+    def small(self) -> SmallGroup | None:
+        """The small-parameter batch this slot is updated in, or None.  Held weakly: the batch holds
+        its slots, and a cycle would keep every slot -- its parameter group, hence every parameter,
+        and its state, a view of an arena shared with all the others -- alive until the garbage
+        collector ran, instead of freeing the HBM when the optimizer is dropped."""
+        return None if self._small is None else self._small()
+
+    @small.setter
+    def small(self, group: SmallGroup | None) -> None:
+        self._small = None if group is None else weakref.ref(group)
 
     # The moments through the state (copies for interleaved layouts), as the reference's slots expose them.
     @property

@@ -76,11 +76,19 @@ def windows(numel: int) -> list[tuple[int, int]]:
 def run_config(name: str, warm: int | None = None, tensors: int = 6, cfg: dict | None = None,
                windows_of=None, layout: str = "auto") -> None:
     """Build the configuration, run its warm-up steps (the configuration's own count: c1 5, c2 10,
-    else 2), then check one more step on sampled windows against the oracle."""
+    else 2), then check one more step on sampled windows against the oracle; then check that
+    dropping the optimizer and the model freed all of it."""
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    base = torch.cuda.memory_allocated(dev)
+    _sampled_parity(name, warm, tensors, cfg, windows_of, layout)
+    _check_released(name, base)
+
+
+def _sampled_parity(name, warm, tensors, cfg, windows_of, layout) -> None:
     cfg = cfg or bench.CONFIGS[name]
     warm = cfg.get("warm_steps", 2) if warm is None else warm
     dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
     opt, params = bench.build(cfg, dev, layout=layout)
     windows_of = windows_of or windows
     try:
@@ -136,6 +144,15 @@ def run_config(name: str, warm: int | None = None, tensors: int = 6, cfg: dict |
         torch.cuda.empty_cache()
 
 
+def _check_released(name: str, base: int) -> None:
+    """The dropped optimizer and model left nothing allocated: reference counting alone frees the
+    state arena, the parameters and the gradients (no cycle waits for the garbage collector)."""
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    left = torch.cuda.memory_allocated() - base
+    assert left < 64 << 20, f"{name}: {left / 2**30:.2f} GiB still allocated after the optimizer was dropped"
+
+
 @pytest.mark.parametrize("name", ["c3p", "c3", "c4", "c2", "c1"])
 def test_full_size_config_sampled_parity(name):
     run_config(name)
@@ -155,9 +172,16 @@ CHUNK = 1 << 28   # elements per oracle call
 def test_full_size_every_element(name):
     """One step after the configuration's warm-up steps, every element of every tensor against the
     oracle: master (and its low plane), moments, FP8 block scales and the bf16 working weight."""
-    cfg = bench.CONFIGS[name]
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    base = torch.cuda.memory_allocated(dev)
+    _every_element(name)
+    _check_released(name, base)
+
+
+def _every_element(name: str) -> None:
+    cfg = bench.CONFIGS[name]
+    dev = torch.device("cuda", 0)
     opt, params = bench.build(cfg, dev)
     try:
         for _ in range(cfg.get("warm_steps", 2)):
