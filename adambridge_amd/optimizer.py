@@ -250,8 +250,8 @@ class AdamBridge(torch.optim.Optimizer):
     HIP-specific: ``state_layout`` -- 'auto' (default) keeps each parameter's master and
     moments interleaved where a layout for its precision exists (AdamW with BF16 moments:
     16 bytes per pair of elements; AdamW with FP8 moments: one 768-byte record per
-    128-element block, block scales apart; Lion with a BF16 moment: one 768-byte record per
-    128 elements), which stream faster from HBM than separate arrays; 'separate' keeps the
+    128-element block, block scales apart; Lion with a BF16 moment: one 1536-byte record per
+    256 elements), which stream faster from HBM than separate arrays; 'separate' keeps the
     reference's arrays; values, rounding and checkpoints are identical either way.
     ``double_buffer`` -- interleaved BF16 state alternates between two buffers (reads and
     writes go to different memory), at 8 (Lion 6) more bytes per parameter; FP8 records are
