@@ -292,6 +292,53 @@ def test_lion_no_eps():
         ab.LionBridge(tiny_mlp(device=DEV).parameters(), eps=1e-8)
 
 
+@pytest.mark.parametrize("layout,precision", [("auto", "bf16"), ("separate", "bf16"), ("separate", "fp32"),
+                                              ("separate", "fp8")])
+def test_lion_state_dict_resume_is_exact(layout, precision):
+    """reference test_lion.py:102-124: a Lion checkpoint resumed into a fresh optimizer continues bit
+    for bit (bf16 parameters, so the master is a buffer of its own; 'auto' keeps the BF16 moment in
+    Lion records, whose checkpoint holds the reference's separate arrays); AdamBridge refuses it."""
+    kw = dict(lr=1e-3, precision=precision, state_layout=layout, seed=3)
+    model = tiny_mlp(device=DEV, dtype=torch.bfloat16)
+    opt = ab.LionBridge(model.parameters(), **kw)
+    train(model, opt, 3)
+    assert {s.state.layout for s in opt._ordered} == {"lion-records" if layout == "auto" else "separate"}
+    buf = io.BytesIO()
+    torch.save({"model": model.state_dict(), "opt": opt.state_dict()}, buf)
+    train(model, opt, 4, seed=7)
+    expected = [p.detach().clone() for p in model.parameters()]
+    masters = opt.master_params()
+
+    buf.seek(0)
+    ckpt = torch.load(buf, weights_only=True)
+    model2 = tiny_mlp(seed=5, device=DEV, dtype=torch.bfloat16)
+    model2.load_state_dict(ckpt["model"])
+    opt2 = ab.LionBridge(model2.parameters(), **kw)
+    opt2.load_state_dict(ckpt["opt"])
+    train(model2, opt2, 4, seed=7)
+    assert all(torch.equal(a, b) for a, b in zip(expected, model2.parameters()))
+    assert all(torch.equal(a, b) for a, b in zip(masters, opt2.master_params()))
+
+    adam = ab.AdamBridge(tiny_mlp(device=DEV).parameters())
+    with pytest.raises(ValueError, match="exp_avg_sq"):
+        adam.load_state_dict(ckpt["opt"])
+    for o in (opt, opt2, adam):
+        o.close()
+
+
+@pytest.mark.parametrize("precision", ["bf16", "fp8"])
+def test_lion_low_precision_moment_trains_like_fp32(precision):
+    """reference test_lion.py:65-74: a BF16 or FP8 moment trains as the FP32 one does."""
+    results = {}
+    for p in ("fp32", precision):
+        model = tiny_mlp(device=DEV)
+        opt = ab.LionBridge(model.parameters(), lr=3e-4, precision=p)
+        results[p] = train(model, opt, 60)
+        opt.close()
+    assert results[precision][-1] < 0.5 * results[precision][0]
+    assert abs(results[precision][-1] - results["fp32"][-1]) < 0.1 * results["fp32"][0]
+
+
 @pytest.mark.parametrize("window", [3, 2])
 def test_accumulation_steps_match_accumulated_adamw(window):
     """reference test_lion.py:132-153 (AdamW with accumulation_steps)."""
