@@ -142,11 +142,14 @@ def synthetic_grad(cfg: dict, k: int, shape, gen, device):
     return torch.randn(shape, generator=gen, device=device, dtype=torch.bfloat16).mul_(scale)
 
 
-def gpu_bench(cfg: dict, steps: int, warmup: int, layout: str = "auto", double_buffer: bool = False) -> dict:
+def gpu_bench(cfg: dict, steps: int, warmup: int, layout: str = "auto", double_buffer: bool = False,
+              keep: list | None = None) -> dict:
     """Time ``steps`` optimizer steps after ``warmup`` untimed ones.  A configuration with
     ``rotate`` = R builds R independent copies (weights, gradients, state) and steps them in turn,
     so that consecutive launches stream from HBM, not from the 256 MB Infinity Cache (c1 moves
-    470 MB per step); each timed step is still one full step of one copy."""
+    470 MB per step); each timed step is still one full step of one copy.  ``keep``: a list that
+    receives the optimizers and parameters instead of their being released (the caller closes the
+    optimizers)."""
     import torch
 
     device = torch.device("cuda", 0)
@@ -185,11 +188,22 @@ def gpu_bench(cfg: dict, steps: int, warmup: int, layout: str = "auto", double_b
                  layout=state_layout, state_bytes=opts[0].memory_report()["total"], copies=len(opts),
                  kernel_ms=kernel_s * 1e3, kernel_ms_min=min(durs) * 1e3, kernel_ms_max=max(durs) * 1e3,
                  achieved_gbs=achieved, bytes_per_param=bpp)
+    if keep is not None:
+        keep.extend(copies)
+        return stats
     for opt in opts:
         opt.close()
     del opts, copies
     torch.cuda.empty_cache()
     return stats
+
+
+def torch_release() -> None:
+    """Return cached device memory to the driver (after the held builds are dropped)."""
+    import torch
+
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
 
 
 def calibrate_copy(nbytes: int) -> None:
@@ -511,6 +525,8 @@ def main() -> int:
                     help="diagnostic: build and time the state N times in this process, printing each "
                          "on stderr (the GPU's power state can change between them); the JSON line "
                          "reports the first")
+    ap.add_argument("--no-second-build", action="store_true",
+                    help="skip timing a second state built while the first is alive (the placement object)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="first run 3 device-to-device copies of BYTES bytes (a known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -529,8 +545,25 @@ def main() -> int:
         calibrate_copy(args.calibrate_copy)
     print(f"[bench] config {args.config}: {cfg['desc']}; warmup {args.warmup}, steps {args.steps}",
           file=sys.stderr, flush=True)
-    g = gpu_bench(cfg, args.steps, args.warmup, args.layout, args.double_buffer)
+    held: list = []
+    g = gpu_bench(cfg, args.steps, args.warmup, args.layout, args.double_buffer, keep=held)
     print(f"[bench] GPU: {g['kernel_ms']:.3f} ms/launch, {g['achieved_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+    placement = None
+    if not args.no_second_build:
+        # The state a fresh process builds first can land where HBM serves this update's traffic
+        # more slowly; a second state, built while the first is still allocated, shows the rate the
+        # same kernel reaches elsewhere in HBM.  The line's value and roofline are the first build's.
+        s2 = gpu_bench(cfg, args.steps, args.warmup, args.layout, args.double_buffer)
+        placement = {"first_build_kernel_ms": g["kernel_ms"], "second_build_kernel_ms": s2["kernel_ms"],
+                     "second_build_gbs": s2["achieved_gbs"], "second_build_frac": s2["achieved_gbs"] / HBM_PEAK_GBS,
+                     "note": "value and roofline are the first build's; the second state is built and timed "
+                             "while the first is still allocated"}
+        print(f"[bench] second build: {s2['kernel_ms']:.3f} ms/launch, {s2['achieved_gbs']:.0f} GB/s",
+              file=sys.stderr, flush=True)
+    for opt, _ in held:
+        opt.close()
+    del held
+    torch_release()
     for k in range(1, args.rebuilds):
         r = gpu_bench(cfg, args.steps, args.warmup, args.layout, args.double_buffer)
         print(f"[bench] rebuild {k}: {r['kernel_ms']:.3f} ms/launch, {r['achieved_gbs']:.0f} GB/s", file=sys.stderr,
@@ -573,6 +606,7 @@ def main() -> int:
                      "traffic": args.traffic if args.traffic is not None else MEASURED_TRAFFIC.get(args.config),
                      "kernel_ms": g["kernel_ms"]},
         "copy_ceiling": ceiling,
+        "placement": placement,
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample",
                                                                       "ms_per_step", "gbs", "all_cores", "host")},
     }
