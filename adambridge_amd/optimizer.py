@@ -495,14 +495,35 @@ class AdamBridge(torch.optim.Optimizer):
 
     def state_dict(self) -> dict[str, Any]:
         """The reference's checkpoint (optimizer.py:525-544), after applying pending delayed updates so
-        that the model's weights match the saved masters."""
+        that the model's weights match the saved masters.  States in the reference's separate arrays
+        are exported as their own device tensors; interleaved states are gathered into the reference's
+        arrays, on the device when it has room for all of them, else parameter by parameter into host
+        memory (then the device holds one parameter's copy at a time)."""
         self._engine.flush()
         self._engine.wait()
         out = super().state_dict()
-        out["state"] = {s.index: {"step": s.step, **s.state.export()} for s in self._ordered if s.state is not None}
+        host = self._export_to_host()
+        out["state"] = {s.index: {"step": s.step, **s.state.export(host=host and s.state.gathers)}
+                        for s in self._ordered if s.state is not None}
         out["adambridge"] = {"precision": self.precision, "master_precision": self.master_precision, "format": 1,
                              "algorithm": self._algorithm}
         return out
+
+    _EXPORT_MARGIN = 1 << 30   # device bytes left free when a checkpoint is gathered on the device
+
+    def _export_to_host(self) -> bool:
+        """True if gathering every interleaved state's checkpoint arrays on its device would not fit in
+        the memory free there (the driver's free memory plus what torch holds cached and unused)."""
+        need: dict[torch.device, int] = {}
+        for slot in self._ordered:
+            if slot.state is not None and slot.state.gathers:
+                need[slot.state.device] = need.get(slot.state.device, 0) + slot.state.export_bytes()
+        for device, nbytes in need.items():
+            free = torch.cuda.mem_get_info(device)[0]
+            free += torch.cuda.memory_reserved(device) - torch.cuda.memory_allocated(device)
+            if nbytes + self._EXPORT_MARGIN > free:
+                return True
+        return False
 
     def load_state_dict(self, state_dict: dict[str, Any]) -> None:
         """An AdamBridge / LionBridge checkpoint, or a torch.optim.AdamW one, moments converted to this

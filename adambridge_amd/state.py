@@ -61,6 +61,7 @@ class ParamState:
     precision = ""            # moment precision
     master_precision = "fp32"
     master_is_param = False   # the master is the FP32 parameter itself, updated in place
+    gathers = False           # a checkpoint export builds new tensors (interleaved layouts)
 
     def __init__(self, numel: int, device, roles: tuple[str, ...]):
         self.numel = int(numel)
@@ -95,12 +96,13 @@ class ParamState:
         """Checkpoint master entry: an FP32 tensor, or an FP24 store dictionary."""
         return self.master_fp32()
 
-    def export(self) -> dict[str, Any]:
-        """This state's checkpoint entries: ``master``, ``exp_avg`` and (AdamW) ``exp_avg_sq``."""
+    def export(self, host: bool = False) -> dict[str, Any]:
+        """This state's checkpoint entries: ``master``, ``exp_avg`` and (AdamW) ``exp_avg_sq``; with
+        ``host``, as copies in host memory (what is gathered on the device is freed on return)."""
         out = {"master": self.export_master()}
         for role, key in zip(self.roles, ("exp_avg", "exp_avg_sq")):
             out[key] = self.moment(role).state_dict()
-        return out
+        return _on_host(out) if host else out
 
     def load(self, master: Any = None, moments: dict[str, MomentStore] | None = None) -> None:
         """Take validated checkpoint master weights (or FP32 values) and moment stores of this state's
@@ -116,6 +118,15 @@ class ParamState:
         and 'p_lo'), 'm', 'v' (FP32 values, BF16 bits, or FP8 codes with 'm_scale' / 'v_scale' of the
         blocks covering the range; FP8 ranges start on a block boundary)."""
         raise NotImplementedError
+
+
+def _on_host(entry: Any) -> Any:
+    """``entry`` (a tensor, or a checkpoint dictionary of them) with every tensor copied to host memory."""
+    if isinstance(entry, torch.Tensor):
+        return entry.cpu()
+    if isinstance(entry, dict):
+        return {k: _on_host(v) for k, v in entry.items()}
+    return entry
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -206,6 +217,12 @@ def _moved(store: MomentStore, device) -> MomentStore:
 
 class _Interleaved(ParamState):
     """State in one buffer (two when double-buffered): ``current`` is read, ``target`` written."""
+
+    gathers = True
+
+    def export_bytes(self) -> int:
+        """Device bytes a checkpoint export of this state gathers (one buffer's worth)."""
+        return self.current.nbytes
 
     def __init__(self, numel, device, roles, buffers: list[torch.Tensor]):
         super().__init__(numel, device, roles)
@@ -388,6 +405,9 @@ class AdamRecordState(_Interleaved):
 
     def footprint(self):
         return 4 * self.numel, self.current.nbytes - 4 * self.numel + sum(s.nbytes for s in self.scales.values())
+
+    def export_bytes(self):
+        return self.current.nbytes + sum(s.nbytes for s in self.scales.values())
 
     def window(self, lo, hi):
         b0, b1 = lo // 128, -(-hi // 128)

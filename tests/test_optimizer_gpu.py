@@ -863,6 +863,48 @@ def test_state_layouts_give_identical_bytes(hooks, precision):
             assert all(torch.equal(x, y) for x, y in zip(xs, ys))
 
 
+@pytest.mark.parametrize("algo,precision", [("adamw", "bf16"), ("adamw", "fp8"), ("lion", "bf16")])
+def test_interleaved_checkpoint_gathered_on_host_when_the_device_is_short(algo, precision):
+    """Interleaved states (BF16 pairs, FP8 records, Lion records) are gathered into the reference's
+    checkpoint arrays on the device when it has room, else into host memory parameter by parameter;
+    either checkpoint loads into a fresh optimizer with identical masters and moments."""
+    torch.manual_seed(0)
+    model = TinyLM().to(DEV).to(torch.bfloat16)
+    cls = ab.LionBridge if algo == "lion" else ab.AdamBridge
+    opt = cls(model.parameters(), lr=3e-3, precision=precision)
+    for step in range(3):
+        lm_loss(model, step).backward()
+        opt.step()
+        opt.zero_grad()
+    assert all(s.state.gathers for s in opt._ordered)
+
+    def tensors(entry):
+        if isinstance(entry, torch.Tensor):
+            return [entry]
+        return [t for v in entry.values() for t in tensors(v)] if isinstance(entry, dict) else []
+
+    on_device = opt.state_dict()
+    opt._EXPORT_MARGIN = 1 << 62   # as if the device had no room left
+    on_host = opt.state_dict()
+    assert all(t.is_cuda for e in on_device["state"].values() for t in tensors(e))
+    assert all(not t.is_cuda for e in on_host["state"].values() for t in tensors(e))
+    buf = io.BytesIO()
+    torch.save(on_host, buf)
+    buf.seek(0)
+    saved = torch.load(buf, weights_only=True)
+    masters = opt.master_params()
+    moments = [(s.m.to_fp32(), None if s.v is None else s.v.to_fp32()) for s in opt._ordered]
+    for sd in (on_device, saved):
+        other = cls(TinyLM().to(DEV).to(torch.bfloat16).parameters(), lr=3e-3, precision=precision)
+        other.load_state_dict(sd)
+        assert all(torch.equal(x, y) for x, y in zip(masters, other.master_params()))
+        for (m, v), s in zip(moments, other._ordered):
+            assert torch.equal(m, s.m.to_fp32()) and (v is None or torch.equal(v, s.v.to_fp32()))
+            assert s.step == 3
+        other.close()
+    opt.close()
+
+
 @pytest.mark.parametrize("precision", ["bf16", "fp8"])
 def test_packed_state_checkpoint_and_set_precision(precision):
     """Checkpoints of the interleaved layouts are the reference format and load into either layout;
