@@ -106,8 +106,7 @@ def build(cfg: dict, device, seed: int = 0, layout: str = "auto", double_buffer:
 
     # Allocated in the order a training job allocates them: every weight when the model is built, the
     # gradients during the first backward pass (last layer first), the optimizer state at the first
-    # step.  (Allocating each weight next to its gradient instead puts the 7B bf16-moment step at
-    # 20.9-21.5 ms per launch, against 20.7-20.8 in this order.)
+    # step.
     gen = torch.Generator(device=device).manual_seed(seed)
     shapes = [shape for _, shape in cfg["shapes"]()]
     params = [torch.nn.Parameter(torch.randn(shape, generator=gen, device=device, dtype=torch.bfloat16).mul_(0.02))
