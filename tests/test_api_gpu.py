@@ -4,7 +4,6 @@ test_hardening.py, test_lion.py, test_gpu_state.py), plus chunked segments throu
 import copy
 import ctypes
 
-import numpy as np
 import pytest
 import torch
 

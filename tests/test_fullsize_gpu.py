@@ -20,7 +20,6 @@ by chunk (host memory bounded by one chunk) for comparison with what the launch 
 
 from __future__ import annotations
 
-import math
 import sys
 from pathlib import Path
 

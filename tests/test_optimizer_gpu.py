@@ -5,7 +5,6 @@ oracle (parameter index, step counting, lazy state and seeds included).
 """
 
 import copy
-import ctypes
 import io
 
 import numpy as np
