@@ -510,7 +510,8 @@ def main() -> int:
     ap.add_argument("--config", default="c3p", choices=sorted(CONFIGS) + ["c5"],
                     help="c5: the hooked training pipeline (prints its own JSON line)")
     ap.add_argument("--cpu-params", type=int, default=1 << 30, help="CPU baseline sample size (parameters)")
-    ap.add_argument("--cpu-steps", type=int, default=10)
+    ap.add_argument("--cpu-steps", type=int, default=80,
+                    help="timed steps of each CPU-baseline run (about 10 s of CPU work at the default sample)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-copy-ceiling", action="store_true",
                     help="skip timing a plain copy of the update's bytes (the copy_ceiling object)")
