@@ -55,3 +55,38 @@ def test_noalloc_matches_multi_step_on_two_calls(order):
         for w, g, o in zip(want, got, oracle):
             assert not O.outputs_equal(w, g), f"noalloc differs from multi_step ({count} segments)"
             assert not O.outputs_equal(o, g), f"noalloc differs from the oracle ({count} segments)"
+
+
+def test_noalloc_call_with_device_tables_replays_from_a_graph():
+    """Under stream capture, where a pooled call that needs a segment table is refused (its table
+    would come from a reused host slot at replay), the allocation-free call is captured whole: its
+    tables are written by kernels whose arguments carry the descriptors.  Each of three replays --
+    with eager work and synchronisations between them -- applies the same step again and is checked
+    against the oracle on the previous state."""
+    from hip_cases import Prepared
+
+    rng = np.random.default_rng(83)
+    kernels = _hip.load()
+    warm = Prepared(mixed_cases(rng, 12, 1, seed=5))
+    kernels.multi_step_noalloc(torch.cuda.current_stream(), warm.arr)   # device array located before capture
+    torch.cuda.synchronize()
+    cases = mixed_cases(rng, 40, 2, seed=9)   # 20 segments of each of two variants: device tables
+    mine = Prepared(cases)
+    graph = torch.cuda.CUDAGraph()
+    side = torch.zeros(1024, device="cuda")
+    with torch.cuda.graph(graph):
+        kernels.multi_step_noalloc(torch.cuda.current_stream(), mine.arr)
+        side.add_(1.0)
+    torch.cuda.synchronize()
+    state = mine.collect()   # capturing ran nothing
+    for w, g in zip(cases, state):
+        assert not O.outputs_equal(w, g), "the capture changed the state"
+    for replay in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        want = O.run_many(state, "oracle", 16)
+        state = mine.collect()
+        for w, g in zip(want, state):
+            assert not O.outputs_equal(w, g), f"replay {replay} differs from the oracle"
+        side.mul_(0.5)   # eager work between replays
+        torch.cuda.synchronize()
