@@ -122,6 +122,16 @@ class _Registry:
         return [s for s in self.ordered if not s.submitted and s.param.grad is not None
                 and (include_small or s.small is None)]
 
+    def hook_targets(self, params: Iterable[torch.Tensor] | None = None) -> list[torch.Tensor]:
+        """The parameters that get a gradient hook: those of ``params`` (default: every registered one)
+        that take gradients and are not updated in a small-parameter batch."""
+        slots = self.ordered if params is None else [self.by_param[p] for p in params if p in self.by_param]
+        return [s.param for s in slots if s.param.requires_grad and s.small is None]
+
+    def new_step(self) -> None:
+        for slot in self.ordered:
+            slot.submitted = False
+
 
 class _StepWindow:
     """What the gradient hooks may do in the current step (optimizer.py:285-304): nothing inside
@@ -133,6 +143,27 @@ class _StepWindow:
         self.suppressed = 0      # no_sync nesting depth
         self.backwards = 0       # backward passes finished since the last step
         self.counting = False    # an end-of-backward callback is queued
+        self.closed = 0          # steps closed without an error
+
+    @contextlib.contextmanager
+    def suppress(self):
+        """Hooks do nothing inside (nestable)."""
+        self.suppressed += 1
+        try:
+            yield
+        finally:
+            self.suppressed -= 1
+
+    @contextlib.contextmanager
+    def closing(self, registry: _Registry):
+        """Close a step: whatever happens inside, the next one starts with no parameter marked as
+        updated and no backward pass counted; a step closed without an error is counted."""
+        try:
+            yield
+        finally:
+            registry.new_step()
+            self.backwards = 0
+        self.closed += 1
 
     def hook_may_update(self) -> bool:
         if self.suppressed:
@@ -147,9 +178,6 @@ class _StepWindow:
     def _backward_finished(self) -> None:
         self.backwards += 1
         self.counting = False
-
-    def restart(self) -> None:
-        self.backwards = 0
 
 
 class _HookSet:
@@ -185,23 +213,30 @@ class _CheckpointReader:
     checkpoint may come from another model, another version or an untrusted source)."""
 
     def __init__(self, state_dict: dict[str, Any], slots: list[ParamSlot], lion: bool):
-        entries = {}
-        for key, entry in state_dict["state"].items():
-            index = int(key) if isinstance(key, str) and key.isdigit() else key
-            if type(index) is not int or not 0 <= index < len(slots):
-                raise ValueError(f"checkpoint state for parameter {index!r}: this optimizer has parameters "
-                                 f"0..{len(slots) - 1}")
-            entries[index] = entry
-        for index, entry in entries.items():
-            numel = slots[index].numel
-            if entry.get("master") is not None:
-                check_master_state(entry["master"], numel, f"master weights of parameter {index}")
-            for key in ("exp_avg", "exp_avg_sq"):
-                if isinstance(entry.get(key), torch.Tensor):
-                    _checked(entry[key], numel, f"{key} of parameter {index}")
-            if not lion and "exp_avg_sq" not in entry:
-                raise ValueError("checkpoint has no exp_avg_sq (saved by LionBridge?); AdamW needs both moments")
-        self.entries = entries
+        self.entries = {self._index(key, len(slots)): entry for key, entry in state_dict["state"].items()}
+        for index, entry in self.entries.items():
+            self._validate(index, entry, slots[index].numel, lion)
+
+    @staticmethod
+    def _index(key: Any, count: int) -> int:
+        """The parameter index a state key names (string keys come back from JSON round trips)."""
+        index = int(key) if isinstance(key, str) and key.isdigit() else key
+        if type(index) is int and 0 <= index < count:
+            return index
+        raise ValueError(f"checkpoint state for parameter {index!r}: this optimizer has parameters 0..{count - 1}")
+
+    @staticmethod
+    def _validate(index: int, entry: dict[str, Any], numel: int, lion: bool) -> None:
+        """Sizes and formats of one entry: its master (tensor or store dictionary), its plain-tensor
+        moments (the torch.optim.AdamW layout; store dictionaries are checked when rebuilt), and the
+        second moment AdamW needs."""
+        if entry.get("master") is not None:
+            check_master_state(entry["master"], numel, f"master weights of parameter {index}")
+        plain = {k: v for k, v in entry.items() if k in ("exp_avg", "exp_avg_sq") and isinstance(v, torch.Tensor)}
+        for key, tensor in plain.items():
+            _checked(tensor, numel, f"{key} of parameter {index}")
+        if not lion and "exp_avg_sq" not in entry:
+            raise ValueError("checkpoint has no exp_avg_sq (saved by LionBridge?); AdamW needs both moments")
 
     @staticmethod
     def moment(saved: Any, numel: int, role: str, precision: str, device):
@@ -302,7 +337,6 @@ class AdamBridge(torch.optim.Optimizer):
         self._registry = _Registry()
         self._window = _StepWindow(accumulation_steps)
         self._hooks = _HookSet(self._on_grad_ready)
-        self._steps_synced = 0
         self._autotune_log: list[str] = []
         if autotune:
             self._autotune_log.append("autotune: nothing to tune on the GPU (no host threads, one kernel launch)")
@@ -353,9 +387,7 @@ class AdamBridge(torch.optim.Optimizer):
         """Update each parameter as soon as its gradient is ready (optimizer.py:255-269): the
         parameters of ``model`` (default: all) that require gradients and are not small."""
         if not self._hooks.active:
-            keep = None if model is None else {id(p) for p in model.parameters()}
-            self._hooks.add(s.param for s in self._ordered
-                            if s.param.requires_grad and s.small is None and (keep is None or id(s.param) in keep))
+            self._hooks.add(self._registry.hook_targets(None if model is None else model.parameters()))
             self._hooks.active = True
         return self
 
@@ -366,14 +398,9 @@ class AdamBridge(torch.optim.Optimizer):
     def _hooked(self) -> bool:
         return self._hooks.active
 
-    @contextlib.contextmanager
     def no_sync(self):
-        """Accumulate gradients without updating (every micro-batch but the last)."""
-        self._window.suppressed += 1
-        try:
-            yield
-        finally:
-            self._window.suppressed -= 1
+        """Accumulate gradients without updating (every micro-batch but the last): a context manager."""
+        return self._window.suppress()
 
     def _on_grad_ready(self, p: torch.Tensor) -> None:
         """The hook (optimizer.py:291-304): update ``p`` now, unless the step window says otherwise."""
@@ -402,27 +429,27 @@ class AdamBridge(torch.optim.Optimizer):
         and with gradient accumulation any parameter whose window the step cut short -- then order
         every update before subsequent work on the current stream (a stream wait, not a host wait;
         with delayed updates, only the write-backs)."""
-        try:
+        with self._window.closing(self._registry):
             if not self._window.suppressed:
-                if self.accumulation_steps > 1:
-                    late = self._registry.pending(include_small=False)
-                    if late:
-                        self._submit(late, [s.param.grad for s in late], hooked=False, release=False)
-                release = self.release_grads and self._hooks.active
-                for batch in self._registry.small:
-                    live = [s for s in batch.slots if not s.submitted and s.param.grad is not None]
-                    if live:
-                        self._submit(live, [s.param.grad for s in live], hooked=self._hooks.active, release=release)
+                self._update_leftovers()
             stats = self._engine.finish_step()
-        finally:
-            for slot in self._ordered:
-                slot.submitted = False
-            self._window.restart()
         self.last_step_stats = stats
-        self._steps_synced += 1
-        if self.delay_updates and self._steps_synced >= self.delay_warmup_steps:
-            self._engine.delay = True
+        if self.delay_updates and self._window.closed >= self.delay_warmup_steps:
+            self._engine.delay = True   # the warm-up steps are over (optimizer.py:349-350)
         return stats
+
+    def _update_leftovers(self) -> None:
+        """What the hooks did not update: with gradient accumulation, the parameters whose window the
+        step cut short; the small parameters, one launch per device."""
+        if self.accumulation_steps > 1:
+            late = self._registry.pending(include_small=False)
+            if late:
+                self._submit(late, [s.param.grad for s in late], hooked=False, release=False)
+        release = self.release_grads and self._hooks.active
+        for batch in self._registry.small:
+            live = [s for s in batch.slots if not s.submitted and s.param.grad is not None]
+            if live:
+                self._submit(live, [s.param.grad for s in live], hooked=self._hooks.active, release=release)
 
     def flush(self) -> None:
         """Apply every pending (delayed) update to the parameters (optimizer.py:432-436)."""
@@ -547,12 +574,12 @@ class AdamBridge(torch.optim.Optimizer):
     def close(self) -> None:
         """Apply pending delayed updates and release the engine (optimizer.py:604-612)."""
         self.detach_hooks()
-        if not self._finalizer.alive:
+        if self._finalizer.detach() is None:   # closed before
             return
         try:
             self._engine.flush()
         finally:
-            self._finalizer()
+            self._engine.close()
 
 
 OptiComputeAdamW = AdamBridge
