@@ -341,6 +341,15 @@ class UpdateEngine:
         lanes = self.lanes(device)
         with torch.cuda.device(device):
             current = torch.cuda.current_stream(device)
+            for slot, g in zip(slots, grads):
+                if g.numel() != slot.numel:
+                    raise ValueError(f"gradient of parameter {slot.index} has {g.numel()} elements, "
+                                     f"expected {slot.numel}")
+                if g.device != device:
+                    raise ValueError(f"gradient of parameter {slot.index} is on {g.device}, parameter on {device}")
+            # A strided gradient is read from a contiguous copy (logical order), made on the compute
+            # stream before `ready` is recorded, so that the update waits for it.
+            grads = [g if g.is_contiguous() else g.contiguous() for g in grads]
             fresh = [s for s in slots if not s.initialized]
             if fresh:                              # built on the compute stream, before `ready`
                 self.initialize(fresh)
@@ -359,13 +368,6 @@ class UpdateEngine:
                         self._fresh[slot] = None
                 if owed:
                     lanes.side.wait_event(self._write_back(device, owed, ready))
-            grads = [g if g.is_contiguous() else g.contiguous() for g in grads]
-            for slot, g in zip(slots, grads):
-                if g.numel() != slot.numel:
-                    raise ValueError(f"gradient of parameter {slot.index} has {g.numel()} elements, "
-                                     f"expected {slot.numel}")
-                if g.device != device:
-                    raise ValueError(f"gradient of parameter {slot.index} is on {g.device}, parameter on {device}")
             structs: dict[int, _hip.Group] = {}   # each group's hyperparameters, read once per launch
             for slot in slots:
                 slot.step += 1

@@ -164,6 +164,45 @@ def test_hooked_and_grouped_parameters_match_torch_adamw(threshold):
     opt.close()
 
 
+@pytest.mark.parametrize("mode", ["step", "hooks", "hooks-deferred", "delayed"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_strided_parameters_update_like_contiguous_ones(dtype, mode):
+    """A parameter stored transposed, whose gradient autograd lays out the same way, gets the updates of
+    a contiguous parameter holding the same values, bit for bit: the update reads the gradient in
+    logical order from a contiguous copy made before the update is ordered after the compute stream,
+    writes the new weights to a buffer of its own and copies them into the strided parameter."""
+    torch.manual_seed(0)
+    base = [torch.randn(48, 300, device=DEV).to(dtype), torch.randn(300, device=DEV).to(dtype)]
+    flat = [torch.nn.Parameter(base[0].clone()), torch.nn.Parameter(base[1].clone())]
+    strided = [torch.nn.Parameter(base[0].t().contiguous().t()), torch.nn.Parameter(base[1].clone())]
+    assert not strided[0].is_contiguous() and torch.equal(strided[0], flat[0])
+    kw = dict(lr=1e-2, weight_decay=0.1, small_param_threshold=0, overlap_writeback=mode != "hooks-deferred",
+              delay_updates=mode == "delayed", delay_warmup_steps=1)
+    opts = [ab.AdamBridge(ps, **kw) for ps in (flat, strided)]
+    hooked = mode != "step"
+    if hooked:
+        for opt in opts:
+            opt.attach_hooks()
+    gen = torch.Generator(device=DEV).manual_seed(1)
+    for step in range(6):
+        x = torch.randn(64, 48, device=DEV, generator=gen).to(dtype)
+        for ps, opt in zip((flat, strided), opts):
+            opt.zero_grad(set_to_none=True)
+            # the same GEMM for both (contiguous operands); the strided parameter's gradient is then
+            # laid out like the parameter by autograd
+            (x @ ps[0].contiguous() + ps[1]).float().pow(2).mean().backward()
+            if hooked:
+                opt.step_sync()
+            else:
+                assert ps is flat or not ps[0].grad.is_contiguous()
+                opt.step()
+    for opt in opts:
+        opt.close()
+    for a, b in zip(flat, strided):
+        assert torch.equal(a, b)
+    assert not torch.equal(flat[0], base[0])
+
+
 def _stale_reference(model, steps, make_opt, warmup):
     """Losses and final weights of an optimizer whose updates reach the model one step late after
     ``warmup`` exact steps (reference test_cuda.py:129-152)."""
