@@ -44,8 +44,14 @@ sys.path.insert(0, str(ROOT))
 METRIC = "params updated/sec and achieved HBM GB/s (% roofline), AdamW bf16 moments @7B"
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the update kernel, measured with rocprofv3 FETCH_SIZE + WRITE_SIZE, each
-# scaled by its reading for a copy of known size (profiles/*_hbm_traffic.md).
+# scaled by its reading for a copy of known size, in separate profiling runs of this script (the
+# counters cannot be read from inside the process they profile); each figure's run is in its file.
 MEASURED_TRAFFIC = {"c3p": 134.767e9, "c1": 469.84e6, "c2": 9.8808e9, "c3": 108.67e9, "c4": 24.700e9}
+TRAFFIC_PROFILE = {"c3p": "profiles/k_update_packed_c3p_hbm_traffic.md",
+                   "c1": "profiles/k_update_c1_packed_c2_trace_traffic.md",
+                   "c2": "profiles/k_update_c1_packed_c2_trace_traffic.md",
+                   "c3": "profiles/k_update_fp8_c3_trace_traffic_instructions.md",
+                   "c4": "profiles/k_update_lion_rec_c4_trace_traffic.md"}
 
 
 # ------------------------------------------------------------ parameter lists
@@ -604,6 +610,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": g["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": g["achieved_gbs"] / HBM_PEAK_GBS,
                      "traffic": args.traffic if args.traffic is not None else MEASURED_TRAFFIC.get(args.config),
+                     "traffic_source": "--traffic" if args.traffic is not None else TRAFFIC_PROFILE.get(args.config),
                      "kernel_ms": g["kernel_ms"]},
         "copy_ceiling": ceiling,
         "placement": placement,
