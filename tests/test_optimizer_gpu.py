@@ -203,9 +203,10 @@ def test_strided_parameters_update_like_contiguous_ones(dtype, mode):
     assert not torch.equal(flat[0], base[0])
 
 
-def _stale_reference(model, steps, make_opt, warmup):
+def _stale_reference(model, steps, make_opt, warmup, micro=1):
     """Losses and final weights of an optimizer whose updates reach the model one step late after
-    ``warmup`` exact steps (reference test_cuda.py:129-152)."""
+    ``warmup`` exact steps (reference test_cuda.py:129-152); with ``micro`` > 1, each step
+    accumulates the gradients of ``micro`` backward passes (seeds 10 k + j) on the same weights."""
     master = copy.deepcopy(model).float()
     ref = make_opt(master.parameters())
     snapshots = [[p.detach().clone() for p in master.parameters()]]
@@ -216,9 +217,10 @@ def _stale_reference(model, steps, make_opt, warmup):
             for p, w in zip(model.parameters(), snapshots[lag]):
                 p.copy_(w)
         model.zero_grad()
-        loss = lm_loss(model, k)
-        loss.backward()
-        losses.append(loss.item())
+        for j in range(micro):
+            loss = lm_loss(model, k if micro == 1 else 10 * k + j)
+            loss.backward()
+            losses.append(loss.item())
         for p, q in zip(master.parameters(), model.parameters()):
             p.grad = q.grad.float()
         ref.step()
@@ -247,6 +249,31 @@ def test_delayed_updates_match_one_step_stale_adamw(warmup, precision):
     assert max(abs(a - b) for a, b in zip(losses, want_losses)) < tol
     assert max((p - w).abs().max().item() for p, w in zip(model.parameters(), want)) < (
         1e-5 if precision == "fp32" else 1e-2)
+    opt.close()
+
+
+@pytest.mark.parametrize("warmup", [0, 2])
+def test_delayed_updates_with_accumulation_match_stale_accumulated_adamw(warmup):
+    """Delayed updates with accumulation_steps=2 and batched small parameters (reference
+    tests/test_gpu_state.py:99-114, which checks only that the weights stay finite): the weights
+    follow AdamW on the accumulated gradients, one step stale after the warm-up steps."""
+    torch.manual_seed(0)
+    model = TinyLM().to(DEV)
+    want_losses, want = _stale_reference(copy.deepcopy(model), 6, lambda ps: torch.optim.AdamW(ps, lr=3e-3), warmup,
+                                         micro=2)
+    opt = ab.AdamBridge(model.parameters(), lr=3e-3, delay_updates=True, delay_warmup_steps=warmup,
+                        accumulation_steps=2, small_param_threshold=2000).attach_hooks(model)
+    assert any(s.small is not None for s in opt._ordered) and any(s.small is None for s in opt._ordered)
+    losses = []
+    for k in range(1, 7):
+        for j in range(2):
+            loss = lm_loss(model, 10 * k + j)
+            loss.backward()
+            losses.append(loss.item())
+        opt.step_sync()
+    opt.flush()
+    assert max(abs(a - b) for a, b in zip(losses, want_losses)) < 1e-4
+    assert max((p - w).abs().max().item() for p, w in zip(model.parameters(), want)) < 1e-5
     opt.close()
 
 
