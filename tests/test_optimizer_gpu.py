@@ -497,6 +497,43 @@ def test_params_without_grad_are_skipped():
     opt.close()
 
 
+@pytest.mark.parametrize("hooks", [False, True])
+def test_param_group_added_after_steps_trains_like_torch_adamw(hooks):
+    """add_param_group between steps (reference optimizer.py:225-237): the new parameters take the
+    next indices and their own hyperparameters, and are hooked when hooks are attached."""
+    ref_model = tiny_mlp(device=DEV)
+    model = copy.deepcopy(ref_model)
+
+    def first(m):
+        return [m[0].weight, m[0].bias]
+
+    def second(m):
+        return {"params": [m[2].weight, m[2].bias, m[3].weight, m[3].bias], "lr": 3e-3, "weight_decay": 0.1}
+
+    ref = torch.optim.AdamW(first(ref_model), lr=1e-2, weight_decay=0.0)
+    opt = ab.AdamBridge(first(model), lr=1e-2, weight_decay=0.0, small_param_threshold=0)
+    if hooks:
+        opt.attach_hooks()
+    torch.manual_seed(1)
+    for step in range(6):
+        if step == 2:
+            ref.add_param_group(second(ref_model))
+            opt.add_param_group(second(model))
+            assert [s.index for s in opt._ordered] == list(range(6))
+        x = torch.randn(16, 48, device=DEV)
+        for m, o in ((ref_model, ref), (model, opt)):
+            o.zero_grad(set_to_none=True)
+            m(x).pow(2).mean().backward()
+            if o is opt and hooks:
+                if step >= 2:   # the added parameters were updated by their hooks
+                    assert model[3].weight.grad is None
+                o.step_sync()
+            else:
+                o.step()
+    assert max_param_diff(ref_model, model) < 1e-6
+    opt.close()
+
+
 def test_weights_loaded_after_construction_are_respected():
     """reference test_optimizer.py:141-150: lazy master."""
     model = tiny_mlp(seed=0, device=DEV)
