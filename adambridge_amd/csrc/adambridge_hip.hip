@@ -74,12 +74,13 @@ struct DevSeg {
     int64_t n_main;      // [0, n_main) take the fused form, [n_main, n) the scalar-tail form
     int64_t tile_begin;  // first tile of this segment in the launch
     uint32_t idx0;       // uint32(offset): element i draws rounding bits at idx0 + i
-    uint32_t flags;      // kVec: every pointer allows 16-byte access; kSR: stochastic rounding
+    uint32_t flags;      // kVec: every pointer allows 16-byte access; kSR: stochastic rounding;
+                         // kPrev: out receives the weight of the master before the update
     Coef c;
     uint32_t seed_m, seed_v, seed_p, pad;
 };
 static_assert(sizeof(DevSeg) == 144, "DevSeg layout");
-constexpr uint32_t kVec = 1u, kSR = 2u;
+constexpr uint32_t kVec = 1u, kSR = 2u, kPrev = 4u;
 
 struct Launch {
     const DevSeg* table;     // device table when nsegs > kInline
@@ -420,6 +421,7 @@ __device__ __forceinline__ void update_tile(const DevSeg& s, int64_t tile, int64
     const int64_t hi = lo + T < n ? lo + T : n;
     const Coef c = s.c;
     const int64_t nvec = (s.flags & kVec) ? (n_main & ~(int64_t)1) : 0;
+    const bool prev = (s.flags & kPrev) != 0;   // uniform: out from the master as loaded
     int64_t vend = hi < nvec ? hi : nvec;
     if (vend < lo) vend = lo;
 
@@ -431,6 +433,7 @@ __device__ __forceinline__ void update_tile(const DevSeg& s, int64_t tile, int64
         load2<MV>(s.m, i, m0, m1);
         if constexpr (ALGO == ALGO_ADAMW) load2<MV>(s.v, i, v0, v1);
         load_master2<PT>(s, i, p0, p1);
+        if (prev) store_out2<OT>(s.out, i, p0, p1);
         if constexpr (ALGO == ALGO_ADAMW) {
             p0 = adamw<true>(p0, g0, m0, v0, c);
             p1 = adamw<true>(p1, g1, m1, v1, c);
@@ -441,7 +444,7 @@ __device__ __forceinline__ void update_tile(const DevSeg& s, int64_t tile, int64
         store_master2<PT, SR>(s, i, p0, p1, idx);
         store_moment2<MV, SR>(s.m, i, m0, m1, idx, s.seed_m);
         if constexpr (ALGO == ALGO_ADAMW) store_moment2<MV, SR>(s.v, i, v0, v1, idx, s.seed_v);
-        store_out2<OT>(s.out, i, p0, p1);
+        if (!prev) store_out2<OT>(s.out, i, p0, p1);
     }
     // the rest one element per lane: misaligned buffers, a ragged end, the scalar tail
     for (int64_t i = vend + threadIdx.x; i < hi; i += kThreads) {
@@ -449,6 +452,7 @@ __device__ __forceinline__ void update_tile(const DevSeg& s, int64_t tile, int64
         const float g = load1<GT>(s.g, i);
         float m = load1<MV>(s.m, i);
         float p = load_master1<PT>(s, i);
+        if (prev) store_out1<OT>(s.out, i, p);
         if constexpr (ALGO == ALGO_ADAMW) {
             float v = load1<MV>(s.v, i);
             p = adamw_sel(p, g, m, v, c, i < n_main);
@@ -458,7 +462,7 @@ __device__ __forceinline__ void update_tile(const DevSeg& s, int64_t tile, int64
         }
         p = store_master1<PT, SR>(s, i, p, idx);
         store_moment1<MV, SR>(s.m, i, m, SR ? hash32(idx ^ s.seed_m) : 0u);
-        store_out1<OT>(s.out, i, p);
+        if (!prev) store_out1<OT>(s.out, i, p);
     }
 }
 
@@ -600,7 +604,7 @@ __device__ __forceinline__ float block_scale(float amax)
 // FULL: the whole block lies inside the segment, takes the fused form and allows vector access --
 // straight-line code.  FULL is the same for the 16 lanes of a block, so the DPP maxima below always
 // run with the whole group active.
-template <int ALGO, int PT, int GT, int OT, bool SR, bool FULL>
+template <int ALGO, int PT, int GT, int OT, bool SR, bool FULL, bool PREV>
 __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_t b0, int lane)
 {
     constexpr bool kLion = ALGO == ALGO_LION;
@@ -632,12 +636,14 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     if (full) {
         load8<GT>(s.g, e0, g);
         load_master8<PT>(s, e0, p);
+        if constexpr (PREV) store_out8<OT>(s.out, e0, p);   // out from the master as loaded
     } else {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const bool in = e0 + k < n;
             g[k] = in ? load1<GT>(s.g, e0 + k) : 0.0f;
             p[k] = in ? load_master1<PT>(s, e0 + k) : 0.0f;
+            if (PREV && in) store_out1<OT>(s.out, e0 + k, p[k]);
         }
     }
     {
@@ -670,13 +676,13 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     }
     if (full) {
         store_master8<PT, SR>(s, e0, p, idx);
-        store_out8<OT>(s.out, e0, p);
+        if constexpr (!PREV) store_out8<OT>(s.out, e0, p);
     } else {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             if (e0 + k < n) {
                 const float stored = store_master1<PT, SR>(s, e0 + k, p[k], idx + k);
-                store_out1<OT>(s.out, e0 + k, stored);
+                if (!PREV) store_out1<OT>(s.out, e0 + k, stored);
             }
         }
     }
@@ -758,7 +764,7 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     }
 }
 
-template <int ALGO, int PT, int GT, int OT, bool SR>
+template <int ALGO, int PT, int GT, int OT, bool SR, bool PREV>
 __device__ __forceinline__ void update_tile_fp8(const DevSeg& s, int64_t tile, int64_t T)
 {
     constexpr bool kLion = ALGO == ALGO_LION;
@@ -774,16 +780,16 @@ __device__ __forceinline__ void update_tile_fp8(const DevSeg& s, int64_t tile, i
     if (T == kFp8Quantum) {
         const int64_t b0 = (tile - s.tile_begin) * kFp8Quantum + group * kFp8Block;
         if (b0 >= s.n) return;
-        if (vec && b0 + kFp8Block <= full_end) fp8_block<ALGO, PT, GT, OT, SR, true>(s, c, b0, lane);
-        else fp8_block<ALGO, PT, GT, OT, SR, false>(s, c, b0, lane);
+        if (vec && b0 + kFp8Block <= full_end) fp8_block<ALGO, PT, GT, OT, SR, true, PREV>(s, c, b0, lane);
+        else fp8_block<ALGO, PT, GT, OT, SR, false, PREV>(s, c, b0, lane);
         return;
     }
     const int64_t lo = (tile - s.tile_begin) * T;
     const int64_t hi = lo + T < s.n ? lo + T : s.n;
     // larger tiles (ADAMBRIDGE_TILE_FP8): each 16-lane group walks every 16th block of the tile
     for (int64_t b0 = lo + group * kFp8Block; b0 < hi; b0 += (kThreads / 16) * kFp8Block) {
-        if (vec && b0 + kFp8Block <= full_end) fp8_block<ALGO, PT, GT, OT, SR, true>(s, c, b0, lane);
-        else fp8_block<ALGO, PT, GT, OT, SR, false>(s, c, b0, lane);
+        if (vec && b0 + kFp8Block <= full_end) fp8_block<ALGO, PT, GT, OT, SR, true, PREV>(s, c, b0, lane);
+        else fp8_block<ALGO, PT, GT, OT, SR, false, PREV>(s, c, b0, lane);
     }
 }
 
@@ -793,8 +799,17 @@ __global__ __launch_bounds__(kThreads) void k_update_fp8(Launch L)
     const int64_t tile = block_tile(L);
     if (tile >= L.ntiles) return;
     const DevSeg s = find_segment(L, tile);
-    if (s.flags & kSR) update_tile_fp8<ALGO, PT, GT, OT, true>(s, tile, L.tile);
-    else update_tile_fp8<ALGO, PT, GT, OT, false>(s, tile, L.tile);
+    // the out-from-previous-master form is its own instantiation: a runtime test inside the block
+    // code cost this VALU-heavy kernel 6% (measured on the 7B FP8 step)
+    if (s.flags & kPrev) {
+        if constexpr (OT != DT_NONE) {
+            if (s.flags & kSR) update_tile_fp8<ALGO, PT, GT, OT, true, true>(s, tile, L.tile);
+            else update_tile_fp8<ALGO, PT, GT, OT, false, true>(s, tile, L.tile);
+        }
+        return;
+    }
+    if (s.flags & kSR) update_tile_fp8<ALGO, PT, GT, OT, true, false>(s, tile, L.tile);
+    else update_tile_fp8<ALGO, PT, GT, OT, false, false>(s, tile, L.tile);
 }
 
 // ------------------------------------------------- packed AdamW state kernel
@@ -829,6 +844,17 @@ __device__ __forceinline__ void adamw_pair_tail(const DevSeg& s, int64_t i, u32x
     o1 = p[1];
 }
 
+// The working weights of elements i and (if both) i + 1.
+template <int OT>
+__device__ __forceinline__ void store_pair_out(void* out, int64_t i, bool vec2, bool both, float o0, float o1)
+{
+    if (vec2) store_out2<OT>(out, i, o0, o1);
+    else {
+        store_out1<OT>(out, i, o0);
+        if (both) store_out1<OT>(out, i + 1, o1);
+    }
+}
+
 template <int GT, int OT, bool SR>
 __device__ __forceinline__ void update_tile_packed(const DevSeg& s, int64_t tile, int64_t T)
 {
@@ -837,6 +863,7 @@ __device__ __forceinline__ void update_tile_packed(const DevSeg& s, int64_t tile
     const u32x4* __restrict__ src = static_cast<const u32x4*>(s.p);
     u32x4* __restrict__ dst = reinterpret_cast<u32x4*>(s.p_lo);
     const bool vec = (s.flags & kVec) != 0;   // g and out allow 2-element access
+    const bool prev = (s.flags & kPrev) != 0;  // uniform: out from the master as loaded
     const int64_t lo = (tile - s.tile_begin) * T;
     const int64_t hi = lo + T < n ? lo + T : n;
     for (int64_t i = lo + threadIdx.x * 2; i < hi; i += kThreads * 2) {
@@ -850,6 +877,7 @@ __device__ __forceinline__ void update_tile_packed(const DevSeg& s, int64_t tile
             g0 = load1<GT>(s.g, i);
             if (both) g1 = load1<GT>(s.g, i + 1);
         }
+        if (prev) store_pair_out<OT>(s.out, i, vec && both, both, bitsf(x.x), bitsf(x.y));
         float o0, o1;
         if (i + 2 <= n_main) {
             float p0 = bitsf(x.x), p1 = bitsf(x.y);
@@ -867,11 +895,7 @@ __device__ __forceinline__ void update_tile_packed(const DevSeg& s, int64_t tile
             adamw_pair_tail(s, i, x, g0, g1, both ? 2 : 1, idx, SR, n_main, o0, o1);
         }
         st(dst + pair, x);
-        if (vec && both) store_out2<OT>(s.out, i, o0, o1);
-        else {
-            store_out1<OT>(s.out, i, o0);
-            if (both) store_out1<OT>(s.out, i + 1, o1);
-        }
+        if (!prev) store_pair_out<OT>(s.out, i, vec && both, both, o0, o1);
     }
 }
 
@@ -903,6 +927,20 @@ __global__ __launch_bounds__(kThreads) void k_update_packed(Launch L)
 constexpr int64_t kLionRecordElems = 256;
 constexpr int64_t kLionRecordBytes = 1536;
 
+// The working weights of elements i .. i + 3 below n, from FP32 bits.
+template <int OT>
+__device__ __forceinline__ void store_quad_out(void* out, int64_t i, int64_t n, bool vec4, const uint32_t (&p)[4])
+{
+    if (vec4) {
+        store_out2<OT>(out, i, bitsf(p[0]), bitsf(p[1]));
+        store_out2<OT>(out, i + 2, bitsf(p[2]), bitsf(p[3]));
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (i + k < n) store_out1<OT>(out, i + k, bitsf(p[k]));
+    }
+}
+
 template <int GT, int OT, bool SR>
 __device__ __forceinline__ void update_tile_lion_rec(const DevSeg& s, int64_t tile, int64_t T)
 {
@@ -911,6 +949,7 @@ __device__ __forceinline__ void update_tile_lion_rec(const DevSeg& s, int64_t ti
     const uint8_t* __restrict__ src = static_cast<const uint8_t*>(s.p);
     uint8_t* __restrict__ dst = s.p_lo;
     const bool vec = (s.flags & kVec) != 0;   // g and out allow 2-element access
+    const bool prev = (s.flags & kPrev) != 0;  // uniform: out from the master as loaded
     const int64_t lo = (tile - s.tile_begin) * T;
     const int64_t hi = lo + T < n ? lo + T : n;
     for (int64_t i = lo + threadIdx.x * 4; i < hi; i += kThreads * 4) {
@@ -933,6 +972,7 @@ __device__ __forceinline__ void update_tile_lion_rec(const DevSeg& s, int64_t ti
         }
         const uint32_t p_in[4] = {pw.x, pw.y, pw.z, pw.w};
         const uint32_t m_in[4] = {mw.x & 0xffffu, mw.x >> 16, mw.y & 0xffffu, mw.y >> 16};
+        if (prev) store_quad_out<OT>(s.out, i, n, vec && all, p_in);
         uint32_t p_out[4], m_out[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -944,14 +984,7 @@ __device__ __forceinline__ void update_tile_lion_rec(const DevSeg& s, int64_t ti
         }
         st(reinterpret_cast<u32x4*>(dst + at), u32x4{p_out[0], p_out[1], p_out[2], p_out[3]});
         st(reinterpret_cast<u32x2*>(dst + at_m), u32x2{m_out[0] | (m_out[1] << 16), m_out[2] | (m_out[3] << 16)});
-        if (vec && all) {
-            store_out2<OT>(s.out, i, bitsf(p_out[0]), bitsf(p_out[1]));
-            store_out2<OT>(s.out, i + 2, bitsf(p_out[2]), bitsf(p_out[3]));
-        } else {
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                if (i + k < n) store_out1<OT>(s.out, i + k, bitsf(p_out[k]));
-        }
+        if (!prev) store_quad_out<OT>(s.out, i, n, vec && all, p_out);
     }
 }
 

@@ -8,14 +8,19 @@ parameters in place; what is left to the host is ordering and bookkeeping.
 
 Streams and events take the place of the reference's threads::
 
-    compute stream        side stream                 write-back stream (delayed mode)
-    --------------        -----------                 --------------------------------
+    compute stream        side stream                 write-back stream
+    --------------        -----------                 -----------------
     grad ready  -------->  wait `ready`
-    (backward goes on)     [wait `written`]  <-------  wait `ready` + previous update: out -> param
-                           fused update (one launch)
-                           record `done`
-    step_sync: current stream waits for the side stream (exact mode)
-               or for the write-back stream only (delayed mode)
+    (backward goes on)     fused update (one launch)
+                           record `done`  ---------->  [at step_sync: wait `done`; buffered
+                                                        weights -> parameters]
+    step_sync: current stream waits for both
+
+Delayed updates (``delay``) keep the reference's semantics -- each parameter receives its
+updates one step late -- without a buffer of their own: the update writes the parameter's
+weight of the master as it was before the update (the previous update's result, flag
+ADAMBRIDGE_SEG_OUT_PREVIOUS), so the newest weight stays in the master until the parameter's
+next update, or a flush, writes it.
 
 ``update`` may be called from the autograd thread (the gradient hooks) and
 never waits on the host.  The rounding streams are keyed by (parameter index,
@@ -34,6 +39,7 @@ from dataclasses import dataclass, field
 import torch
 
 from . import _hip
+from .formats import bf16_weight
 from .precision import MomentStore, make_store
 from .state import ParamState, choose_layout, new_states
 
@@ -53,7 +59,7 @@ class ParamSlot:
         self.numel = param.numel()
         self.step = 0
         self.state: ParamState | None = None
-        self.out: torch.Tensor | None = None        # write-back buffer (delayed or deferred write-back)
+        self.out: torch.Tensor | None = None        # write-back buffer (deferred write-back, strided parameter)
         self.out_view: torch.Tensor | None = None   # the same, shaped like the parameter
         self.submitted = False                      # updated (or queued) in the current step
         self.seg = _hip.Segment(n=self.numel, index=index)
@@ -140,8 +146,8 @@ class _Hyper:
 
 
 class _Lanes:
-    """A device's two streams besides the caller's: updates run on ``side``, delayed write-backs on
-    ``wb`` (both at the default priority)."""
+    """A device's two streams besides the caller's: updates run on ``side``, copies into the parameters
+    (buffered weights, owed delayed updates) on ``wb`` (both at the default priority)."""
 
     def __init__(self, device: torch.device):
         self.side = torch.cuda.Stream(device)
@@ -174,14 +180,13 @@ class UpdateEngine:
         self._hyper = _Hyper(seed, stochastic_rounding)
         self._lock = threading.RLock()
         self._lanes: dict[torch.device, _Lanes] = {}
-        self._owed: dict[ParamSlot, None] = {}     # delayed: `out` holds an update not yet in the parameter
+        self._owed: dict[ParamSlot, None] = {}     # delayed: the master holds an update not yet in the parameter
         self._fresh: dict[ParamSlot, None] = {}    # delayed: updated during the current step
-        self._deferred: list[ParamSlot] = []       # overlap_writeback=False: out -> param at step_sync
+        self._deferred: list[ParamSlot] = []       # weights written to `out`, copied in at step_sync
         self._num_updates = 0
         self._ready_events: list[torch.cuda.Event] = []
         self._update_events: list[tuple[torch.cuda.Event, torch.cuda.Event]] = []
         self._used: set[torch.device] = set()
-        self._grads_kept = False
         self.launch_log: list | None = None   # a list: (start, end, elements) of every launch, read after a sync
         self._closed = False
 
@@ -273,32 +278,35 @@ class UpdateEngine:
                     self._ensure_out(slots[i])
 
     def _ensure_out(self, slot: ParamSlot) -> None:
-        """The write-back buffer of a slot whose updates go there first (delayed or deferred write-back,
-        a non-contiguous parameter)."""
+        """The write-back buffer of a slot whose updates go there first (deferred write-back, a
+        non-contiguous parameter)."""
         p = slot.param
-        wanted = not slot.state.master_is_param and (
-            self.delay_capable or not self.overlap_writeback or not p.is_contiguous())
+        wanted = not slot.state.master_is_param and (not self.overlap_writeback or not p.is_contiguous())
         if wanted and slot.out is None:
             slot.out = torch.empty(slot.numel, dtype=p.dtype, device=p.device)
             slot.out_view = slot.out.view(p.shape)
 
     # ------------------------------------------------------------ descriptors
 
-    def _target(self, slot: ParamSlot, hooked: bool) -> tuple[int | None, torch.dtype | None]:
-        """Where the kernel writes the new working weight: (device address, dtype), or (None, None)."""
+    def _target(self, slot: ParamSlot, hooked: bool) -> tuple[int | None, torch.dtype | None, bool]:
+        """Where the kernel writes the working weight: (device address, dtype, buffered), or (None, None,
+        False).  Buffered: the slot's `out`, copied into the parameter at step_sync -- a strided
+        parameter, or a hooked update with overlap_writeback=False (exact mode only: a delayed update
+        writes the previous weight, which the parameter may take at once)."""
         state = slot.state
         if state.master_is_param:
-            return None, None                   # the master is the parameter
+            return None, None, False            # the master is the parameter
         p = slot.param
-        if self.delay or (hooked and not self.overlap_writeback) or not p.is_contiguous():
+        if not p.is_contiguous() or (hooked and not self.overlap_writeback and not self.delay):
             if slot.out is None:
                 slot.out = torch.empty(slot.numel, dtype=p.dtype, device=p.device)
                 slot.out_view = slot.out.view(p.shape)
-            return slot.out.data_ptr(), slot.out.dtype
-        return p.data_ptr(), p.dtype
+            return slot.out.data_ptr(), slot.out.dtype, True
+        return p.data_ptr(), p.dtype, False
 
     def _describe(self, slot: ParamSlot, grad: torch.Tensor, hooked: bool, group: _hip.Group):
-        """The slot's descriptor for this update: gradient, output, step, group (state fields bound)."""
+        """The slot's descriptor for this update: gradient, output, step, group (state fields bound).
+        Returns the descriptor's pointer and whether the weight goes to the slot's buffer."""
         seg = slot.seg
         if slot.bound is not slot.state or slot.state.alternates:
             slot.state.bind(seg)
@@ -310,23 +318,26 @@ class UpdateEngine:
         else:
             raise TypeError(f"gradients must be float32 or bfloat16, got {grad.dtype}")
         seg.g = grad.data_ptr()
-        out, dtype = self._target(slot, hooked)
+        out, dtype, buffered = self._target(slot, hooked)
+        if self.delay and slot.step == 1:
+            # a delayed first update owes the parameter nothing: its weight is the one the master was
+            # made from (which an FP24 master holds only rounded)
+            out, dtype, buffered = None, None, False
         seg.out = out
         seg.out_dtype = _hip.DT_NONE if out is None else _hip.DT_F32 if dtype is torch.float32 else _hip.DT_BF16
+        seg.reserved = _hip.SEG_OUT_PREVIOUS if self.delay and out is not None else 0
         seg.step = slot.step
         seg.offset = 0
         seg.algorithm = _hip.ALGORITHMS[self.algorithm]
         seg.group = ctypes.pointer(group)
-        return slot.seg_ptr
+        return slot.seg_ptr, buffered
 
     # ------------------------------------------------------------ submission
 
-    def update(self, slots: list[ParamSlot], grads: list[torch.Tensor], hooked: bool = False,
-               grads_kept: bool = True) -> None:
+    def update(self, slots: list[ParamSlot], grads: list[torch.Tensor], hooked: bool = False) -> None:
         """Enqueue one fused update of ``slots`` with ``grads``, one launch per device, on the device's side
-        stream after the work already queued on its current stream.  ``grads_kept``: the gradients stay
-        attached to the parameters, where later compute-stream work may change them, so even a delayed
-        step makes the compute stream wait for this update."""
+        stream after the work already queued on its current stream (the gradients are kept alive for it
+        by ``record_stream``; the caller's stream waits for it at :meth:`finish_step`)."""
         by_device: dict[torch.device, list[int]] = {}
         for i, slot in enumerate(slots):
             if not slot.initialized:
@@ -334,8 +345,6 @@ class UpdateEngine:
             by_device.setdefault(slot.param.device, []).append(i)
         for device, picks in by_device.items():
             self._launch(device, [slots[i] for i in picks], [grads[i] for i in picks], hooked)
-            if grads_kept:
-                self._grads_kept = True
 
     def _launch(self, device: torch.device, slots: list[ParamSlot], grads: list[torch.Tensor], hooked: bool) -> None:
         lanes = self.lanes(device)
@@ -358,26 +367,19 @@ class UpdateEngine:
             if self.timing:
                 self._ready_events.append(ready)
             lanes.side.wait_event(ready)
-            if self.delay:
-                owed = []
-                with self._lock:
-                    for slot in slots:
-                        if slot in self._owed:
-                            owed.append(slot)
-                            del self._owed[slot]
-                        self._fresh[slot] = None
-                if owed:
-                    lanes.side.wait_event(self._write_back(device, owed, ready))
             structs: dict[int, _hip.Group] = {}   # each group's hyperparameters, read once per launch
             for slot in slots:
                 slot.step += 1
             try:
-                ptrs = []
+                ptrs, buffered = [], []
                 for slot, g in zip(slots, grads):
                     gs = structs.get(id(slot.group))
                     if gs is None:
                         gs = structs[id(slot.group)] = self._hyper.refresh(slot.group)
-                    ptrs.append(self._describe(slot, g, hooked, gs))
+                    ptr, into_out = self._describe(slot, g, hooked, gs)
+                    ptrs.append(ptr)
+                    if into_out:
+                        buffered.append(slot)
                 timed = self.timing or self.launch_log is not None
                 start = torch.cuda.Event(enable_timing=True) if timed else None
                 if start is not None:
@@ -397,9 +399,12 @@ class UpdateEngine:
             for slot in slots:
                 slot.done_ev = done
                 slot.state.advance()
-                if (not self.delay and slot.out is not None and not slot.state.master_is_param
-                        and (hooked and not self.overlap_writeback or not slot.param.is_contiguous())):
-                    self._deferred.append(slot)
+            self._deferred += buffered
+            if self.delay:   # each update wrote the weight owed from the slot's last one, and owes its own
+                with self._lock:
+                    for slot in slots:
+                        self._owed.pop(slot, None)
+                        self._fresh[slot] = None
             for g in grads:
                 g.record_stream(lanes.side)
             self._used.add(device)
@@ -432,6 +437,30 @@ class UpdateEngine:
         for device, members in by_device.items():
             self._write_back(device, members, None)
 
+    def _weights_from_masters(self, slots: list[ParamSlot]) -> None:
+        """Write each slot's newest weight -- its master in the parameter's dtype, as the kernels round
+        it -- into the parameter, on the write-back stream after the compute stream so far (which may
+        still read the old weights) and the slot's latest update.  For delayed updates owed to
+        parameters that their next update will not reach in time."""
+        by_device: dict[torch.device, list[ParamSlot]] = {}
+        for slot in slots:
+            if slot.state is not None and not slot.state.master_is_param:
+                by_device.setdefault(slot.param.device, []).append(slot)
+        for device, members in by_device.items():
+            lanes = self.lanes(device)
+            with torch.cuda.device(device):
+                ready = torch.cuda.Event()
+                ready.record(torch.cuda.current_stream(device))
+                lanes.wb.wait_event(ready)
+                for ev in {id(s.done_ev): s.done_ev for s in members if s.done_ev is not None}.values():
+                    lanes.wb.wait_event(ev)
+                with torch.cuda.stream(lanes.wb), torch.no_grad():
+                    for slot in members:
+                        master = slot.state.master_fp32()
+                        weight = master if slot.param.dtype == torch.float32 else bf16_weight(master)
+                        slot.param.copy_(weight.view(slot.param.shape))
+            self._used.add(device)
+
     # ---------------------------------------------------------- synchronizing
 
     def finish_step(self) -> StepStats:
@@ -439,19 +468,16 @@ class UpdateEngine:
         Delayed mode: updates owed from earlier steps whose parameters got no gradient this step are
         written back now, so no parameter lags by more than one step."""
         t0 = time.perf_counter()
-        if self.delay:
-            with self._lock:
-                left, self._owed, self._fresh = list(self._owed), self._fresh, {}
-            self._write_back_all(left)
+        with self._lock:   # owed updates whose parameters got no gradient this step: written now
+            left, self._owed, self._fresh = list(self._owed), self._fresh, {}
+        self._weights_from_masters(left)
         deferred, self._deferred = self._deferred, []
         self._write_back_all(deferred)
-        kept, self._grads_kept = self._grads_kept, False
-        for device in self._used:
+        for device in self._used:   # the updates write the parameters, delayed ones too
             lanes = self.lanes(device)
             current = torch.cuda.current_stream(device)
             current.wait_stream(lanes.wb)
-            if not self.delay or kept:
-                current.wait_stream(lanes.side)
+            current.wait_stream(lanes.side)
         stats = StepStats(stall=time.perf_counter() - t0)
         with self._lock:
             stats.num_updates, self._num_updates = self._num_updates, 0
@@ -482,12 +508,12 @@ class UpdateEngine:
     def flush(self) -> None:
         """Write every pending delayed update into its parameter and order all of it before the caller's
         next work, which then sees the weights an exact optimizer would have produced."""
+        deferred, self._deferred = self._deferred, []
+        self._write_back_all(deferred)
         with self._lock:
             pending = list({**self._owed, **self._fresh})
             self._owed, self._fresh = {}, {}
-        self._write_back_all(pending)
-        deferred, self._deferred = self._deferred, []
-        self._write_back_all(deferred)
+        self._weights_from_masters(pending)
         for device in self._used:
             lanes = self.lanes(device)
             current = torch.cuda.current_stream(device)

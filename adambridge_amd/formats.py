@@ -38,7 +38,7 @@ import torch
 __all__ = [
     "PRECISIONS", "MASTER_PRECISIONS", "FP8_BLOCK", "Fp8Format", "FP8_FORMATS", "canonical_precision",
     "canonical_master_precision", "moment_bytes", "bytes_per_param", "lowbias32", "stream_seed", "counter_hash",
-    "round_bits_stochastic", "bf16_encode", "fp8_blocks", "fp8_encode", "fp8_decode", "fp24_round", "fp24_split",
+    "round_bits_stochastic", "bf16_encode", "bf16_weight", "fp8_blocks", "fp8_encode", "fp8_decode", "fp24_round", "fp24_split",
     "fp24_join",
 ]
 
@@ -178,6 +178,16 @@ def bf16_encode(x: torch.Tensor, seed: int | None = None, start: int = 0) -> tor
             _device_convert(flat, out, None, flat.numel(), "m")
         return out
     return flat.to(torch.bfloat16)
+
+
+def bf16_weight(x: torch.Tensor) -> torch.Tensor:
+    """FP32 ``x`` as the bf16 working weight the kernels write (kernels.c:108-112): nearest-even,
+    a NaN kept with its sign and payload and made quiet.  A new flat tensor on x's device."""
+    bits = _as_u32(x)
+    nan = bits.bitwise_and(0x7FFFFFFF) > 0x7F800000
+    rounded = (bits + 0x7FFF + bits.bitwise_right_shift(16).bitwise_and_(1)).bitwise_and_(_U32)
+    bits = torch.where(nan, bits.bitwise_or(0x00400000), rounded).bitwise_right_shift_(16)
+    return bits.sub_(bits.ge(0x8000).long() << 16).to(torch.int16).view(torch.bfloat16)
 
 
 # ---------------------------------------------------------------------- FP8

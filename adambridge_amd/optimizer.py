@@ -271,6 +271,8 @@ class AdamBridge(torch.optim.Optimizer):
     enqueued (``release_grads=True``).  ``delay_updates=True`` applies each
     update one step late (weights one step stale, as the reference and
     DeepSpeed's delayed parameter update); ``flush()`` applies what is pending.
+    The update kernel then writes each parameter the weight of its master from
+    before the update, so the stale weights take no memory or copies of their own.
 
     Args follow the reference (optimizer.py:126-216): ``lr``, ``betas``, ``eps``,
     ``weight_decay`` as in torch.optim.AdamW; ``precision`` 'fp32' | 'bf16' | 'fp8'
@@ -416,7 +418,7 @@ class AdamBridge(torch.optim.Optimizer):
         if any(g.is_sparse for g in grads):
             raise RuntimeError("AdamBridge does not support sparse gradients")
         try:
-            self._engine.update(slots, grads, hooked=hooked, grads_kept=not release)
+            self._engine.update(slots, grads, hooked=hooked)
         except Exception as exc:   # surfaced as the reference surfaces its workers' errors (engine.py:1150-1158)
             raise RuntimeError(f"adambridge update failed: {exc}") from exc
         for slot in slots:
@@ -427,8 +429,7 @@ class AdamBridge(torch.optim.Optimizer):
     def step_sync(self) -> StepStats:
         """Close the step (optimizer.py:332-355): update what the hooks left -- the small parameters,
         and with gradient accumulation any parameter whose window the step cut short -- then order
-        every update before subsequent work on the current stream (a stream wait, not a host wait;
-        with delayed updates, only the write-backs)."""
+        every update before subsequent work on the current stream (a stream wait, not a host wait)."""
         with self._window.closing(self._registry):
             if not self._window.suppressed:
                 self._update_leftovers()

@@ -141,8 +141,17 @@ typedef struct adambridge_segment {
     int32_t out_dtype;
     int32_t algorithm;
     int32_t p_dtype;         /* DT_F32 (or 0), DT_F24, DT_PACKED, DT_PACKED_FP8 or DT_PACKED_LION */
-    int32_t reserved;
+    int32_t reserved;        /* 0, or ADAMBRIDGE_SEG_OUT_PREVIOUS */
 } adambridge_segment;
+
+/* ADAMBRIDGE_SEG_OUT_PREVIOUS (a flag in adambridge_segment.reserved; no counterpart in the
+ * reference, which leaves the field zero): out receives the working weight of the master as it
+ * was stored BEFORE this update -- the value the previous update of the segment wrote to out --
+ * instead of the new one.  For updates that reach the weights one step late (delay_updates):
+ * the update writes the stale weight straight into the parameter, with no buffer of its own and
+ * no copy, and the new weight is the master's, to be written by the next update or a flush.
+ * Every other bit of the field is ignored, as the reference ignores the field. */
+#define ADAMBRIDGE_SEG_OUT_PREVIOUS 1
 
 /* kernels.c:1493. */
 ADAMBRIDGE_API int adambridge_abi_version(void);

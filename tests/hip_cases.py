@@ -44,7 +44,7 @@ def hip_segment(case: O.Case, tensors: dict, group: _hip.Group | None) -> _hip.S
 class Prepared:
     """Device copies of cases, their segments and coefficients, ready for one library call."""
 
-    def __init__(self, cases: list[O.Case], tensors_hook=None):
+    def __init__(self, cases: list[O.Case], tensors_hook=None, seg_flags: int = 0):
         self.work = [c.copy() for c in cases]
         for c in self.work:
             O.check_sizes(c)   # every buffer covers what the launch will touch, before anything runs
@@ -57,6 +57,8 @@ class Prepared:
                                   seed=c.group["seed"] & (2**64 - 1), stochastic=int(c.group["stochastic"]))
                        if self.by_group else None for c in self.work]
         self.segs = [hip_segment(c, t, g) for c, t, g in zip(self.work, self.dev, self.groups)]
+        for seg in self.segs:
+            seg.reserved = seg_flags
         self.arr = _hip.load().segment_array([ctypes.pointer(s) for s in self.segs])
         self.hps = None if self.by_group else [
             _hip.HParams(**{k: c.hparams[k] for k, _ in _hip.HParams._fields_}) for c in self.work]
@@ -81,11 +83,12 @@ class Prepared:
 
 
 def run_hip(cases: list[O.Case], width: int = 16, pool: int | None = None,
-            tensors_hook=None) -> list[O.Case]:
+            tensors_hook=None, seg_flags: int = 0) -> list[O.Case]:
     """Update copies of ``cases`` in one call of the HIP library; returns them.
 
-    ``tensors_hook(i, tensors)`` may replace device tensors before the call (misalignment tests)."""
-    prep = Prepared(cases, tensors_hook)
+    ``tensors_hook(i, tensors)`` may replace device tensors before the call (misalignment tests);
+    ``seg_flags`` goes into every segment's ``reserved`` field."""
+    prep = Prepared(cases, tensors_hook, seg_flags)
     kernels = _hip.load()
     kernels.set_simd_level(WIDTH_LEVEL[width])
     try:
@@ -156,7 +159,7 @@ def unpack_state(case: O.Case, state: np.ndarray) -> None:
 
 
 def run_hip_packed(cases: list[O.Case], width: int = 16, double_buffer: bool = False,
-                   misalign_g: bool = False) -> list[O.Case]:
+                   misalign_g: bool = False, seg_flags: int = 0) -> list[O.Case]:
     """Like run_hip for AdamW / FP32 master / BF16 moment cases, through the interleaved layout
     (ADAMBRIDGE_DT_PACKED): pack on the host, one call, unpack the result."""
     kernels = _hip.load()
@@ -186,7 +189,7 @@ def run_hip_packed(cases: list[O.Case], width: int = 16, double_buffer: bool = F
                                  g=g.data_ptr(), m=None, v=None, out=out.data_ptr() if out is not None else None,
                                  group=ctypes.pointer(grp) if grp is not None else None, n=c.n, step=c.step,
                                  index=c.index, offset=c.offset, g_dtype=c.g_dtype, mv_dtype=O.DT_BF16,
-                                 out_dtype=c.out_dtype, algorithm=0, p_dtype=_hip.DT_PACKED))
+                                 out_dtype=c.out_dtype, algorithm=0, p_dtype=_hip.DT_PACKED, reserved=seg_flags))
     arr = kernels.segment_array([ctypes.pointer(s) for s in segs])
     kernels.set_simd_level(WIDTH_LEVEL[width])
     try:
@@ -242,7 +245,8 @@ def unpack_records(case: O.Case, rec: np.ndarray) -> None:
         case.arrays[key] = codes[:, :, lo:lo + 8].reshape(-1)[:size].copy()
 
 
-def run_hip_records(cases: list[O.Case], width: int = 16, misalign_g: bool = False) -> list[O.Case]:
+def run_hip_records(cases: list[O.Case], width: int = 16, misalign_g: bool = False,
+                    seg_flags: int = 0) -> list[O.Case]:
     """Like run_hip for AdamW / FP32 master / FP8 moment cases, through the block-record layout
     (ADAMBRIDGE_DT_PACKED_FP8): pack on the host, one call, unpack the result."""
     kernels = _hip.load()
@@ -271,7 +275,7 @@ def run_hip_records(cases: list[O.Case], width: int = 16, misalign_g: bool = Fal
                                  out=out.data_ptr() if out is not None else None,
                                  group=ctypes.pointer(grp) if grp is not None else None, n=c.n, step=c.step,
                                  index=c.index, offset=c.offset, g_dtype=c.g_dtype, mv_dtype=O.DT_FP8,
-                                 out_dtype=c.out_dtype, algorithm=0, p_dtype=_hip.DT_PACKED8))
+                                 out_dtype=c.out_dtype, algorithm=0, p_dtype=_hip.DT_PACKED8, reserved=seg_flags))
     arr = kernels.segment_array([ctypes.pointer(s) for s in segs])
     kernels.set_simd_level(WIDTH_LEVEL[width])
     try:
@@ -325,7 +329,7 @@ def unpack_lion_records(case: O.Case, rec: np.ndarray) -> tuple[np.ndarray, np.n
 
 
 def run_hip_lion_records(cases: list[O.Case], width: int = 16, double_buffer: bool = False,
-                         misalign_g: int = 0, padding: list | None = None) -> list[O.Case]:
+                         misalign_g: int = 0, padding: list | None = None, seg_flags: int = 0) -> list[O.Case]:
     """Like run_hip for Lion / FP32 master / BF16 moment cases, through the record layout
     (ADAMBRIDGE_DT_PACKED_LION): pack on the host, one call, unpack the result.  ``misalign_g``
     elements shift the gradient off its allocation's alignment; ``padding`` receives each case's
@@ -356,7 +360,8 @@ def run_hip_lion_records(cases: list[O.Case], width: int = 16, double_buffer: bo
                                  g=g.data_ptr(), m=None, v=None, out=out.data_ptr() if out is not None else None,
                                  group=ctypes.pointer(grp) if grp is not None else None, n=c.n, step=c.step,
                                  index=c.index, offset=c.offset, g_dtype=c.g_dtype, mv_dtype=O.DT_BF16,
-                                 out_dtype=c.out_dtype, algorithm=O.LION, p_dtype=_hip.DT_PACKED_LION))
+                                 out_dtype=c.out_dtype, algorithm=O.LION, p_dtype=_hip.DT_PACKED_LION,
+                                 reserved=seg_flags))
     arr = kernels.segment_array([ctypes.pointer(s) for s in segs])
     kernels.set_simd_level(WIDTH_LEVEL[width])
     try:

@@ -46,6 +46,18 @@ def test_layouts_and_version():
     assert lib.adambridge_backend() == b"hip/gfx950"
 
 
+def test_header_codes_match_the_python_mirror():
+    """The storage codes and the segment flag the header defines are the ones _hip passes."""
+    text = HEADER.read_text()
+    codes = {name: int(v) for name, v in re.findall(r"ADAMBRIDGE_(DT_\w+)\s*=\s*(\d+)", text)}
+    mirror = {"DT_NONE": _hip.DT_NONE, "DT_F32": _hip.DT_F32, "DT_BF16": _hip.DT_BF16, "DT_FP8": _hip.DT_FP8,
+              "DT_F24": _hip.DT_F24, "DT_PACKED": _hip.DT_PACKED, "DT_PACKED_FP8": _hip.DT_PACKED8,
+              "DT_PACKED_LION": _hip.DT_PACKED_LION}
+    assert codes == mirror
+    flag = re.search(r"#define ADAMBRIDGE_SEG_OUT_PREVIOUS (\d+)", text)
+    assert flag and int(flag.group(1)) == _hip.SEG_OUT_PREVIOUS
+
+
 def test_simd_level_switch():
     k = _hip.HipKernels()
     assert k.detected_simd_level == "avx512"

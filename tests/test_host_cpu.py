@@ -19,6 +19,7 @@ import torch
 from oracle import oracle as O
 
 import adambridge_amd as ab
+from adambridge_amd import formats as F
 from adambridge_amd import precision as P
 
 
@@ -43,6 +44,20 @@ def test_precision_aliases_and_bytes_per_param():
 
 
 # ------------------------------------------------- rounding streams and codecs
+
+def test_bf16_weight_is_the_kernels_weight_rounding():
+    """formats.bf16_weight (the weight written into a parameter for an owed delayed update) rounds as
+    the kernels' working-weight output does (kernels.c:108-112): nearest-even, NaN sign and payload
+    kept with the quiet bit set -- against the oracle's rule, on special values and random bits."""
+    rng = np.random.default_rng(3)
+    special = np.array([0, 0x80000000, 0x7F800000, 0xFF800000, 0x7F800001, 0xFFC00001, 0x7FBFFFFF, 0x7F7FFFFF,
+                        0xFF7FFFFF, 0x00000001, 0x8000FFFF, 0x3F808000, 0x3F818000, 0x3F807FFF, 0x7FFF0000,
+                        0xFFFF8000], dtype=np.uint32)
+    bits = np.concatenate([special, rng.integers(0, 2**32, 1 << 18, dtype=np.uint64).astype(np.uint32)])
+    got = F.bf16_weight(torch.from_numpy(bits.view(np.float32).copy()))
+    assert got.dtype == torch.bfloat16
+    assert np.array_equal(got.view(torch.int16).numpy().view(np.uint16), O.bf16_bits(bits.view(np.float32)))
+
 
 def test_random_bits_is_the_kernels_counter_hash():
     lib = O.load_oracle()

@@ -553,6 +553,48 @@ def test_fp8_larger_tile_matches_oracle():
     assert run.returncode == 0, run.stdout + run.stderr[-3000:]
 
 
+def _previous_weight(case):
+    """The working weight of the case's master as it is before the update: what
+    ADAMBRIDGE_SEG_OUT_PREVIOUS writes to out (kernels.c:108-112 for a bf16 out)."""
+    p = case.arrays["p"]
+    old = O.f24_value(p, case.arrays["p_lo"]) if case.p_dtype == O.DT_F24 else p.view(np.float32)
+    return O.bf16_bits(old) if case.out_dtype == O.DT_BF16 else old.astype(np.float32)
+
+
+@pytest.mark.parametrize("layout", ["separate", "pairs", "fp8-records", "lion-records"])
+def test_out_previous_writes_the_weight_from_before_the_update(layout):
+    """ADAMBRIDGE_SEG_OUT_PREVIOUS (delayed updates): out receives the weight of the master as stored
+    before the update -- FP32, or bf16 by the kernels' rounding of FP32 and decoded FP24 masters,
+    NaN masters included -- and the state is updated exactly as without the flag."""
+    from hip_cases import run_hip_lion_records, run_hip_packed, run_hip_records
+    from adambridge_amd import _hip
+
+    rng = np.random.default_rng(31 + len(layout))
+    combos = {"separate": [(a, mv, pt) for a in ALGOS for mv in MVS for pt in PTS],
+              "pairs": [(O.ADAMW, O.DT_BF16, O.DT_F32)], "fp8-records": [(O.ADAMW, O.DT_FP8, O.DT_F32)],
+              "lion-records": [(O.LION, O.DT_BF16, O.DT_F32)]}[layout]
+    runner = {"separate": run_hip, "pairs": run_hip_packed, "fp8-records": run_hip_records,
+              "lion-records": run_hip_lion_records}[layout]
+    cases = []
+    for (algo, mv, pt), gt, ot, sr, n in itertools.product(combos, [O.DT_BF16, O.DT_F32], [O.DT_F32, O.DT_BF16],
+                                                             [True, False], [1, 15, 17, 129, 1000, 8192 + 77]):
+        off = int(rng.integers(0, 50)) * 128 if mv == O.DT_FP8 else int(rng.integers(0, 2**32))
+        cases.append(O.make_case(rng, n, algorithm=algo, mv_dtype=mv, p_dtype=pt, g_dtype=gt, out_dtype=ot,
+                                 stochastic=sr, offset=off, index=int(rng.integers(0, 1000)),
+                                 step=int(rng.integers(1, 50))))
+    regular = len(cases)
+    cases += [O.make_case(rng, 3000, algorithm=algo, mv_dtype=mv, p_dtype=pt, special=True)
+              for algo, mv, pt in combos]   # zeros, subnormals, infinities and NaNs in every input
+    want = O.run_many(cases, "oracle", 16)
+    got = runner(cases, 16, seg_flags=_hip.SEG_OUT_PREVIOUS)
+    for i, (c, w, g) in enumerate(zip(cases, want, got)):
+        prev = _previous_weight(c)
+        assert np.array_equal(g.arrays["out"].view(np.uint8), prev.view(np.uint8)), \
+            f"{layout}: case {i} (n={c.n}, out_dtype={c.out_dtype}): out is not the weight from before the update"
+        w.arrays["out"] = prev
+        check(w, g, special=i >= regular)
+
+
 def test_stream_copy_copies_exactly():
     """adambridge_stream_copy, the counter-calibration copy: every byte, sizes around its 4 KiB tile."""
     from adambridge_amd import _hip

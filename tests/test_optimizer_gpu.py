@@ -277,6 +277,47 @@ def test_delayed_updates_with_accumulation_match_stale_accumulated_adamw(warmup)
     opt.close()
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("kind", ["adamw-bf16", "adamw-fp8", "adamw-fp32", "adamw-bf16-fp24", "lion-bf16"])
+def test_delayed_weights_are_the_exact_weights_one_step_late(kind, dtype):
+    """With gradients that do not depend on the weights, a delayed optimizer's parameters after step
+    k are, bit for bit, an exact optimizer's after step k - 1 -- a parameter that gets no gradient
+    at a step included -- its masters equal the exact ones at every step, and flush() brings the
+    parameters level (the update writes the weight from before it; the newest waits in the master)."""
+    algo, precision, *rest = kind.split("-")
+    master = rest[0] if rest else "fp32"
+    cls = ab.LionBridge if algo == "lion" else ab.AdamBridge
+    torch.manual_seed(0)
+    shapes = [(300, 70), (1001,), (64, 64), (5,)]
+    base = [torch.randn(s, device=DEV).mul_(0.02).to(dtype) for s in shapes]
+    exact_ps = [torch.nn.Parameter(t.clone()) for t in base]
+    delayed_ps = [torch.nn.Parameter(t.clone()) for t in base]
+    kw = dict(lr=1e-2, weight_decay=0.1, precision=precision, master_precision=master, small_param_threshold=0)
+    exact = cls(exact_ps, **kw)
+    delayed = cls(delayed_ps, delay_updates=True, delay_warmup_steps=0, **kw)
+    history = [[p.detach().clone() for p in exact_ps]]
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    for k in range(1, 6):
+        grads = [torch.randn(s, device=DEV, generator=gen).mul_(1e-2).to(dtype) for s in shapes]
+        skip = 2 if k == 3 else None   # parameter 2 gets no gradient at step 3
+        for ps, opt in ((exact_ps, exact), (delayed_ps, delayed)):
+            for i, (p, g) in enumerate(zip(ps, grads)):
+                p.grad = None if i == skip else g.clone()
+            opt.step()
+        history.append([p.detach().clone() for p in exact_ps])
+        for i, (got, want) in enumerate(zip(delayed_ps, history[k - 1])):
+            assert torch.equal(got, want), f"step {k}: parameter {i} is not the exact weight of step {k - 1}"
+        for a, b in zip(exact.master_params(), delayed.master_params()):
+            assert torch.equal(a, b)
+    assert not torch.equal(history[-1][0], history[-2][0])
+    delayed.flush()
+    torch.cuda.synchronize()
+    for got, want in zip(delayed_ps, exact_ps):
+        assert torch.equal(got, want)
+    exact.close()
+    delayed.close()
+
+
 def test_delayed_updates_state_dict_close_and_unused_params():
     """reference test_cuda.py:180-209."""
     torch.manual_seed(0)
