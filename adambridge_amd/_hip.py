@@ -72,7 +72,7 @@ EXPORTS = (
     "adambridge_pool_set_spin", "adambridge_multi_step", "adambridge_multi_apply", "adambridge_pool_set_stream",
     "adambridge_pool_sync", "adambridge_set_stream", "adambridge_last_error", "adambridge_backend",
     "adambridge_check_conversions", "adambridge_convert", "adambridge_plan_launches",
-    "adambridge_multi_step_noalloc", "adambridge_stream_copy",
+    "adambridge_multi_step_noalloc", "adambridge_stream_copy", "adambridge_recycle_device_memory",
 )
 
 
@@ -109,6 +109,7 @@ def open_library(path: Path = LIB_PATH) -> ctypes.CDLL:
         "adambridge_plan_launches": (ctypes.c_int, [_SegArray, i32, ctypes.POINTER(i64), i32]),
         "adambridge_multi_step_noalloc": (ctypes.c_int, [vp, _SegArray, i32]),
         "adambridge_stream_copy": (ctypes.c_int, [vp, vp, i64]),
+        "adambridge_recycle_device_memory": (ctypes.c_int, [i64]),
     }
     for name in EXPORTS:
         fn = getattr(lib, name)
@@ -247,6 +248,12 @@ class HipKernels:
             self.set_stream(torch.cuda.current_stream(dst.device))
             self._check(self._lib.adambridge_stream_copy(src.data_ptr(), dst.data_ptr(), dst.nbytes),
                         "adambridge_stream_copy")
+
+    def recycle_device_memory(self, nbytes: int, device: torch.device) -> bool:
+        """Allocate ``nbytes`` on ``device`` and free them at once (adambridge_recycle_device_memory),
+        ahead of allocating a buffer of that size; False if the allocation failed (nothing held)."""
+        with torch.cuda.device(device):
+            return self._lib.adambridge_recycle_device_memory(int(nbytes)) == 0
 
     _CONVERT_DTYPES = {torch.float32: DT_F32, torch.bfloat16: DT_BF16, torch.float8_e4m3fn: DT_FP8,
                        torch.float8_e5m2: DT_FP8, torch.uint8: DT_FP8}

@@ -625,3 +625,20 @@ def test_stream_copy_beyond_one_launch():
     finally:
         del src, dst
         torch.cuda.empty_cache()
+
+
+def test_recycle_device_memory_holds_nothing_and_clears_its_error():
+    """adambridge_recycle_device_memory allocates and frees at once; an allocation the device cannot
+    make is reported, holds nothing and leaves no HIP error behind for the next launch check."""
+    from adambridge_amd import _hip
+
+    k = _hip.load()
+    dev = torch.device("cuda", 0)
+    free0 = torch.cuda.mem_get_info(dev)[0]
+    assert k.recycle_device_memory(1 << 30, dev)
+    assert not k.recycle_device_memory(1 << 50, dev)   # 1 PiB: more than the device has
+    assert "recycle" in k.last_error()
+    x = torch.arange(1 << 20, device=dev, dtype=torch.float32).mul_(2.0)   # launches and checks succeed
+    torch.cuda.synchronize()
+    assert float(x[-1]) == 2.0 * ((1 << 20) - 1)
+    assert abs(torch.cuda.mem_get_info(dev)[0] - free0) < (256 << 20)
