@@ -530,3 +530,31 @@ def test_dropped_optimizer_leaves_no_cycle_holding_its_state(monkeypatch, precis
         gc.set_debug(0)
         gc.garbage.clear()
         gc.enable()
+
+
+def test_large_state_arenas_follow_an_allocate_free_of_their_size(monkeypatch):
+    """new_states allocates an arena of RECYCLE_MIN_BYTES or more right after the library has
+    allocated and freed a block of the arena's size (the placement that streams at a copy's rate),
+    and a smaller arena, or the separate layout, without it.  (Host tensors stand in for HBM.)"""
+    from adambridge_amd import _hip
+    from adambridge_amd import state as S
+
+    calls = []
+
+    class Lib:
+        def recycle_device_memory(self, nbytes, device):
+            calls.append((nbytes, device))
+            return True
+
+    monkeypatch.setattr(_hip, "load", lambda: Lib())
+    masters = [torch.zeros(3000), torch.zeros(1001)]
+    _, total = S.arena_plan("pairs", [m.numel() for m in masters])
+    monkeypatch.setattr(S, "RECYCLE_MIN_BYTES", total)
+    states = S.new_states("pairs", "adamw", "bf16", "fp32", "cpu", masters)
+    assert calls == [(total, torch.device("cpu"))]
+    assert states[0].master_fp32().numel() == 3000
+    monkeypatch.setattr(S, "RECYCLE_MIN_BYTES", total + 1)
+    S.new_states("pairs", "adamw", "bf16", "fp32", "cpu", masters)
+    monkeypatch.setattr(S, "RECYCLE_MIN_BYTES", 0)
+    S.new_states("separate", "adamw", "bf16", "fp32", "cpu", masters)
+    assert len(calls) == 1
