@@ -218,10 +218,11 @@ class UpdateEngine:
                              "separate" if self.state_layout == "separate" else "auto",
                              self._master_is_param(slot.param))
 
-    def initialize(self, slots: list[ParamSlot]) -> None:
+    def initialize(self, slots: list[ParamSlot], place: bool = True) -> None:
         """Lazy state for ``slots`` (engine.py:991-1025; precision.py:263-267, 307-311, 365-371): the master
         from each parameter's current value (FP32, or FP24 rounded to nearest), moments zero, FP8
-        scales one.  The interleaved states of one device and layout share one arena."""
+        scales one.  The interleaved states of one device and layout share one arena, placed by an
+        allocate/free of its size first unless ``place`` is False (see state.new_states)."""
         for slot in slots:
             self.check_param(slot.param)
         todo: dict[tuple[torch.device, str], list[ParamSlot]] = {}
@@ -232,7 +233,7 @@ class UpdateEngine:
                 masters = [s.param.detach().reshape(-1) for s in members]
                 params = [s.param if self._master_is_param(s.param) else None for s in members]
                 states = new_states(layout, self.algorithm, self.precision, self.master_precision, device, masters,
-                                    self.double_buffer, params)
+                                    self.double_buffer, params, place)
                 for slot, state in zip(members, states):
                     self._adopt(slot, state)
                     self._ensure_out(slot)
@@ -360,8 +361,8 @@ class UpdateEngine:
             # stream before `ready` is recorded, so that the update waits for it.
             grads = [g if g.is_contiguous() else g.contiguous() for g in grads]
             fresh = [s for s in slots if not s.initialized]
-            if fresh:                              # built on the compute stream, before `ready`
-                self.initialize(fresh)
+            if fresh:   # built on the compute stream, before `ready`; a hook does not wait for the device
+                self.initialize(fresh, place=not hooked)
             ready = torch.cuda.Event(enable_timing=self.timing)
             ready.record(current)
             if self.timing:

@@ -451,7 +451,7 @@ def arena_plan(layout: str, sizes: list[int], double_buffer: bool = False) -> tu
 
 def new_states(layout: str, algorithm: str, precision: str, master_precision: str, device,
                masters: list[torch.Tensor], double_buffer: bool = False,
-               master_params: list[torch.Tensor | None] | None = None) -> list[ParamState]:
+               master_params: list[torch.Tensor | None] | None = None, place: bool = True) -> list[ParamState]:
     """Fresh states for several parameters on one device: master from ``masters[i]`` (any dtype;
     FP24 rounds to nearest) or, in the separate layout, the FP32 parameter ``master_params[i]`` itself;
     moments zero, FP8 scales one.
@@ -463,7 +463,9 @@ def new_states(layout: str, algorithm: str, precision: str, master_precision: st
     more is allocated right after a block of its size was allocated from the driver and freed,
     which places it where the update streams at a copy's rate: 20.75 against 21.43 ms for that
     first build (the driver's first placements in a fresh process stream this update ~3% slower;
-    measured on MI355X, cause unknown).  The allocate/free holds no more memory than the arena."""
+    measured on MI355X, cause unknown).  The allocate/free holds no more memory than the arena; it
+    waits for the device to go idle (the free does), so ``place=False`` skips it where that would
+    stall a pipeline (the states a gradient hook creates during the first backward pass)."""
     roles = ("m",) if algorithm == "lion" else ("m", "v")
     if layout == "separate":
         out: list[ParamState] = []
@@ -482,7 +484,7 @@ def new_states(layout: str, algorithm: str, precision: str, master_precision: st
     cls = _INTERLEAVED[layout]
     sizes = [t.numel() for t in masters]
     offsets, total = arena_plan(layout, sizes, double_buffer)
-    if RECYCLE_MIN_BYTES is not None and total >= RECYCLE_MIN_BYTES:
+    if place and RECYCLE_MIN_BYTES is not None and total >= RECYCLE_MIN_BYTES:
         _hip.load().recycle_device_memory(total, torch.device(device))   # placement only: failure is harmless
     arena = torch.zeros(total, dtype=torch.uint8, device=device)
     states = []

@@ -535,7 +535,8 @@ def test_dropped_optimizer_leaves_no_cycle_holding_its_state(monkeypatch, precis
 def test_large_state_arenas_follow_an_allocate_free_of_their_size(monkeypatch):
     """new_states allocates an arena of RECYCLE_MIN_BYTES or more right after the library has
     allocated and freed a block of the arena's size (the placement that streams at a copy's rate),
-    and a smaller arena, or the separate layout, without it.  (Host tensors stand in for HBM.)"""
+    and a smaller arena, the states a gradient hook creates, or the separate layout, without it.
+    (Host tensors stand in for HBM.)"""
     from adambridge_amd import _hip
     from adambridge_amd import state as S
 
@@ -553,6 +554,7 @@ def test_large_state_arenas_follow_an_allocate_free_of_their_size(monkeypatch):
     states = S.new_states("pairs", "adamw", "bf16", "fp32", "cpu", masters)
     assert calls == [(total, torch.device("cpu"))]
     assert states[0].master_fp32().numel() == 3000
+    S.new_states("pairs", "adamw", "bf16", "fp32", "cpu", masters, place=False)   # a hook's state
     monkeypatch.setattr(S, "RECYCLE_MIN_BYTES", total + 1)
     S.new_states("pairs", "adamw", "bf16", "fp32", "cpu", masters)
     monkeypatch.setattr(S, "RECYCLE_MIN_BYTES", 0)
