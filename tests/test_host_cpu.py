@@ -560,3 +560,19 @@ def test_large_state_arenas_follow_an_allocate_free_of_their_size(monkeypatch):
     monkeypatch.setattr(S, "RECYCLE_MIN_BYTES", 0)
     S.new_states("separate", "adamw", "bf16", "fp32", "cpu", masters)
     assert len(calls) == 1
+
+
+def test_command_line_info_reports_the_library():
+    """python -m adambridge_amd info (reference python -m adambridge info, native.py:472-496)."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    run = subprocess.run([sys.executable, "-m", "adambridge_amd", "info"], cwd=root, capture_output=True,
+                         text=True, timeout=120)
+    assert run.returncode == 0, run.stderr
+    assert "libadambridge_hip.so" in run.stdout and "backend:  hip/gfx950" in run.stdout
+    usage = subprocess.run([sys.executable, "-m", "adambridge_amd", "nonsense"], cwd=root, capture_output=True,
+                           text=True, timeout=120)
+    assert usage.returncode == 2 and "{build,info}" in usage.stderr
