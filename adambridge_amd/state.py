@@ -449,6 +449,12 @@ def arena_plan(layout: str, sizes: list[int], double_buffer: bool = False) -> tu
     return offsets, total
 
 
+def _place(nbytes: int, device, place: bool) -> None:
+    """Before allocating ``nbytes`` of state: an allocate/free of that size (see new_states)."""
+    if place and RECYCLE_MIN_BYTES is not None and nbytes >= RECYCLE_MIN_BYTES:
+        _hip.load().recycle_device_memory(nbytes, torch.device(device))   # placement only: failure is harmless
+
+
 def new_states(layout: str, algorithm: str, precision: str, master_precision: str, device,
                masters: list[torch.Tensor], double_buffer: bool = False,
                master_params: list[torch.Tensor | None] | None = None, place: bool = True) -> list[ParamState]:
@@ -459,15 +465,22 @@ def new_states(layout: str, algorithm: str, precision: str, master_precision: st
     Interleaved states share one arena: a single zeroed allocation, each buffer at a 2 MiB-aligned
     offset -- one allocation instead of one per parameter.  The update streams from it as fast as
     from per-parameter allocations (the 7B bf16-moment step built first in a fresh process: 21.43
-    ms per launch from the arena, 21.41 from 291 allocations).  An arena of RECYCLE_MIN_BYTES or
-    more is allocated right after a block of its size was allocated from the driver and freed,
-    which places it where the update streams at a copy's rate: 20.75 against 21.43 ms for that
-    first build (the driver's first placements in a fresh process stream this update ~3% slower;
-    measured on MI355X, cause unknown).  The allocate/free holds no more memory than the arena; it
+    ms per launch from the arena, 21.41 from 291 allocations).  State of RECYCLE_MIN_BYTES or more
+    (an arena, or the separate layout's stores together) is allocated right after a block of its
+    size was allocated from the driver and freed, which places it where the update streams at a
+    copy's rate: 20.63 against 21.43 ms for that first build, and 30.13 against 31.49 ms with FP32
+    moments in separate arrays (the driver's first placements in a fresh process stream this
+    update 3-4% slower; measured on MI355X, cause unknown).  The allocate/free holds no more memory
+    than the state; it
     waits for the device to go idle (the free does), so ``place=False`` skips it where that would
     stall a pipeline (the states a gradient hook creates during the first backward pass)."""
     roles = ("m",) if algorithm == "lion" else ("m", "v")
     if layout == "separate":
+        # the stores are allocations of their own; the same placement step covers them all at once
+        own_master = [not (master_params and master_params[i] is not None) for i in range(len(masters))]
+        total = sum(int(t.numel() * ((3 if master_precision == "fp24" else 4) * own + len(roles) * F.moment_bytes(precision)))
+                    for t, own in zip(masters, own_master))
+        _place(total, device, place)
         out: list[ParamState] = []
         for i, values in enumerate(masters):
             param = master_params[i] if master_params else None
@@ -484,8 +497,7 @@ def new_states(layout: str, algorithm: str, precision: str, master_precision: st
     cls = _INTERLEAVED[layout]
     sizes = [t.numel() for t in masters]
     offsets, total = arena_plan(layout, sizes, double_buffer)
-    if place and RECYCLE_MIN_BYTES is not None and total >= RECYCLE_MIN_BYTES:
-        _hip.load().recycle_device_memory(total, torch.device(device))   # placement only: failure is harmless
+    _place(total, device, place)
     arena = torch.zeros(total, dtype=torch.uint8, device=device)
     states = []
     for n, offs, values in zip(sizes, offsets, masters):

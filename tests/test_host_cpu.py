@@ -535,8 +535,8 @@ def test_dropped_optimizer_leaves_no_cycle_holding_its_state(monkeypatch, precis
 def test_large_state_arenas_follow_an_allocate_free_of_their_size(monkeypatch):
     """new_states allocates an arena of RECYCLE_MIN_BYTES or more right after the library has
     allocated and freed a block of the arena's size (the placement that streams at a copy's rate),
-    and a smaller arena, the states a gradient hook creates, or the separate layout, without it.
-    (Host tensors stand in for HBM.)"""
+    and so do the separate layout's stores, counted together; smaller state, or the states a
+    gradient hook creates, go without it.  (Host tensors stand in for HBM.)"""
     from adambridge_amd import _hip
     from adambridge_amd import state as S
 
@@ -557,9 +557,12 @@ def test_large_state_arenas_follow_an_allocate_free_of_their_size(monkeypatch):
     S.new_states("pairs", "adamw", "bf16", "fp32", "cpu", masters, place=False)   # a hook's state
     monkeypatch.setattr(S, "RECYCLE_MIN_BYTES", total + 1)
     S.new_states("pairs", "adamw", "bf16", "fp32", "cpu", masters)
-    monkeypatch.setattr(S, "RECYCLE_MIN_BYTES", 0)
+    sep = 4001 * (4 + 2 * 2)   # FP32 master and two BF16 moments of the two parameters
+    monkeypatch.setattr(S, "RECYCLE_MIN_BYTES", sep)
     S.new_states("separate", "adamw", "bf16", "fp32", "cpu", masters)
-    assert len(calls) == 1
+    assert calls[1:] == [(sep, torch.device("cpu"))]
+    S.new_states("separate", "adamw", "bf16", "fp32", "cpu", masters, master_params=[masters[0], None])
+    assert len(calls) == 2   # the first parameter is its own master: 3000 x 4 bytes fewer, under the minimum
 
 
 def test_command_line_info_reports_the_library():
