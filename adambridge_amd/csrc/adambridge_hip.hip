@@ -435,8 +435,7 @@ __device__ __forceinline__ void update_tile(const DevSeg& s, int64_t tile, int64
         load_master2<PT>(s, i, p0, p1);
         if (prev) store_out2<OT>(s.out, i, p0, p1);
         if constexpr (ALGO == ALGO_ADAMW) {
-            p0 = adamw<true>(p0, g0, m0, v0, c);
-            p1 = adamw<true>(p1, g1, m1, v1, c);
+            adamw_pair_fused(p0, p1, g0, g1, m0, m1, v0, v1, c);   // adamw<true> on each, short roots
         } else {
             p0 = lion(p0, g0, m0, c);
             p1 = lion(p1, g1, m1, c);
