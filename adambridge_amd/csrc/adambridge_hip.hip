@@ -997,6 +997,92 @@ __global__ __launch_bounds__(kThreads) void k_update_lion_rec(Launch L)
     else update_tile_lion_rec<GT, OT, false>(s, tile, L.tile);
 }
 
+// --------------------------------------------- FP32-moment AdamW record kernel
+//
+// AdamW with an FP32 master and FP32 moments in one 3072-byte record per 256
+// elements: the record's 256 masters, then its 256 m, then its 256 v, each
+// in element order.  Each lane takes 4 consecutive elements: three 16-byte
+// state accesses, each wavefront instruction one contiguous 1 KiB span, and
+// 8-byte gradient and output accesses -- the access shape of the Lion records,
+// in place of the separate layout's 8-byte accesses to three arrays.  Fused
+// elements take the pair kernel's arithmetic (adamw_pair_fused); the scalar
+// tail of the reproduced SIMD level the unfused form, element by element; a
+// record's slots past n are padding and are written back unchanged.  FP32
+// moments and master are stored exactly (no stochastic rounding).
+
+constexpr int64_t kF32RecordElems = 256;
+constexpr int64_t kF32RecordBytes = 3072;
+
+template <int GT, int OT>
+__device__ __forceinline__ void update_tile_f32rec(const DevSeg& s, int64_t tile, int64_t T)
+{
+    const int64_t n = s.n, n_main = s.n_main;
+    const Coef c = s.c;
+    const uint8_t* __restrict__ src = static_cast<const uint8_t*>(s.p);
+    uint8_t* __restrict__ dst = s.p_lo;
+    const bool vec = (s.flags & kVec) != 0;   // g and out allow 2-element access
+    const bool prev = (s.flags & kPrev) != 0;  // uniform: out from the master as loaded
+    const int64_t lo = (tile - s.tile_begin) * T;
+    const int64_t hi = lo + T < n ? lo + T : n;
+    for (int64_t i = lo + threadIdx.x * 4; i < hi; i += kThreads * 4) {
+        // i % 4 == 0: record i / 256, masters at 4 (i % 256), m 1024 bytes on, v 2048 bytes on
+        const int64_t at = (i / kF32RecordElems) * kF32RecordBytes + (i % kF32RecordElems) * 4;
+        const u32x4 pw = ld(reinterpret_cast<const u32x4*>(src + at));
+        const u32x4 mw = ld(reinterpret_cast<const u32x4*>(src + at + 1024));
+        const u32x4 vw = ld(reinterpret_cast<const u32x4*>(src + at + 2048));
+        const bool all = i + 4 <= n;
+        float g[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (vec && all) {
+            load2<GT>(s.g, i, g[0], g[1]);
+            load2<GT>(s.g, i + 2, g[2], g[3]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (i + k < n) g[k] = load1<GT>(s.g, i + k);
+        }
+        const uint32_t p_in[4] = {pw.x, pw.y, pw.z, pw.w};
+        const uint32_t m_in[4] = {mw.x, mw.y, mw.z, mw.w};
+        const uint32_t v_in[4] = {vw.x, vw.y, vw.z, vw.w};
+        if (prev) store_quad_out<OT>(s.out, i, n, vec && all, p_in);
+        float p[4], m[4], v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            p[k] = bitsf(p_in[k]);
+            m[k] = bitsf(m_in[k]);
+            v[k] = bitsf(v_in[k]);
+        }
+        if (i + 4 <= n_main) {
+            adamw_pair_fused(p[0], p[1], g[0], g[1], m[0], m[1], v[0], v[1], c);
+            adamw_pair_fused(p[2], p[3], g[2], g[3], m[2], m[3], v[2], v[3], c);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (i + k < n) p[k] = adamw_sel(p[k], g[k], m[k], v[k], c, i + k < n_main);
+        }
+        uint32_t p_out[4], m_out[4], v_out[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const bool in = all || i + k < n;   // padding keeps its bits
+            p_out[k] = in ? fbits(p[k]) : p_in[k];
+            m_out[k] = in ? fbits(m[k]) : m_in[k];
+            v_out[k] = in ? fbits(v[k]) : v_in[k];
+        }
+        st(reinterpret_cast<u32x4*>(dst + at), u32x4{p_out[0], p_out[1], p_out[2], p_out[3]});
+        st(reinterpret_cast<u32x4*>(dst + at + 1024), u32x4{m_out[0], m_out[1], m_out[2], m_out[3]});
+        st(reinterpret_cast<u32x4*>(dst + at + 2048), u32x4{v_out[0], v_out[1], v_out[2], v_out[3]});
+        if (!prev) store_quad_out<OT>(s.out, i, n, vec && all, p_out);
+    }
+}
+
+template <int GT, int OT>
+__global__ __launch_bounds__(kThreads) void k_update_f32rec(Launch L)
+{
+    const int64_t tile = block_tile(L);
+    if (tile >= L.ntiles) return;
+    const DevSeg s = find_segment(L, tile);
+    update_tile_f32rec<GT, OT>(s, tile, L.tile);
+}
+
 // ------------------------------------------------------- segment-table writer
 //
 // The allocation-free entry point keeps its segment tables in a device array
@@ -1124,6 +1210,22 @@ static const auto kPacked = make_packed_table(std::make_integer_sequence<int, kN
 static const auto kPacked8 = make_packed8_table(std::make_integer_sequence<int, kNumPacked>{});
 static const auto kLionRec = make_lion_rec_table(std::make_integer_sequence<int, kNumPacked>{});
 
+// FP32-moment record kernels (AdamW) follow: index kNumKernels + 3 * kNumPacked + gt * 3 + ot.
+template <int I>
+constexpr KernelFn f32rec_entry()
+{
+    constexpr int ot = I % 3, gt = I / 3;
+    return &k_update_f32rec<gt ? DT_BF16 : DT_F32, ot == 0 ? DT_NONE : ot == 1 ? DT_F32 : DT_BF16>;
+}
+
+template <int... I>
+constexpr auto make_f32rec_table(std::integer_sequence<int, I...>)
+{
+    return std::array<KernelFn, sizeof...(I)>{f32rec_entry<I>()...};
+}
+
+static const auto kF32Rec = make_f32rec_table(std::make_integer_sequence<int, kNumPacked>{});
+
 // Kernel family of a table index: the FP8 block kernel, or a two-element-per-lane kernel.
 inline bool kernel_is_fp8(int index)
 {
@@ -1136,7 +1238,8 @@ inline KernelFn kernel_at(int index)
     if (index < kNumKernels) return kKernels[index];
     if (index < kNumKernels + kNumPacked) return kPacked[index - kNumKernels];
     if (index < kNumKernels + 2 * kNumPacked) return kPacked8[index - kNumKernels - kNumPacked];
-    return kLionRec[index - kNumKernels - 2 * kNumPacked];
+    if (index < kNumKernels + 3 * kNumPacked) return kLionRec[index - kNumKernels - 2 * kNumPacked];
+    return kF32Rec[index - kNumKernels - 3 * kNumPacked];
 }
 
 inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
@@ -1147,6 +1250,8 @@ inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
         return kNumKernels + kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
     if (pt == DT_PACKED_LION)
         return kNumKernels + 2 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
+    if (pt == DT_PACKED_F32)
+        return kNumKernels + 3 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
     const int mvi = mv == DT_F32 ? 0 : mv == DT_BF16 ? 1 : 2;
     const int pti = pt == DT_F24 ? 1 : 0;
     const int gti = gt == DT_BF16 ? 1 : 0;

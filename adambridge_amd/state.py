@@ -20,6 +20,7 @@ separate        anything (the reference's arrays)      master 4 (FP24: 3) + mome
 pairs           AdamW, FP32 master, BF16 moments       16 per 2 elements (x2 double-buffered)
 fp8-records     AdamW, FP32 master, FP8 moments        768 per 128 + two FP32 scales per 128
 lion-records    Lion, FP32 master, BF16 moment         1536 per 256 (x2 double-buffered)
+f32-records     AdamW, FP32 master, FP32 moments       3072 per 256 (x2 double-buffered)
 ==============  =====================================  ======================================
 
 The interleaved layouts turn the master and moment streams into one stream of
@@ -38,10 +39,10 @@ from . import _hip
 from . import formats as F
 from .precision import BF16Store, FP8Store, FP24Store, FP32Store, MomentStore, load_master_, make_master, make_store
 
-__all__ = ["ParamState", "SeparateState", "PairState", "AdamRecordState", "LionRecordState", "choose_layout",
-           "new_state", "new_states", "arena_plan", "LAYOUTS"]
+__all__ = ["ParamState", "SeparateState", "PairState", "AdamRecordState", "LionRecordState", "F32RecordState",
+           "choose_layout", "new_state", "new_states", "arena_plan", "LAYOUTS"]
 
-LAYOUTS = ("separate", "pairs", "fp8-records", "lion-records")
+LAYOUTS = ("separate", "pairs", "fp8-records", "lion-records", "f32-records")
 
 # Arenas of at least this many bytes follow an allocate/free of their own size (new_states); None: never.
 RECYCLE_MIN_BYTES: int | None = 256 << 20
@@ -53,7 +54,7 @@ def choose_layout(algorithm: str, precision: str, master_precision: str, request
     there is one and the master is an FP32 buffer of the optimizer's own, else 'separate'."""
     if requested == "separate" or master_is_param or master_precision != "fp32":
         return "separate"
-    return {("adamw", "bf16"): "pairs", ("adamw", "fp8"): "fp8-records",
+    return {("adamw", "bf16"): "pairs", ("adamw", "fp8"): "fp8-records", ("adamw", "fp32"): "f32-records",
             ("lion", "bf16"): "lion-records"}.get((algorithm, precision), "separate")
 
 
@@ -357,6 +358,45 @@ class LionRecordState(_Interleaved):
         return {"p": self._column("p").reshape(-1)[lo:hi], "m": self._column("m").reshape(-1)[lo:hi]}
 
 
+class F32RecordState(_Interleaved):
+    """AdamW, FP32 master, FP32 moments: 3072-byte records of 256 elements, the 256 masters, then the
+    256 m, then the 256 v values, each in element order (ADAMBRIDGE_DT_PACKED_F32)."""
+
+    layout = "f32-records"
+    precision = "fp32"
+
+    def __init__(self, numel, device, double_buffer: bool = False, memory: list[torch.Tensor] | None = None):
+        records = max(1, -(-int(numel) // 256))
+        bufs = [m.view(records, 3072) for m in memory] if memory else \
+            [torch.zeros(records, 3072, dtype=torch.uint8, device=device) for _ in range(2 if double_buffer else 1)]
+        super().__init__(numel, device, ("m", "v"), bufs)
+
+    @staticmethod
+    def buffer_bytes(numel: int) -> int:
+        return max(1, -(-int(numel) // 256)) * 3072
+
+    def bind(self, seg):
+        seg.p, seg.p_lo = self.current.data_ptr(), _ptr(self.target)
+        seg.m = seg.v = seg.m_scale = seg.v_scale = None
+        seg.p_dtype, seg.mv_dtype = _hip.DT_PACKED_F32, _hip.DT_F32
+
+    def _column(self, role):
+        k = {"p": 0, "m": 1, "v": 2}[role]
+        return self.current[:, 1024 * k:1024 * (k + 1)].view(torch.float32)
+
+    def moment(self, role):
+        return FP32Store(self.numel, init=self._column(role).reshape(-1)[: self.numel], device=self.device)
+
+    def load(self, master=None, moments=None):
+        if master is not None:
+            self._put("p", _as_master_values(master, self.numel, self.device))
+        for role, store in (moments or {}).items():
+            self._put(role, store.to_fp32().to(self.device))
+
+    def window(self, lo, hi):
+        return {r: self._column(r).reshape(-1)[lo:hi] for r in ("p", "m", "v")}
+
+
 class AdamRecordState(_Interleaved):
     """AdamW, FP32 master, FP8 moments: one 768-byte record per 128-element block
     (ADAMBRIDGE_DT_PACKED_FP8) -- lane l's elements 8l .. 8l + 7 keep their masters at 16l (first
@@ -430,7 +470,8 @@ def _bf16_bits(store: MomentStore, device) -> torch.Tensor:
 
 # -------------------------------------------------------------------- building
 
-_INTERLEAVED = {"pairs": PairState, "lion-records": LionRecordState, "fp8-records": AdamRecordState}
+_INTERLEAVED = {"pairs": PairState, "lion-records": LionRecordState, "fp8-records": AdamRecordState,
+                "f32-records": F32RecordState}
 ARENA_ALIGN = 2 << 20
 
 

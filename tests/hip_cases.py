@@ -382,3 +382,86 @@ def run_hip_lion_records(cases: list[O.Case], width: int = 16, double_buffer: bo
         if out is not None:
             c.arrays["out"] = from_device(out, c.arrays["out"])
     return work
+
+
+def pack_f32_records(case: O.Case) -> np.ndarray:
+    """Separate FP32 master, m and v -> ADAMBRIDGE_DT_PACKED_F32 records (records x 3072 bytes): per
+    256 elements, the 256 masters, the 256 m, the 256 v, each in element order.  Padding slots hold
+    a fixed NaN pattern so that a test can see the kernel leave them unchanged."""
+    n = case.n
+    nr = max(1, -(-n // 256))
+    rec = np.zeros((nr, 3, 256), np.uint32)
+    for k, key in enumerate(("p", "m", "v")):
+        col = np.full(nr * 256, 0x7FA5A5A5 + k, np.uint32)
+        col[:n] = case.arrays[key].view(np.uint32)
+        rec[:, k, :] = col.reshape(nr, 256)
+    return rec.reshape(nr, 768).view(np.uint8).reshape(nr, 3072)
+
+
+def unpack_f32_records(case: O.Case, rec: np.ndarray) -> list[np.ndarray]:
+    """ADAMBRIDGE_DT_PACKED_F32 records -> the case's separate master, m and v (in place); returns
+    the padding slots (bits) past n of each."""
+    n = case.n
+    cols = np.ascontiguousarray(rec).view(np.uint32).reshape(-1, 3, 256)
+    pads = []
+    for k, key in enumerate(("p", "m", "v")):
+        col = cols[:, k, :].reshape(-1)
+        case.arrays[key] = col[:n].view(np.float32).copy()
+        pads.append(col[n:].copy())
+    return pads
+
+
+def run_hip_f32_records(cases: list[O.Case], width: int = 16, double_buffer: bool = False,
+                        misalign_g: int = 0, padding: list | None = None, seg_flags: int = 0) -> list[O.Case]:
+    """Like run_hip for AdamW / FP32 master / FP32 moment cases, through the record layout
+    (ADAMBRIDGE_DT_PACKED_F32): pack on the host, one call, unpack the result.  ``misalign_g``
+    elements shift the gradient off its allocation's alignment; ``padding`` receives each case's
+    padding slots after the call."""
+    kernels = _hip.load()
+    work = [c.copy() for c in cases]
+    entries, segs = [], []
+    by_group = all(c.group is not None for c in work)
+    for c in work:
+        assert c.algorithm == O.ADAMW and c.mv_dtype == O.DT_F32 and c.p_dtype == O.DT_F32
+        O.check_sizes(c)
+        rec = torch.from_numpy(pack_f32_records(c)).cuda()
+        dst = torch.full_like(rec, 0x5A) if double_buffer else None
+        g = to_device(c.arrays["g"])
+        keep = []
+        if misalign_g:
+            buf = torch.empty(g.numel() + int(misalign_g), dtype=g.dtype, device=g.device)
+            buf[int(misalign_g):].copy_(g)
+            keep.append(buf)
+            g = buf[int(misalign_g):]
+        out = to_device(c.arrays["out"]) if "out" in c.arrays else None
+        grp = None
+        if by_group:
+            grp = _hip.Group(**{k: c.group[k] for k in ("lr", "beta1", "beta2", "eps", "weight_decay")},
+                             seed=c.group["seed"] & (2**64 - 1), stochastic=int(c.group["stochastic"]))
+        entries.append((rec, dst, g, out, grp, keep))
+        segs.append(_hip.Segment(p=rec.data_ptr(), p_lo=dst.data_ptr() if dst is not None else None,
+                                 g=g.data_ptr(), m=None, v=None, out=out.data_ptr() if out is not None else None,
+                                 group=ctypes.pointer(grp) if grp is not None else None, n=c.n, step=c.step,
+                                 index=c.index, offset=c.offset, g_dtype=c.g_dtype, mv_dtype=O.DT_F32,
+                                 out_dtype=c.out_dtype, algorithm=O.ADAMW, p_dtype=_hip.DT_PACKED_F32,
+                                 reserved=seg_flags))
+    arr = kernels.segment_array([ctypes.pointer(s) for s in segs])
+    kernels.set_simd_level(WIDTH_LEVEL[width])
+    try:
+        kernels.set_stream(torch.cuda.current_stream())
+        if by_group:
+            kernels.multi_step(None, arr)
+        else:
+            hps = [_hip.HParams(**{k: c.hparams[k] for k, _ in _hip.HParams._fields_}) for c in work]
+            kernels.multi_apply(None, arr, hps)
+        torch.cuda.synchronize()
+    finally:
+        kernels.set_simd_level(None)
+    for c, (rec, dst, g, out, grp, keep) in zip(work, entries):
+        pad = unpack_f32_records(c, (dst if dst is not None else rec).cpu().numpy())
+        if padding is not None:
+            padding.append(pad)
+        if out is not None:
+            c.arrays["out"] = from_device(out, c.arrays["out"])
+    return work
+

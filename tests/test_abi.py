@@ -52,7 +52,7 @@ def test_header_codes_match_the_python_mirror():
     codes = {name: int(v) for name, v in re.findall(r"ADAMBRIDGE_(DT_\w+)\s*=\s*(\d+)", text)}
     mirror = {"DT_NONE": _hip.DT_NONE, "DT_F32": _hip.DT_F32, "DT_BF16": _hip.DT_BF16, "DT_FP8": _hip.DT_FP8,
               "DT_F24": _hip.DT_F24, "DT_PACKED": _hip.DT_PACKED, "DT_PACKED_FP8": _hip.DT_PACKED8,
-              "DT_PACKED_LION": _hip.DT_PACKED_LION}
+              "DT_PACKED_LION": _hip.DT_PACKED_LION, "DT_PACKED_F32": _hip.DT_PACKED_F32}
     assert codes == mirror
     flag = re.search(r"#define ADAMBRIDGE_SEG_OUT_PREVIOUS (\d+)", text)
     assert flag and int(flag.group(1)) == _hip.SEG_OUT_PREVIOUS

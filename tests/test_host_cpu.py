@@ -305,6 +305,32 @@ def test_lion_and_pair_layout_offsets(n):
     assert pairs.current.data_ptr() != pairs.buffers[0].data_ptr() and pairs.target is pairs.buffers[0]
 
 
+@pytest.mark.parametrize("n", [1, 255, 256, 257, 1000])
+def test_f32_record_layout_offsets(n):
+    """F32RecordState: element 256r + i (i < 256) keeps its master at byte 4i of record r, its m at
+    1024 + 4i and its v at 2048 + 4i (ADAMBRIDGE_DT_PACKED_F32); moments and windows read back the
+    values loaded, double buffering alternates the buffers."""
+    from adambridge_amd.state import F32RecordState
+    rng = np.random.default_rng(n + 11)
+    vals = {r: rng.normal(0, 1, n).astype(np.float32) for r in ("p", "m", "v")}
+    st = F32RecordState(n, "cpu", double_buffer=True)
+    assert F32RecordState.buffer_bytes(n) == -(-n // 256) * 3072 == st.current.nbytes
+    st.load(master=torch.from_numpy(vals["p"]),
+            moments={r: P.FP32Store(n, init=torch.from_numpy(vals[r])) for r in ("m", "v")})
+    rec = st.current.numpy()
+    for e in range(n):
+        r, i = divmod(e, 256)
+        for k, role in enumerate(("p", "m", "v")):
+            assert rec[r, 1024 * k + 4 * i:1024 * k + 4 * i + 4].view(np.float32)[0] == vals[role][e]
+    assert np.array_equal(st.master_fp32().numpy(), vals["p"])
+    for role in ("m", "v"):
+        assert np.array_equal(st.moment(role).to_fp32().numpy(), vals[role])
+    w = st.window(n // 3, n)
+    assert np.array_equal(w["v"].numpy(), vals["v"][n // 3:])
+    st.advance()
+    assert st.target is st.buffers[0] and st.current.data_ptr() == st.buffers[1].data_ptr()
+
+
 def test_fp24_master_store_round_trip():
     n = 1000
     x = torch.randn(n) * 3

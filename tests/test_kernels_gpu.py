@@ -415,6 +415,85 @@ def test_lion_records_reject_bad_segments():
     assert torch.count_nonzero(rec).item() == 0   # nothing ran
 
 
+# ------------------------------------------------ FP32-moment AdamW records
+
+from hip_cases import run_hip_f32_records  # noqa: E402
+
+
+@pytest.mark.parametrize("double_buffer", [False, True])
+def test_f32_records_match_oracle(double_buffer):
+    """ADAMBRIDGE_DT_PACKED_F32 (master, m and v FP32 in 3072-byte records) gives the separate
+    layout's bytes: sizes around the record, the lane's 4 elements and the reproduced SIMD widths'
+    tails (fused body, unfused scalar tail at widths 16, 8 and 0), offsets, every grad/out dtype; in
+    place, the padding slots of the last record keep their bits."""
+    rng = np.random.default_rng(51)
+    cases = []
+    for gt, ot, n in itertools.product([O.DT_BF16, O.DT_F32], [O.DT_NONE, O.DT_F32, O.DT_BF16],
+                                       [1, 2, 3, 4, 5, 15, 16, 17, 255, 256, 257, 1000, 2048 + 77, 5001]):
+        cases.append(O.make_case(rng, n, mv_dtype=O.DT_F32, g_dtype=gt, out_dtype=ot,
+                                 stochastic=bool(rng.integers(0, 2)), offset=int(rng.integers(0, 2**32)),
+                                 index=int(rng.integers(0, 999)), step=int(rng.integers(1, 30))))
+    for width in (16, 8, 0):
+        want = O.run_many(cases, "oracle", width)
+        pads: list = []
+        got = run_hip_f32_records(cases, width, double_buffer=double_buffer, padding=pads)
+        for w, g in zip(want, got):
+            check(w, g)
+        if not double_buffer:
+            for pad, c in zip(pads, cases):
+                for k, col in enumerate(pad):
+                    assert (col == 0x7FA5A5A5 + k).all(), f"padding changed at n={c.n}"
+
+
+def test_f32_records_misaligned_gradient_and_specials():
+    """Gradients shifted by one element (the element-wise path) and by two, and non-finite inputs
+    (zeros, subnormals, infinities, NaNs in every input)."""
+    rng = np.random.default_rng(52)
+    cases = [O.make_case(rng, n, mv_dtype=O.DT_F32, special=sp) for n, sp in
+             ((999, False), (4096, False), (4096, True), (5001, True))]
+    want = O.run_many(cases, "oracle", 16)
+    for shift in (1, 2):
+        got = run_hip_f32_records(cases, 16, misalign_g=shift)
+        for w, g in zip(want, got):
+            bad = O.outputs_equal(w, g, nan_equiv=True)
+            assert not bad, (shift, bad)
+
+
+def test_f32_records_multi_step_groups_and_steps():
+    """Several segments per call through the group path, then three consecutive steps of one."""
+    rng = np.random.default_rng(53)
+    cases = [O.make_case(rng, 3000 + 64 * k + 3, mv_dtype=O.DT_F32, explicit=False, index=k, step=k + 2, seed=5)
+             for k in range(12)]
+    want = O.run_many(cases, "oracle", 16)
+    got = run_hip_f32_records(cases, 16)
+    for w, g in zip(want, got):
+        check(w, g)
+    case = O.make_case(rng, 5000, mv_dtype=O.DT_F32)
+    grads = [O.make_case(rng, 5000, mv_dtype=O.DT_F32).arrays["g"] for _ in range(3)]
+    check(run_steps(case, grads, oracle_runner, 16), run_steps(case, grads, run_hip_f32_records, 16))
+
+
+def test_f32_records_reject_bad_segments():
+    """Lion (-12), BF16 moments (-4), a missing gradient (-2) and misaligned records (-14), before
+    anything runs."""
+    import ctypes
+    from adambridge_amd import _hip
+    rng = np.random.default_rng(54)
+    k = _hip.load()
+    case = O.make_case(rng, 300, mv_dtype=O.DT_F32)
+    rec = torch.zeros(2 * 3072 + 16, dtype=torch.uint8, device="cuda")
+    g = torch.zeros(300, dtype=torch.bfloat16, device="cuda")
+    hp = _hip.HParams(**{kk: case.hparams[kk] for kk, _ in _hip.HParams._fields_})
+    base = dict(p=rec.data_ptr(), g=g.data_ptr(), n=300, step=1, mv_dtype=O.DT_F32, g_dtype=O.DT_BF16,
+                out_dtype=0, algorithm=0, p_dtype=_hip.DT_PACKED_F32)
+    for change, code in ((dict(algorithm=1), -12), (dict(mv_dtype=O.DT_BF16), -4), (dict(g=None), -2),
+                         (dict(p=rec.data_ptr() + 8), -14), (dict(p_lo=rec.data_ptr() + 4), -14)):
+        seg = _hip.Segment(**{**base, **change})
+        with pytest.raises(RuntimeError, match=rf"code {code}"):
+            k.multi_apply(None, k.segment_array([ctypes.pointer(seg)]), [hp])
+    assert torch.count_nonzero(rec).item() == 0   # nothing ran
+
+
 # ------------------------------------------------ fused_adamw, pools, streams
 
 @pytest.mark.parametrize("mv", [O.DT_F32, O.DT_BF16])
@@ -561,20 +640,20 @@ def _previous_weight(case):
     return O.bf16_bits(old) if case.out_dtype == O.DT_BF16 else old.astype(np.float32)
 
 
-@pytest.mark.parametrize("layout", ["separate", "pairs", "fp8-records", "lion-records"])
+@pytest.mark.parametrize("layout", ["separate", "pairs", "fp8-records", "lion-records", "f32-records"])
 def test_out_previous_writes_the_weight_from_before_the_update(layout):
     """ADAMBRIDGE_SEG_OUT_PREVIOUS (delayed updates): out receives the weight of the master as stored
     before the update -- FP32, or bf16 by the kernels' rounding of FP32 and decoded FP24 masters,
     NaN masters included -- and the state is updated exactly as without the flag."""
-    from hip_cases import run_hip_lion_records, run_hip_packed, run_hip_records
+    from hip_cases import run_hip_f32_records, run_hip_lion_records, run_hip_packed, run_hip_records
     from adambridge_amd import _hip
 
     rng = np.random.default_rng(31 + len(layout))
     combos = {"separate": [(a, mv, pt) for a in ALGOS for mv in MVS for pt in PTS],
               "pairs": [(O.ADAMW, O.DT_BF16, O.DT_F32)], "fp8-records": [(O.ADAMW, O.DT_FP8, O.DT_F32)],
-              "lion-records": [(O.LION, O.DT_BF16, O.DT_F32)]}[layout]
+              "lion-records": [(O.LION, O.DT_BF16, O.DT_F32)], "f32-records": [(O.ADAMW, O.DT_F32, O.DT_F32)]}[layout]
     runner = {"separate": run_hip, "pairs": run_hip_packed, "fp8-records": run_hip_records,
-              "lion-records": run_hip_lion_records}[layout]
+              "lion-records": run_hip_lion_records, "f32-records": run_hip_f32_records}[layout]
     cases = []
     for (algo, mv, pt), gt, ot, sr, n in itertools.product(combos, [O.DT_BF16, O.DT_F32], [O.DT_F32, O.DT_BF16],
                                                              [True, False], [1, 15, 17, 129, 1000, 8192 + 77]):

@@ -972,12 +972,12 @@ def test_multi_tensor_launch_count():
     opt.close()
 
 
-@pytest.mark.parametrize("precision", ["bf16", "fp8"])
+@pytest.mark.parametrize("precision", ["bf16", "fp8", "fp32"])
 @pytest.mark.parametrize("hooks", [False, True])
 def test_state_layouts_give_identical_bytes(hooks, precision):
-    """The interleaved layouts (default: BF16 pairs, FP8 block records), the separate layout and
-    the double-buffered interleaved layout produce the same weights, masters and moments (FP8:
-    codes and scales), step after step."""
+    """The interleaved layouts (default: BF16 pairs, FP8 block records, FP32 records), the separate
+    layout and the double-buffered interleaved layout produce the same weights, masters and moments
+    (FP8: codes and scales), step after step."""
     results = []
     for kw in (dict(state_layout="separate"), dict(), dict(double_buffer=True)):
         torch.manual_seed(0)
@@ -1006,9 +1006,10 @@ def test_state_layouts_give_identical_bytes(hooks, precision):
             assert all(torch.equal(x, y) for x, y in zip(xs, ys))
 
 
-@pytest.mark.parametrize("algo,precision", [("adamw", "bf16"), ("adamw", "fp8"), ("lion", "bf16")])
+@pytest.mark.parametrize("algo,precision", [("adamw", "bf16"), ("adamw", "fp8"), ("lion", "bf16"),
+                                            ("adamw", "fp32")])
 def test_interleaved_checkpoint_gathered_on_host_when_the_device_is_short(algo, precision):
-    """Interleaved states (BF16 pairs, FP8 records, Lion records) are gathered into the reference's
+    """Interleaved states (BF16 pairs, FP8 records, Lion records, FP32 records) are gathered into the reference's
     checkpoint arrays on the device when it has room, else into host memory parameter by parameter;
     either checkpoint loads into a fresh optimizer with identical masters and moments."""
     torch.manual_seed(0)
@@ -1082,7 +1083,7 @@ def test_packed_state_checkpoint_and_set_precision(precision):
         other.close()
     m_before = [s.m.to_fp32() for s in opt._ordered]
     opt.set_precision("fp32")
-    assert all(s.state.layout == "separate" for s in opt._ordered)
+    assert all(s.state.layout == "f32-records" for s in opt._ordered)   # bf16 parameters: FP32 records
     for s, m in zip(opt._ordered, m_before):
         assert torch.equal(s.m.to_fp32(), m)
     opt.set_precision(precision)
