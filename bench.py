@@ -48,8 +48,8 @@ HBM_PEAK_GBS = 8000.0
 # counters cannot be read from inside the process they profile); each figure's run is in its file.
 MEASURED_TRAFFIC = {"c3p": 134.767e9, "c1": 469.84e6, "c2": 9.8808e9, "c3": 108.67e9, "c4": 24.700e9}
 TRAFFIC_PROFILE = {"c3p": "profiles/k_update_packed_c3p_hbm_traffic.md",
-                   "c1": "profiles/k_update_c1_packed_c2_trace_traffic.md",
-                   "c2": "profiles/k_update_c1_packed_c2_trace_traffic.md",
+                   "c1": "profiles/k_update_f32rec_c1_packed_c2_trace_traffic.md",
+                   "c2": "profiles/k_update_f32rec_c1_packed_c2_trace_traffic.md",
                    "c3": "profiles/k_update_fp8_c3_trace_traffic_instructions.md",
                    "c4": "profiles/k_update_lion_rec_c4_trace_traffic.md"}
 
