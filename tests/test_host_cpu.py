@@ -605,3 +605,17 @@ def test_command_line_info_reports_the_library():
     usage = subprocess.run([sys.executable, "-m", "adambridge_amd", "nonsense"], cwd=root, capture_output=True,
                            text=True, timeout=120)
     assert usage.returncode == 2 and "{build,info}" in usage.stderr
+
+
+def test_layout_choice_for_every_algorithm_precision_and_master():
+    """Each (algorithm, moment precision) with an FP32 master of the optimizer's own gets its
+    interleaved layout; an FP24 master, an FP32 parameter updated in place, Lion without a record
+    layout for its precision, and state_layout='separate' keep the reference's arrays."""
+    from adambridge_amd.state import choose_layout
+    want = {("adamw", "bf16"): "pairs", ("adamw", "fp8"): "fp8-records", ("adamw", "fp32"): "f32-records",
+            ("lion", "bf16"): "lion-records", ("lion", "fp8"): "separate", ("lion", "fp32"): "separate"}
+    for (algo, prec), layout in want.items():
+        assert choose_layout(algo, prec, "fp32") == layout, (algo, prec)
+        assert choose_layout(algo, prec, "fp24") == "separate"
+        assert choose_layout(algo, prec, "fp32", master_is_param=True) == "separate"
+        assert choose_layout(algo, prec, "fp32", requested="separate") == "separate"
