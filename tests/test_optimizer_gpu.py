@@ -575,6 +575,44 @@ def test_param_group_added_after_steps_trains_like_torch_adamw(hooks):
     opt.close()
 
 
+@pytest.mark.parametrize("precision", ["fp32", "bf16", "fp8"])
+@pytest.mark.parametrize("hooks", [False, True])
+def test_empty_parameters_beside_others(precision, hooks):
+    """A parameter with no elements (an empty bias, a zero-width embedding) takes part in every step,
+    checkpoint and rebuild without touching memory, and the others train as torch AdamW does."""
+    torch.manual_seed(0)
+    shapes = [(64, 48), (0,), (48,), (0, 16)]
+    params = [torch.nn.Parameter(torch.randn(s, device=DEV) * 0.1) for s in shapes]
+    ref_params = [torch.nn.Parameter(p.detach().clone()) for p in params]
+    opt = ab.AdamBridge(params, lr=1e-2, precision=precision, small_param_threshold=0)
+    ref = torch.optim.AdamW(ref_params, lr=1e-2)
+    if hooks:
+        opt.attach_hooks()
+    for step in range(4):
+        grads = [torch.randn(s, device=DEV) * 1e-2 for s in shapes]
+        for ps, o in ((params, opt), (ref_params, ref)):
+            o.zero_grad(set_to_none=True)
+            for p, g in zip(ps, grads):
+                p.grad = g.clone()
+            if o is opt and hooks:
+                o.step_sync()   # gradients set by hand fire no hook: step_sync updates none of them
+                o.step()
+            else:
+                o.step()
+    tol = 1e-6 if precision == "fp32" else 5e-2
+    for p, r in zip(params, ref_params):
+        assert p.shape == r.shape
+        assert p.numel() == 0 or (p - r).abs().max().item() < tol
+    sd = opt.state_dict()
+    assert sd["state"][1]["master"].numel() == 0
+    other = ab.AdamBridge([torch.nn.Parameter(torch.zeros(s, device=DEV)) for s in shapes], lr=1e-2,
+                          precision=precision, small_param_threshold=0)
+    other.load_state_dict(sd)
+    opt.set_precision("bf16" if precision != "bf16" else "fp32")
+    opt.close()
+    other.close()
+
+
 def test_weights_loaded_after_construction_are_respected():
     """reference test_optimizer.py:141-150: lazy master."""
     model = tiny_mlp(seed=0, device=DEV)
