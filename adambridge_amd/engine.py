@@ -41,7 +41,7 @@ import torch
 from . import _hip
 from .formats import bf16_weight
 from .precision import MomentStore, make_store
-from .state import ParamState, choose_layout, new_states
+from .state import ParamState, arena_memory, choose_layout, new_states
 
 __all__ = ["UpdateEngine", "ParamSlot", "SmallGroup", "StepStats"]
 
@@ -188,6 +188,9 @@ class UpdateEngine:
         self._update_events: list[tuple[torch.cuda.Event, torch.cuda.Event]] = []
         self._used: set[torch.device] = set()
         self.launch_log: list | None = None   # a list: (start, end, elements) of every launch, read after a sync
+        self.hooked_slots: list[ParamSlot] = []   # the parameters gradient hooks update (set by the optimizer)
+        self._reserved: dict[ParamSlot, list[torch.Tensor]] = {}   # arena memory set aside for hooked states
+        self._reserved_on: set[torch.device] = set()
         self._closed = False
 
     # ----------------------------------------------------------------- state
@@ -222,7 +225,11 @@ class UpdateEngine:
         """Lazy state for ``slots`` (engine.py:991-1025; precision.py:263-267, 307-311, 365-371): the master
         from each parameter's current value (FP32, or FP24 rounded to nearest), moments zero, FP8
         scales one.  The interleaved states of one device and layout share one arena, placed by an
-        allocate/free of its size first unless ``place`` is False (see state.new_states)."""
+        allocate/free of its size first unless ``place`` is False (see state.new_states).  Without
+        ``place`` (a gradient hook), the first call on a device sets aside one placed arena for the
+        interleaved states of every hooked parameter not initialized yet (``hooked_slots``), and each
+        state is built on its share when its parameter's first update comes -- one placement, one
+        wait for the device, instead of one allocation per parameter where the driver puts it."""
         for slot in slots:
             self.check_param(slot.param)
         todo: dict[tuple[torch.device, str], list[ParamSlot]] = {}
@@ -230,13 +237,37 @@ class UpdateEngine:
             todo.setdefault((slot.param.device, self.layout_for(slot)), []).append(slot)
         for (device, layout), members in todo.items():
             with torch.cuda.device(device), torch.no_grad():
-                masters = [s.param.detach().reshape(-1) for s in members]
-                params = [s.param if self._master_is_param(s.param) else None for s in members]
-                states = new_states(layout, self.algorithm, self.precision, self.master_precision, device, masters,
-                                    self.double_buffer, params, place)
-                for slot, state in zip(members, states):
-                    self._adopt(slot, state)
-                    self._ensure_out(slot)
+                if not place:
+                    self._reserve(device)
+                for group in ([s for s in members if s in self._reserved],
+                              [s for s in members if s not in self._reserved]):
+                    if not group:
+                        continue
+                    memory = [self._reserved.pop(s) for s in group] if group[0] in self._reserved else None
+                    masters = [s.param.detach().reshape(-1) for s in group]
+                    params = [s.param if self._master_is_param(s.param) else None for s in group]
+                    states = new_states(layout, self.algorithm, self.precision, self.master_precision, device,
+                                        masters, self.double_buffer, params, place, memory)
+                    for slot, state in zip(group, states):
+                        self._adopt(slot, state)
+                        self._ensure_out(slot)
+
+    def _reserve(self, device: torch.device) -> None:
+        """Once per device: one placed arena per interleaved layout for the hooked parameters on
+        ``device`` that have no state yet (see :meth:`initialize`)."""
+        if device in self._reserved_on:
+            return
+        self._reserved_on.add(device)
+        by_layout: dict[str, list[ParamSlot]] = {}
+        for slot in self.hooked_slots:
+            if slot.initialized or slot in self._reserved or slot.param.device != device:
+                continue
+            layout = self.layout_for(slot)
+            if layout != "separate":
+                by_layout.setdefault(layout, []).append(slot)
+        for layout, members in by_layout.items():
+            memory = arena_memory(layout, [s.numel for s in members], device, self.double_buffer)
+            self._reserved.update(zip(members, memory))
 
     @staticmethod
     def _adopt(slot: ParamSlot, state: ParamState) -> None:
@@ -253,6 +284,8 @@ class UpdateEngine:
         precision = precision or self.precision
         masters = masters or [None] * len(slots)
         moments = moments or [None] * len(slots)
+        self._reserved.clear()   # set aside for the old precision's layout; set aside again on the next hook
+        self._reserved_on.clear()
         groups: dict[tuple[torch.device, str], list[int]] = {}
         for i, slot in enumerate(slots):
             self.check_param(slot.param)
@@ -532,6 +565,7 @@ class UpdateEngine:
         if self._closed:
             return
         self._closed = True
+        self._reserved.clear()
         try:
             self.wait()
         except Exception:  # noqa: BLE001 -- a finalizer must not raise

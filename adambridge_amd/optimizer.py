@@ -389,8 +389,10 @@ class AdamBridge(torch.optim.Optimizer):
         """Update each parameter as soon as its gradient is ready (optimizer.py:255-269): the
         parameters of ``model`` (default: all) that require gradients and are not small."""
         if not self._hooks.active:
-            self._hooks.add(self._registry.hook_targets(None if model is None else model.parameters()))
+            targets = self._registry.hook_targets(None if model is None else model.parameters())
+            self._hooks.add(targets)
             self._hooks.active = True
+            self._engine.hooked_slots = [self._registry.by_param[p] for p in targets]
         return self
 
     def detach_hooks(self) -> None:

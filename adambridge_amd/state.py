@@ -40,7 +40,7 @@ from . import formats as F
 from .precision import BF16Store, FP8Store, FP24Store, FP32Store, MomentStore, load_master_, make_master, make_store
 
 __all__ = ["ParamState", "SeparateState", "PairState", "AdamRecordState", "LionRecordState", "F32RecordState",
-           "choose_layout", "new_state", "new_states", "arena_plan", "LAYOUTS"]
+           "choose_layout", "new_state", "new_states", "arena_plan", "arena_memory", "LAYOUTS"]
 
 LAYOUTS = ("separate", "pairs", "fp8-records", "lion-records", "f32-records")
 
@@ -498,7 +498,8 @@ def _place(nbytes: int, device, place: bool) -> None:
 
 def new_states(layout: str, algorithm: str, precision: str, master_precision: str, device,
                masters: list[torch.Tensor], double_buffer: bool = False,
-               master_params: list[torch.Tensor | None] | None = None, place: bool = True) -> list[ParamState]:
+               master_params: list[torch.Tensor | None] | None = None, place: bool = True,
+               memory: list[list[torch.Tensor]] | None = None) -> list[ParamState]:
     """Fresh states for several parameters on one device: master from ``masters[i]`` (any dtype;
     FP24 rounds to nearest) or, in the separate layout, the FP32 parameter ``master_params[i]`` itself;
     moments zero, FP8 scales one.
@@ -512,9 +513,9 @@ def new_states(layout: str, algorithm: str, precision: str, master_precision: st
     copy's rate: 20.63 against 21.43 ms for that first build, and 30.13 against 31.49 ms with FP32
     moments in separate arrays (the driver's first placements in a fresh process stream this
     update 3-4% slower; measured on MI355X, cause unknown).  The allocate/free holds no more memory
-    than the state; it
-    waits for the device to go idle (the free does), so ``place=False`` skips it where that would
-    stall a pipeline (the states a gradient hook creates during the first backward pass)."""
+    than the state; it waits for the device to go idle (the free does), so ``place=False`` skips it
+    where that would stall a pipeline.  ``memory``: zeroed buffers of an arena made earlier (arena_memory), one list
+    per state, used instead of a new arena (interleaved layouts)."""
     roles = ("m",) if algorithm == "lion" else ("m", "v")
     if layout == "separate":
         # the stores are allocations of their own; the same placement step covers them all at once
@@ -537,16 +538,25 @@ def new_states(layout: str, algorithm: str, precision: str, master_precision: st
         raise ValueError(f"unknown state layout {layout!r}; expected one of {LAYOUTS}")
     cls = _INTERLEAVED[layout]
     sizes = [t.numel() for t in masters]
-    offsets, total = arena_plan(layout, sizes, double_buffer)
-    _place(total, device, place)
-    arena = torch.zeros(total, dtype=torch.uint8, device=device)
+    if memory is None:
+        memory = arena_memory(layout, sizes, device, double_buffer, place)
     states = []
-    for n, offs, values in zip(sizes, offsets, masters):
-        memory = [arena[o: o + cls.buffer_bytes(n)] for o in offs]
-        state = cls(n, device, double_buffer, memory=memory)
+    for n, mem, values in zip(sizes, memory, masters):
+        state = cls(n, device, double_buffer, memory=mem)
         state.load(master=values.detach().reshape(-1).to(device=device, dtype=torch.float32))
         states.append(state)
     return states
+
+
+def arena_memory(layout: str, sizes: list[int], device, double_buffer: bool = False,
+                 place: bool = True) -> list[list[torch.Tensor]]:
+    """Zeroed device memory for interleaved states of ``sizes`` elements in one arena (placed as in
+    new_states unless ``place`` is False): for each state, its buffer (two when double-buffered)."""
+    cls = _INTERLEAVED[layout]
+    offsets, total = arena_plan(layout, sizes, double_buffer)
+    _place(total, device, place)
+    arena = torch.zeros(total, dtype=torch.uint8, device=device)
+    return [[arena[o: o + cls.buffer_bytes(n)] for o in offs] for n, offs in zip(sizes, offsets)]
 
 
 def new_state(layout: str, algorithm: str, precision: str, master_precision: str, numel: int, device,

@@ -613,6 +613,45 @@ def test_empty_parameters_beside_others(precision, hooks):
     other.close()
 
 
+@pytest.mark.parametrize("precision", ["bf16", "fp8", "fp32"])
+def test_hooked_states_share_one_arena_and_stay_lazy(precision):
+    """The first hook sets aside one arena for every hooked parameter's interleaved state; each state
+    is still built at its parameter's first update, from the value the parameter holds then (a
+    parameter without a gradient in the first step, changed before its first update), and the
+    results equal, bit for bit, those of the same steps through step()."""
+    results = []
+    for hooks in (True, False):
+        torch.manual_seed(0)
+        model = TinyLM().to(DEV).to(torch.bfloat16)
+        opt = ab.AdamBridge(model.parameters(), lr=3e-3, precision=precision, small_param_threshold=2000)
+        if hooks:
+            opt.attach_hooks(model)
+        head = model.blocks[-1][3].weight
+        head.requires_grad_(False)   # no gradient in the first step
+        lm_loss(model, 0).backward()
+        opt.step() if not hooks else opt.step_sync()
+        slot = opt._slots[head]
+        assert not slot.initialized
+        if hooks:
+            hooked = [s for s in opt._ordered if s.small is None and s.initialized]
+            assert len({s.state.current.untyped_storage().data_ptr() for s in hooked}) == 1
+            assert slot in opt._engine._reserved
+        with torch.no_grad():
+            head.mul_(0.5)           # changed before its first update
+        head.requires_grad_(True)
+        for step in range(1, 4):
+            opt.zero_grad(set_to_none=True)
+            lm_loss(model, step).backward()
+            opt.step() if not hooks else opt.step_sync()
+        if hooks:
+            assert slot.state.current.untyped_storage().data_ptr() == hooked[0].state.current.untyped_storage().data_ptr()
+            assert not opt._engine._reserved
+        results.append(([p.detach().clone() for p in model.parameters()], [m.clone() for m in opt.master_params()]))
+        opt.close()
+    for xs, ys in zip(*results):
+        assert all(torch.equal(x, y) for x, y in zip(xs, ys))
+
+
 def test_weights_loaded_after_construction_are_respected():
     """reference test_optimizer.py:141-150: lazy master."""
     model = tiny_mlp(seed=0, device=DEV)
