@@ -619,3 +619,27 @@ def test_layout_choice_for_every_algorithm_precision_and_master():
         assert choose_layout(algo, prec, "fp24") == "separate"
         assert choose_layout(algo, prec, "fp32", master_is_param=True) == "separate"
         assert choose_layout(algo, prec, "fp32", requested="separate") == "separate"
+
+
+@pytest.mark.parametrize("layout", ["pairs", "fp8-records", "lion-records", "f32-records"])
+def test_arena_plan_aligns_large_buffers_and_packs_small_ones(layout):
+    """Buffers of 2 MiB or more start on 2 MiB boundaries, smaller ones on 256-byte boundaries (16-byte
+    state access needs 16); no two buffers overlap, and many small tensors take little more than
+    their own bytes."""
+    from adambridge_amd import state as S
+    cls = S._INTERLEAVED[layout]
+    sizes = [4096, 1 << 20, 3, 896, 300_000, 1 << 18, 4096] * 3
+    for double in (False, True):
+        offsets, total = S.arena_plan(layout, sizes, double)
+        spans = []
+        for n, offs in zip(sizes, offsets):
+            nbytes = cls.buffer_bytes(n)
+            assert len(offs) == (2 if double and layout != "fp8-records" else 1)
+            for o in offs:
+                assert o % (S.ARENA_ALIGN if nbytes >= S.ARENA_ALIGN else S.SMALL_ALIGN) == 0
+                spans.append((o, o + nbytes))
+        spans.sort()
+        assert all(a[1] <= b[0] for a, b in zip(spans, spans[1:])) and spans[-1][1] <= total
+    small = [896] * 1000
+    _, total = S.arena_plan(layout, small)
+    assert total < 1000 * (cls.buffer_bytes(896) + S.SMALL_ALIGN)
