@@ -45,12 +45,14 @@ from .state import ParamState, arena_memory, choose_layout, new_states
 
 __all__ = ["UpdateEngine", "ParamSlot", "SmallGroup", "StepStats"]
 
+_GRAD_CODES = {torch.bfloat16: _hip.DT_BF16, torch.float32: _hip.DT_F32}
+
 
 class ParamSlot:
     """One parameter: its index (rounding stream), group, step count, state and kernel descriptor."""
 
     __slots__ = ("index", "param", "group", "numel", "step", "state", "out", "out_view", "submitted", "seg",
-                 "seg_ptr", "bound", "_small", "done_ev")
+                 "seg_ptr", "bound", "_small", "done_ev", "seg_group", "seg_out")
 
     def __init__(self, index: int, param: torch.Tensor, group: dict):
         self.index = index
@@ -67,6 +69,8 @@ class ParamSlot:
         self.bound: ParamState | None = None        # the state whose buffers seg points at
         self._small: weakref.ref | None = None
         self.done_ev: torch.cuda.Event | None = None   # recorded after the slot's latest update
+        self.seg_group: _hip.Group | None = None    # the group struct seg points at
+        self.seg_out: tuple | None = None           # (out, out_dtype, reserved) seg holds
 
     @property
     def initialized(self) -> bool:
@@ -168,6 +172,7 @@ class UpdateEngine:
             raise ValueError(f"master_precision must be one of {sorted(_hip.MASTER_CODES)}")
         self.kernels = _hip.load()
         self.algorithm = algorithm
+        self._algo_code = _hip.ALGORITHMS[algorithm]
         self.lion = algorithm == "lion"
         self.precision = precision
         self.master_precision = master_precision
@@ -345,25 +350,28 @@ class UpdateEngine:
         if slot.bound is not slot.state or slot.state.alternates:
             slot.state.bind(seg)
             slot.bound = slot.state
-        if grad.dtype is torch.bfloat16:
-            seg.g_dtype = _hip.DT_BF16
-        elif grad.dtype is torch.float32:
-            seg.g_dtype = _hip.DT_F32
-        else:
+        seg.offset = 0
+        seg.algorithm = self._algo_code
+        g_dtype = _GRAD_CODES.get(grad.dtype)
+        if g_dtype is None:
             raise TypeError(f"gradients must be float32 or bfloat16, got {grad.dtype}")
+        seg.g_dtype = g_dtype
         seg.g = grad.data_ptr()
         out, dtype, buffered = self._target(slot, hooked)
         if self.delay and slot.step == 1:
             # a delayed first update owes the parameter nothing: its weight is the one the master was
             # made from (which an FP24 master holds only rounded)
             out, dtype, buffered = None, None, False
-        seg.out = out
-        seg.out_dtype = _hip.DT_NONE if out is None else _hip.DT_F32 if dtype is torch.float32 else _hip.DT_BF16
-        seg.reserved = _hip.SEG_OUT_PREVIOUS if self.delay and out is not None else 0
+        # fields that rarely change are written only when they do (host time per step with ~300 slots)
+        want = (out, _hip.DT_NONE if out is None else _hip.DT_F32 if dtype is torch.float32 else _hip.DT_BF16,
+                _hip.SEG_OUT_PREVIOUS if self.delay and out is not None else 0)
+        if slot.seg_out != want:
+            seg.out, seg.out_dtype, seg.reserved = want
+            slot.seg_out = want
         seg.step = slot.step
-        seg.offset = 0
-        seg.algorithm = _hip.ALGORITHMS[self.algorithm]
-        seg.group = ctypes.pointer(group)
+        if slot.seg_group is not group:
+            seg.group = ctypes.pointer(group)
+            slot.seg_group = group
         return slot.seg_ptr, buffered
 
     # ------------------------------------------------------------ submission
