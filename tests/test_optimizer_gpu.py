@@ -1171,3 +1171,89 @@ def test_packed_state_checkpoint_and_set_precision(precision):
     for x, y in zip(masters, opt.master_params()):
         assert torch.equal(x, y)
     opt.close()
+
+
+# ------------------------------------------------------- randomized schedules
+
+def _schedule(seed, steps):
+    """A seeded sequence of (event, micro-batches): how each step is driven, and whether a checkpoint
+    reload into a new optimizer or a change of moment precision comes first."""
+    rng = np.random.default_rng(seed)
+    events = []
+    for _ in range(steps):
+        before = rng.choice(["none", "none", "reload", "precision"])
+        events.append((str(before), str(rng.choice(["step", "hooks"])), int(rng.integers(1, 4)),
+                       str(rng.choice(["fp32", "bf16", "fp8"]))))
+    return events
+
+
+@pytest.mark.parametrize("lion", [False, True])
+@pytest.mark.parametrize("master", ["fp32", "fp24"])
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_random_schedules_match_plain_steps(seed, master, lion):
+    """Any mix of plain steps, hooked steps, accumulation over no_sync() micro-batches, checkpoint
+    reloads (through torch.save/load) into a new optimizer, and moment precision changes gives the
+    same bytes -- weights, masters, moments -- as plain step() calls on the same gradients with the
+    same precision changes (reference optimizer.py:291-355, 453-463, 525-602)."""
+    cls = ab.LionBridge if lion else ab.AdamBridge
+    kw = dict(lr=2e-3, weight_decay=0.01, master_precision=master, small_param_threshold=2000)
+    if not lion:
+        kw["eps"] = 1e-8
+
+    def make(model, precision):
+        return cls(model.parameters(), precision=precision, **kw)
+
+    torch.manual_seed(seed)
+    ref_model = TinyLM(layers=2).to(DEV).to(torch.bfloat16)
+    model = copy.deepcopy(ref_model)
+    precision = "bf16"
+    ref, opt = make(ref_model, precision), make(model, precision)
+    hooked = False
+    g = torch.Generator().manual_seed(100 + seed)
+    for step, (before, mode, micros, target) in enumerate(_schedule(seed, 12)):
+        if before == "reload":
+            buf = io.BytesIO()
+            torch.save(opt.state_dict(), buf)
+            opt.close()
+            buf.seek(0)
+            opt = make(model, precision)
+            opt.load_state_dict(torch.load(buf, weights_only=True))
+            hooked = False
+        elif before == "precision" and target != precision:
+            precision = target
+            ref.set_precision(precision)
+            opt.set_precision(precision)
+            assert ref.precision == opt.precision == precision
+        grads = [[(torch.randn(p.shape, generator=g) * 0.05).to(device=DEV, dtype=torch.bfloat16)
+                  for p in ref_model.parameters()] for _ in range(micros)]
+        for gs in grads:
+            sum((p * x).sum() for p, x in zip(ref_model.parameters(), gs)).backward()
+        ref.step()
+        ref.zero_grad(set_to_none=True)
+        if mode == "hooks" and not hooked:
+            opt.attach_hooks(model)
+        elif mode == "step" and hooked:
+            opt.detach_hooks()
+        hooked = mode == "hooks"
+        for i, gs in enumerate(grads):
+            loss = sum((p * x).sum() for p, x in zip(model.parameters(), gs))
+            if hooked and i < micros - 1:
+                with opt.no_sync():
+                    loss.backward()
+            else:
+                loss.backward()
+        if hooked:
+            opt.step_sync()
+        else:
+            opt.step()
+            opt.zero_grad(set_to_none=True)
+        assert all(torch.equal(a, b) for a, b in zip(ref_model.parameters(), model.parameters())), \
+            f"weights differ after step {step} ({before}, {mode}, {micros} micro-batches, {precision})"
+    assert all(torch.equal(a, b) for a, b in zip(ref.master_params(), opt.master_params()))
+    for a, b in zip(ref._ordered, opt._ordered):
+        assert a.step == b.step
+        assert torch.equal(a.m.to_fp32(), b.m.to_fp32())
+        if not lion:
+            assert torch.equal(a.v.to_fp32(), b.v.to_fp32())
+    ref.close()
+    opt.close()
