@@ -23,11 +23,21 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "slow: long-running")
 
 
+DEFAULT_GPU_TIMEOUT = 600   # seconds per GPU test when no --timeout is given; the longest takes ~40 s
+
+
 def pytest_collection_modifyitems(config, items):
     skip = pytest.mark.skip(reason="no GPU in this environment")
+    # A GPU test that hangs inside a device call ends the run with its name and stack (pytest-timeout's
+    # thread method) instead of holding the GPU until an outer limit kills everything.
+    bound = (pytest.mark.timeout(DEFAULT_GPU_TIMEOUT, method="thread")
+             if GPU and config.pluginmanager.hasplugin("timeout") and not config.getoption("timeout", None)
+             else None)
     for item in items:
         if "gpu" in item.keywords and not GPU:
             item.add_marker(skip)
+        elif "gpu" in item.keywords and bound is not None and item.get_closest_marker("timeout") is None:
+            item.add_marker(bound)
 
 
 def tiny_mlp(seed=0, din=48, hidden=193, dout=5, dtype=torch.float32, device="cpu"):
