@@ -21,6 +21,7 @@ pairs           AdamW, FP32 master, BF16 moments       16 per 2 elements (x2 dou
 fp8-records     AdamW, FP32 master, FP8 moments        768 per 128 + two FP32 scales per 128
 lion-records    Lion, FP32 master, BF16 moment         1536 per 256 (x2 double-buffered)
 f32-records     AdamW, FP32 master, FP32 moments       3072 per 256 (x2 double-buffered)
+f24-records     AdamW, FP24 master, BF16 moments       1792 per 256 (x2 double-buffered)
 ==============  =====================================  ======================================
 
 The interleaved layouts turn the master and moment streams into one stream of
@@ -40,9 +41,9 @@ from . import formats as F
 from .precision import BF16Store, FP8Store, FP24Store, FP32Store, MomentStore, load_master_, make_master, make_store
 
 __all__ = ["ParamState", "SeparateState", "PairState", "AdamRecordState", "LionRecordState", "F32RecordState",
-           "choose_layout", "new_state", "new_states", "arena_plan", "arena_memory", "LAYOUTS"]
+           "F24RecordState", "choose_layout", "new_state", "new_states", "arena_plan", "arena_memory", "LAYOUTS"]
 
-LAYOUTS = ("separate", "pairs", "fp8-records", "lion-records", "f32-records")
+LAYOUTS = ("separate", "pairs", "fp8-records", "lion-records", "f32-records", "f24-records")
 
 # Arenas of at least this many bytes follow an allocate/free of their own size (new_states); None: never.
 RECYCLE_MIN_BYTES: int | None = 256 << 20
@@ -50,10 +51,12 @@ RECYCLE_MIN_BYTES: int | None = 256 << 20
 
 def choose_layout(algorithm: str, precision: str, master_precision: str, requested: str = "auto",
                   master_is_param: bool = False) -> str:
-    """The layout of a parameter's state: the interleaved one for its (algorithm, precision) when
-    there is one and the master is an FP32 buffer of the optimizer's own, else 'separate'."""
-    if requested == "separate" or master_is_param or master_precision != "fp32":
+    """The layout of a parameter's state: the interleaved one for its (algorithm, precision, master
+    precision) when there is one and the master is a buffer of the optimizer's own, else 'separate'."""
+    if requested == "separate" or master_is_param:
         return "separate"
+    if master_precision == "fp24":
+        return "f24-records" if (algorithm, precision) == ("adamw", "bf16") else "separate"
     return {("adamw", "bf16"): "pairs", ("adamw", "fp8"): "fp8-records", ("adamw", "fp32"): "f32-records",
             ("lion", "bf16"): "lion-records"}.get((algorithm, precision), "separate")
 
@@ -397,6 +400,74 @@ class F32RecordState(_Interleaved):
         return {r: self._column(r).reshape(-1)[lo:hi] for r in ("p", "m", "v")}
 
 
+class F24RecordState(_Interleaved):
+    """AdamW, FP24 master, BF16 moments: 1792-byte records of 256 elements, the 256 master high halves
+    (BF16 bits), the 256 master low bytes, the 256 m and the 256 v values (BF16), each in element
+    order (ADAMBRIDGE_DT_PACKED_F24)."""
+
+    layout = "f24-records"
+    precision = "bf16"
+    master_precision = "fp24"
+
+    def __init__(self, numel, device, double_buffer: bool = False, memory: list[torch.Tensor] | None = None):
+        records = max(1, -(-int(numel) // 256))
+        bufs = [m.view(records, 1792) for m in memory] if memory else \
+            [torch.zeros(records, 1792, dtype=torch.uint8, device=device) for _ in range(2 if double_buffer else 1)]
+        super().__init__(numel, device, ("m", "v"), bufs)
+
+    @staticmethod
+    def buffer_bytes(numel: int) -> int:
+        return max(1, -(-int(numel) // 256)) * 1792
+
+    def bind(self, seg):
+        seg.p, seg.p_lo = self.current.data_ptr(), _ptr(self.target)
+        seg.m = seg.v = seg.m_scale = seg.v_scale = None
+        seg.p_dtype, seg.mv_dtype = _hip.DT_PACKED_F24, _hip.DT_BF16
+
+    def _column(self, role):
+        """'p' the hi plane (BF16 bits), 'lo' the lo plane (uint8), 'm' / 'v' the moments (BF16)."""
+        if role == "lo":
+            return self.current[:, 512:768]
+        k = {"p": 0, "m": 768, "v": 1280}[role]
+        return self.current[:, k:k + 512].view(torch.bfloat16)
+
+    def _planes(self) -> FP24Store:
+        """The master as an FP24 store (a copy of the two planes)."""
+        store = FP24Store(self.numel, device=self.device)
+        store.hi.copy_(self._column("p").reshape(-1)[: self.numel])
+        store.lo.copy_(self._column("lo").reshape(-1)[: self.numel])
+        return store
+
+    def master_fp32(self):
+        return self._planes().to_fp32()
+
+    def export_master(self):
+        return self._planes().state_dict()
+
+    def moment(self, role):
+        store = BF16Store(self.numel, device=self.device)
+        store.data.copy_(self._column(role).reshape(-1)[: self.numel])
+        return store
+
+    def load(self, master=None, moments=None):
+        if master is not None:
+            planes = FP24Store(self.numel, device=self.device)
+            load_master_(planes, master)   # FP24 planes as they are; other values rounded to nearest
+            self._put("p", planes.hi)
+            self._put("lo", planes.lo)
+        for role, store in (moments or {}).items():
+            self._put(role, _bf16_bits(store, self.device))
+
+    def footprint(self):
+        total = sum(b.nbytes for b in self.buffers)
+        master = 3 * self.numel * len(self.buffers)
+        return master, total - master
+
+    def window(self, lo, hi):
+        return {"p": self._column("p").reshape(-1)[lo:hi], "p_lo": self._column("lo").reshape(-1)[lo:hi],
+                "m": self._column("m").reshape(-1)[lo:hi], "v": self._column("v").reshape(-1)[lo:hi]}
+
+
 class AdamRecordState(_Interleaved):
     """AdamW, FP32 master, FP8 moments: one 768-byte record per 128-element block
     (ADAMBRIDGE_DT_PACKED_FP8) -- lane l's elements 8l .. 8l + 7 keep their masters at 16l (first
@@ -471,7 +542,7 @@ def _bf16_bits(store: MomentStore, device) -> torch.Tensor:
 # -------------------------------------------------------------------- building
 
 _INTERLEAVED = {"pairs": PairState, "lion-records": LionRecordState, "fp8-records": AdamRecordState,
-                "f32-records": F32RecordState}
+                "f32-records": F32RecordState, "f24-records": F24RecordState}
 ARENA_ALIGN = 2 << 20
 SMALL_ALIGN = 256
 

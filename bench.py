@@ -97,11 +97,11 @@ CONFIGS = {
 }
 
 
-def min_bytes(precision: str, algo: str, grad_bytes: int = 2, out_bytes: int = 2) -> float:
+def min_bytes(precision: str, algo: str, grad_bytes: int = 2, out_bytes: int = 2, master: str = "fp32") -> float:
     """Minimum bytes per parameter: master read+write, gradient, moments read+write, output
-    (reference benchmarks/bench_kernels.py:63-65)."""
+    (reference benchmarks/bench_kernels.py:63-65; an FP24 master is 3 bytes)."""
     mv = {"fp32": 4, "bf16": 2, "fp8": 1 + 4 / 128}[precision]
-    return 4 * 2 + grad_bytes + mv * 2 * (1 if algo == "lion" else 2) + out_bytes
+    return (3 if master == "fp24" else 4) * 2 + grad_bytes + mv * 2 * (1 if algo == "lion" else 2) + out_bytes
 
 
 # ----------------------------------------------------------------- GPU side
@@ -121,7 +121,7 @@ def build(cfg: dict, device, seed: int = 0, layout: str = "auto", double_buffer:
     for k in reversed(range(len(shapes))):
         grads[k] = synthetic_grad(cfg, k, shapes[k], gen, device)
     kw = dict(lr=cfg["lr"], betas=cfg["betas"], weight_decay=cfg["wd"], precision=cfg["precision"],
-              state_layout=layout, double_buffer=double_buffer)
+              master_precision=cfg.get("master", "fp32"), state_layout=layout, double_buffer=double_buffer)
     opt = ab.LionBridge(params, **kw) if cfg["algo"] == "lion" else ab.AdamBridge(params, **kw)
     for p, g in zip(params, grads):
         p.grad = g
@@ -183,7 +183,7 @@ def gpu_bench(cfg: dict, steps: int, warmup: int, layout: str = "auto", double_b
             print(f"[bench] launches {k}..: " + " ".join(f"{d * 1e3:.2f}" for d in durs[k:k + 10]), file=sys.stderr,
                   flush=True)
     launches_per_step = len(log) / steps
-    bpp = min_bytes(cfg["precision"], cfg["algo"])
+    bpp = min_bytes(cfg["precision"], cfg["algo"], master=cfg.get("master", "fp32"))
     kernel_s = sum(durs) / len(durs)
     elems_per_launch = sum(e for _, _, e in log) / len(log)
     achieved = elems_per_launch * bpp / kernel_s / 1e9
@@ -444,8 +444,13 @@ def cpu_bench(cfg: dict, budget_params: int, steps: int) -> dict:
     lion = cfg["algo"] == "lion"
     group = O.Group(cfg["lr"], cfg["betas"][0], cfg["betas"][1], 0.0 if lion else 1e-8, cfg["wd"], 0, 1, 0)
     keep, segs = [], []
+    f24 = cfg.get("master", "fp32") == "fp24"
     for k, (name, numel) in enumerate(shapes):
         p = np.resize(pat_p, numel)
+        p_lo = None
+        if f24:   # hi plane (the bf16 bits) and lo plane of the same values
+            bits = p.view(np.uint32)
+            p, p_lo = (bits >> 16).astype(np.uint16), ((bits >> 8) & 0xFF).astype(np.uint8)
         g = np.resize(pat_g, numel)
         out = np.empty(numel, np.uint16)
         if mv_dt == O.DT_FP8:
@@ -455,14 +460,17 @@ def cpu_bench(cfg: dict, budget_params: int, steps: int) -> dict:
         else:
             dt = np.float32 if mv_dt == O.DT_F32 else np.uint16
             m, v, ms, vs = np.zeros(numel, dt), np.zeros(numel, dt), None, None
-        keep.append(dict(p=p, g=g, m=m, v=None if lion else v, m_scale=ms, v_scale=None if lion else vs, out=out))
-        segs.append(O.Segment(p=p.ctypes.data, g=g.ctypes.data, m=m.ctypes.data,
+        keep.append(dict(p=p, p_lo=p_lo, g=g, m=m, v=None if lion else v, m_scale=ms, v_scale=None if lion else vs,
+                         out=out))
+        segs.append(O.Segment(p=p.ctypes.data, p_lo=None if p_lo is None else p_lo.ctypes.data,
+                              g=g.ctypes.data, m=m.ctypes.data,
                               v=None if lion else v.ctypes.data, m_scale=None if ms is None else ms.ctypes.data,
                               v_scale=None if (lion or vs is None) else vs.ctypes.data, out=out.ctypes.data,
                               group=ctypes.pointer(group), n=numel, step=1, index=k, offset=0, g_dtype=O.DT_BF16,
-                              mv_dtype=mv_dt, out_dtype=O.DT_BF16, algorithm=1 if lion else 0, p_dtype=O.DT_F32))
+                              mv_dtype=mv_dt, out_dtype=O.DT_BF16, algorithm=1 if lion else 0,
+                              p_dtype=O.DT_F24 if f24 else O.DT_F32))
     arr = (ctypes.POINTER(O.Segment) * len(segs))(*[ctypes.pointer(s) for s in segs])
-    bpp = min_bytes(cfg["precision"], cfg["algo"])
+    bpp = min_bytes(cfg["precision"], cfg["algo"], master=cfg.get("master", "fp32"))
     level = None
     if use_ref:
         lib.adambridge_set_simd_level(-1)
@@ -524,6 +532,8 @@ def main() -> int:
     ap.add_argument("--layout", default="auto", choices=["auto", "packed", "separate"],
                     help="optimizer state layout in HBM (AdamBridge state_layout)")
     ap.add_argument("--double-buffer", action="store_true", help="AdamBridge double_buffer=True")
+    ap.add_argument("--master", default="fp32", choices=["fp32", "fp24"],
+                    help="master weight precision (AdamBridge master_precision); the configurations' own is fp32")
     ap.add_argument("--traffic", type=float, default=None,
                     help="HBM bytes per launch measured by rocprofv3 (FETCH_SIZE+WRITE_SIZE, scaled); "
                          "default: the figure measured for this configuration, when there is one")
@@ -546,7 +556,7 @@ def main() -> int:
         ap.error("--steps and --rebuilds must be >= 1 and --warmup >= 0")
     if args.config == "c5":
         return main_pipeline(args)
-    cfg = CONFIGS[args.config]
+    cfg = dict(CONFIGS[args.config], master=args.master)
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)
     print(f"[bench] config {args.config}: {cfg['desc']}; warmup {args.warmup}, steps {args.steps}",
@@ -586,9 +596,12 @@ def main() -> int:
               f"{cpu['all_cores']['ms_per_step']:.1f} ms/step on {cpu['all_cores']['threads']} ({cpu['host']})",
               file=sys.stderr, flush=True)
     ms_per_step = g["wall"] / args.steps * 1e3
+    # the traffic measured for each configuration, with its own (FP32) master
+    measured, profiled = (MEASURED_TRAFFIC, TRAFFIC_PROFILE) if args.master == "fp32" else ({}, {})
     line = {
-        "metric": METRIC if args.config == "c3p" else
-        f"params updated/sec and achieved HBM GB/s (% roofline), {cfg['desc']} ({args.config})",
+        "metric": METRIC if args.config == "c3p" and args.master == "fp32" else
+        f"params updated/sec and achieved HBM GB/s (% roofline), {cfg['desc']} ({args.config}"
+        f"{', FP24 master' if args.master == 'fp24' else ''})",
         "value": g["params"] * args.steps / g["wall"],
         "unit": "params/s",
         "n_gpus": 1,
@@ -603,14 +616,14 @@ def main() -> int:
                  f"{cfg['gscale']} and {cfg['zeros']:.0%} exact zeros)" if cfg.get("grads") == "elementwise" else
                  "synthetic (bf16 weights ~N(0,0.02), bf16 grads ~N(0,1) x log-uniform per-tensor scale)"),
         "config": {"workload": cfg["desc"], "config": args.config, "params": g["params"], "tensors": g["tensors"],
-                   "moments": cfg["precision"], "master": "fp32", "grad": "bf16", "out": "bf16",
+                   "moments": cfg["precision"], "master": cfg["master"], "grad": "bf16", "out": "bf16",
                    "bytes_per_param": g["bytes_per_param"], "launches_per_step": g["launches_per_step"],
                    "state_layout": g["layout"], "state_bytes": g["state_bytes"], "copies_rotated": g["copies"],
                    "wall_gbs": g["params"] * g["bytes_per_param"] / (ms_per_step / 1e3) / 1e9},
         "roofline": {"bound": "hbm", "achieved": g["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": g["achieved_gbs"] / HBM_PEAK_GBS,
-                     "traffic": args.traffic if args.traffic is not None else MEASURED_TRAFFIC.get(args.config),
-                     "traffic_source": "--traffic" if args.traffic is not None else TRAFFIC_PROFILE.get(args.config),
+                     "traffic": args.traffic if args.traffic is not None else measured.get(args.config),
+                     "traffic_source": "--traffic" if args.traffic is not None else profiled.get(args.config),
                      "kernel_ms": g["kernel_ms"]},
         "copy_ceiling": ceiling,
         "placement": placement,

@@ -39,7 +39,7 @@ extern "C" {
  * SIMD levels reproduced, kernels.c:74: 0 scalar, 1 AVX2 (8 lanes), 2 AVX-512 (16 lanes). */
 enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, ADAMBRIDGE_DT_FP8 = 3,
        ADAMBRIDGE_DT_F24 = 4, ADAMBRIDGE_DT_PACKED = 5, ADAMBRIDGE_DT_PACKED_FP8 = 6,
-       ADAMBRIDGE_DT_PACKED_LION = 7, ADAMBRIDGE_DT_PACKED_F32 = 8 };
+       ADAMBRIDGE_DT_PACKED_LION = 7, ADAMBRIDGE_DT_PACKED_F32 = 8, ADAMBRIDGE_DT_PACKED_F24 = 9 };
 
 /* ADAMBRIDGE_DT_PACKED (p_dtype; no counterpart in the reference): an HBM layout for
  * AdamW with an FP32 master and BF16 moments (mv_dtype DT_BF16).  p points at 16-byte
@@ -75,6 +75,15 @@ enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, AD
  * unchanged.  p_lo is NULL (update in place) or a second buffer of the same layout that receives
  * the new state; m, v and the scales are unused.  Same arithmetic (including the scalar tail's
  * unfused form) as the separate layout. */
+/* ADAMBRIDGE_DT_PACKED_F24 (p_dtype; no counterpart in the reference): an HBM layout for AdamW
+ * with an FP24 master and BF16 moments (mv_dtype DT_BF16).  p points at one 1792-byte record per
+ * 256 elements, ceil(n/256) records, 16-byte aligned.  The record of elements 256r .. 256r + 255
+ * holds their 256 master high halves (the FP24 hi plane, BF16 bits; bytes 0 .. 511), then their
+ * 256 master low bytes (the lo plane; 512 .. 767), then their 256 m values (768 .. 1279), then
+ * their 256 v values (1280 .. 1791), the moments as BF16 bits, everything in element order.
+ * Slots past n are padding, written back unchanged.  p_lo is NULL (update in place) or a second
+ * buffer of the same layout that receives the new state; m, v and the scales are unused.  Same
+ * arithmetic, rounding and rounding streams as the separate layout with an FP24 master. */
 enum { ADAMBRIDGE_ALGO_ADAMW = 0, ADAMBRIDGE_ALGO_LION = 1 };
 
 /* Error codes (kernels.c:1537-1553, 1582-1584, 1620-1621), plus the HIP-side ones. */
@@ -131,9 +140,10 @@ typedef struct adambridge_group {
 typedef struct adambridge_segment {
     void* p;                 /* FP32 master, the FP24 hi plane (uint16) when p_dtype is DT_F24, or the
                                 packed state when p_dtype is DT_PACKED / DT_PACKED_FP8 / DT_PACKED_LION /
-                                DT_PACKED_F32 */
+                                DT_PACKED_F32 / DT_PACKED_F24 */
     uint8_t* p_lo;           /* FP24 lo plane (one byte per element); NULL for FP32; DT_PACKED,
-                                DT_PACKED_LION and DT_PACKED_F32: the destination state (NULL: in place) */
+                                DT_PACKED_LION, DT_PACKED_F32 and DT_PACKED_F24: the destination state
+                                (NULL: in place) */
     const void* g;           /* gradient, g_dtype */
     void* m;                 /* first moment, mv_dtype (FP8: E4M3 codes, padded to 128 per block) */
     void* v;                 /* second moment (FP8: E5M2 codes of sqrt(v)); unused by Lion */
@@ -149,7 +159,8 @@ typedef struct adambridge_segment {
     int32_t mv_dtype;
     int32_t out_dtype;
     int32_t algorithm;
-    int32_t p_dtype;         /* DT_F32 (or 0), DT_F24, DT_PACKED, DT_PACKED_FP8, DT_PACKED_LION or DT_PACKED_F32 */
+    int32_t p_dtype;         /* DT_F32 (or 0), DT_F24, DT_PACKED, DT_PACKED_FP8, DT_PACKED_LION, DT_PACKED_F32
+                                or DT_PACKED_F24 */
     int32_t reserved;        /* 0, or ADAMBRIDGE_SEG_OUT_PREVIOUS */
 } adambridge_segment;
 

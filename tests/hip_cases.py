@@ -411,20 +411,63 @@ def unpack_f32_records(case: O.Case, rec: np.ndarray) -> list[np.ndarray]:
     return pads
 
 
+def pack_f24_records(case: O.Case) -> np.ndarray:
+    """Separate FP24 master planes, BF16 m and v -> ADAMBRIDGE_DT_PACKED_F24 records (records x 1792
+    bytes): per 256 elements, the 256 hi halves, the 256 lo bytes, the 256 m, the 256 v, each in
+    element order.  Padding slots hold fixed patterns so that a test can see the kernel leave them
+    unchanged."""
+    n = case.n
+    nr = max(1, -(-n // 256))
+    rec = np.zeros((nr, 1792), np.uint8)
+    for key, (a, b), dt, fill in (("p", (0, 512), np.uint16, 0x7FA5), ("p_lo", (512, 768), np.uint8, 0xA5),
+                                  ("m", (768, 1280), np.uint16, 0x7FA6), ("v", (1280, 1792), np.uint16, 0x7FA7)):
+        col = np.full(nr * 256, fill, dt)
+        col[:n] = case.arrays[key].view(dt)
+        rec[:, a:b] = col.reshape(nr, 256).view(np.uint8).reshape(nr, b - a)
+    return rec
+
+
+def unpack_f24_records(case: O.Case, rec: np.ndarray) -> list[np.ndarray]:
+    """ADAMBRIDGE_DT_PACKED_F24 records -> the case's separate planes, m and v (in place); returns
+    the padding slots past n of each."""
+    n = case.n
+    rec = np.ascontiguousarray(rec).reshape(-1, 1792)
+    pads = []
+    for key, (a, b), dt in (("p", (0, 512), np.uint16), ("p_lo", (512, 768), np.uint8),
+                            ("m", (768, 1280), np.uint16), ("v", (1280, 1792), np.uint16)):
+        col = np.ascontiguousarray(rec[:, a:b]).view(dt).reshape(-1)
+        case.arrays[key] = col[:n].view(case.arrays[key].dtype).copy()
+        pads.append(col[n:].copy())
+    return pads
+
+
+# record kind -> (p_dtype code, moment dtype, master dtype, pack, unpack)
+_RECORDS = {"f32": (_hip.DT_PACKED_F32, O.DT_F32, O.DT_F32, pack_f32_records, unpack_f32_records),
+            "f24": (_hip.DT_PACKED_F24, O.DT_BF16, O.DT_F24, pack_f24_records, unpack_f24_records)}
+
+
+def run_hip_f24_records(cases: list[O.Case], width: int = 16, **kw) -> list[O.Case]:
+    """run_hip through ADAMBRIDGE_DT_PACKED_F24 records (AdamW, FP24 master, BF16 moments)."""
+    return run_hip_f32_records(cases, width, kind="f24", **kw)
+
+
 def run_hip_f32_records(cases: list[O.Case], width: int = 16, double_buffer: bool = False,
-                        misalign_g: int = 0, padding: list | None = None, seg_flags: int = 0) -> list[O.Case]:
-    """Like run_hip for AdamW / FP32 master / FP32 moment cases, through the record layout
-    (ADAMBRIDGE_DT_PACKED_F32): pack on the host, one call, unpack the result.  ``misalign_g``
-    elements shift the gradient off its allocation's alignment; ``padding`` receives each case's
-    padding slots after the call."""
+                        misalign_g: int = 0, padding: list | None = None, seg_flags: int = 0,
+                        kind: str = "f32") -> list[O.Case]:
+    """Like run_hip for AdamW cases through a record layout: FP32 master and FP32 moments
+    (ADAMBRIDGE_DT_PACKED_F32, ``kind`` 'f32'), or FP24 master and BF16 moments
+    (ADAMBRIDGE_DT_PACKED_F24, 'f24'): pack on the host, one call, unpack the result.
+    ``misalign_g`` elements shift the gradient off its allocation's alignment; ``padding`` receives
+    each case's padding slots after the call."""
+    p_code, mv_dt, pt, pack, unpack = _RECORDS[kind]
     kernels = _hip.load()
     work = [c.copy() for c in cases]
     entries, segs = [], []
     by_group = all(c.group is not None for c in work)
     for c in work:
-        assert c.algorithm == O.ADAMW and c.mv_dtype == O.DT_F32 and c.p_dtype == O.DT_F32
+        assert c.algorithm == O.ADAMW and c.mv_dtype == mv_dt and c.p_dtype == pt
         O.check_sizes(c)
-        rec = torch.from_numpy(pack_f32_records(c)).cuda()
+        rec = torch.from_numpy(pack(c)).cuda()
         dst = torch.full_like(rec, 0x5A) if double_buffer else None
         g = to_device(c.arrays["g"])
         keep = []
@@ -442,8 +485,8 @@ def run_hip_f32_records(cases: list[O.Case], width: int = 16, double_buffer: boo
         segs.append(_hip.Segment(p=rec.data_ptr(), p_lo=dst.data_ptr() if dst is not None else None,
                                  g=g.data_ptr(), m=None, v=None, out=out.data_ptr() if out is not None else None,
                                  group=ctypes.pointer(grp) if grp is not None else None, n=c.n, step=c.step,
-                                 index=c.index, offset=c.offset, g_dtype=c.g_dtype, mv_dtype=O.DT_F32,
-                                 out_dtype=c.out_dtype, algorithm=O.ADAMW, p_dtype=_hip.DT_PACKED_F32,
+                                 index=c.index, offset=c.offset, g_dtype=c.g_dtype, mv_dtype=mv_dt,
+                                 out_dtype=c.out_dtype, algorithm=O.ADAMW, p_dtype=p_code,
                                  reserved=seg_flags))
     arr = kernels.segment_array([ctypes.pointer(s) for s in segs])
     kernels.set_simd_level(WIDTH_LEVEL[width])
@@ -458,7 +501,7 @@ def run_hip_f32_records(cases: list[O.Case], width: int = 16, double_buffer: boo
     finally:
         kernels.set_simd_level(None)
     for c, (rec, dst, g, out, grp, keep) in zip(work, entries):
-        pad = unpack_f32_records(c, (dst if dst is not None else rec).cpu().numpy())
+        pad = unpack(c, (dst if dst is not None else rec).cpu().numpy())
         if padding is not None:
             padding.append(pad)
         if out is not None:

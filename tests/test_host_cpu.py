@@ -331,6 +331,43 @@ def test_f32_record_layout_offsets(n):
     assert st.target is st.buffers[0] and st.current.data_ptr() == st.buffers[1].data_ptr()
 
 
+@pytest.mark.parametrize("n", [1, 255, 256, 257, 1000])
+def test_f24_record_layout_offsets(n):
+    """F24RecordState: element 256r + i (i < 256) keeps its master's hi half at byte 2i of record r,
+    its lo byte at 512 + i, its m at 768 + 2i and its v at 1280 + 2i (ADAMBRIDGE_DT_PACKED_F24); the
+    master loads rounded to FP24 as the separate store rounds it, reads back through master_fp32,
+    the checkpoint planes and windows, and double buffering alternates the buffers."""
+    from adambridge_amd.state import F24RecordState
+    rng = np.random.default_rng(n + 21)
+    master = torch.from_numpy(rng.normal(0, 1, n).astype(np.float32))
+    moments = {r: P.BF16Store(n, init=torch.from_numpy(rng.normal(0, 1, n).astype(np.float32))) for r in ("m", "v")}
+    st = F24RecordState(n, "cpu", double_buffer=True)
+    assert F24RecordState.buffer_bytes(n) == -(-n // 256) * 1792 == st.current.nbytes
+    st.load(master=master, moments=moments)
+    ref = P.make_master("fp24", n, init=master)
+    hi, lo = ref.hi.view(torch.int16).numpy().view(np.uint16), ref.lo.numpy()
+    rec = st.current.numpy()
+    for e in range(n):
+        r, i = divmod(e, 256)
+        assert rec[r, 2 * i:2 * i + 2].view(np.uint16)[0] == hi[e] and rec[r, 512 + i] == lo[e]
+        for base, role in ((768, "m"), (1280, "v")):
+            assert rec[r, base + 2 * i:base + 2 * i + 2].view(np.uint16)[0] == \
+                moments[role].data.view(torch.int16).numpy().view(np.uint16)[e]
+    assert torch.equal(st.master_fp32(), ref.to_fp32())
+    saved = st.export_master()
+    assert saved["precision"] == "fp24" and torch.equal(saved["hi"], ref.hi) and torch.equal(saved["lo"], ref.lo)
+    for role in ("m", "v"):
+        assert torch.equal(st.moment(role).data, moments[role].data)
+    w = st.window(n // 3, n)
+    assert torch.equal(w["p_lo"], ref.lo[n // 3:]) and torch.equal(w["v"], moments["v"].data[n // 3:])
+    other = F24RecordState(n, "cpu")
+    other.load(master=saved)   # FP24 planes are taken as they are
+    assert torch.equal(other.master_fp32(), ref.to_fp32())
+    assert st.footprint() == (3 * n * 2, 2 * st.current.nbytes - 3 * n * 2)
+    st.advance()
+    assert st.target is st.buffers[0] and st.current.data_ptr() == st.buffers[1].data_ptr()
+
+
 def test_fp24_master_store_round_trip():
     n = 1000
     x = torch.randn(n) * 3
@@ -609,19 +646,22 @@ def test_command_line_info_reports_the_library():
 
 def test_layout_choice_for_every_algorithm_precision_and_master():
     """Each (algorithm, moment precision) with an FP32 master of the optimizer's own gets its
-    interleaved layout; an FP24 master, an FP32 parameter updated in place, Lion without a record
-    layout for its precision, and state_layout='separate' keep the reference's arrays."""
+    interleaved layout, and AdamW with BF16 moments and an FP24 master its FP24 records; other FP24
+    combinations, an FP32 parameter updated in place, Lion without a record layout for its
+    precision, and state_layout='separate' keep the reference's arrays."""
     from adambridge_amd.state import choose_layout
     want = {("adamw", "bf16"): "pairs", ("adamw", "fp8"): "fp8-records", ("adamw", "fp32"): "f32-records",
             ("lion", "bf16"): "lion-records", ("lion", "fp8"): "separate", ("lion", "fp32"): "separate"}
     for (algo, prec), layout in want.items():
         assert choose_layout(algo, prec, "fp32") == layout, (algo, prec)
-        assert choose_layout(algo, prec, "fp24") == "separate"
+        assert choose_layout(algo, prec, "fp24") == ("f24-records" if (algo, prec) == ("adamw", "bf16")
+                                                     else "separate")
+        assert choose_layout(algo, prec, "fp24", requested="separate") == "separate"
         assert choose_layout(algo, prec, "fp32", master_is_param=True) == "separate"
         assert choose_layout(algo, prec, "fp32", requested="separate") == "separate"
 
 
-@pytest.mark.parametrize("layout", ["pairs", "fp8-records", "lion-records", "f32-records"])
+@pytest.mark.parametrize("layout", ["pairs", "fp8-records", "lion-records", "f32-records", "f24-records"])
 def test_arena_plan_aligns_large_buffers_and_packs_small_ones(layout):
     """Buffers of 2 MiB or more start on 2 MiB boundaries, smaller ones on 256-byte boundaries (16-byte
     state access needs 16); no two buffers overlap, and many small tensors take little more than

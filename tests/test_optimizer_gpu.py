@@ -1049,17 +1049,19 @@ def test_multi_tensor_launch_count():
     opt.close()
 
 
-@pytest.mark.parametrize("precision", ["bf16", "fp8", "fp32"])
+@pytest.mark.parametrize("precision", ["bf16", "fp8", "fp32", "bf16-fp24"])
 @pytest.mark.parametrize("hooks", [False, True])
 def test_state_layouts_give_identical_bytes(hooks, precision):
-    """The interleaved layouts (default: BF16 pairs, FP8 block records, FP32 records), the separate
-    layout and the double-buffered interleaved layout produce the same weights, masters and moments
-    (FP8: codes and scales), step after step."""
+    """The interleaved layouts (default: BF16 pairs, FP8 block records, FP32 records, FP24-master
+    records), the separate layout and the double-buffered interleaved layout produce the same
+    weights, masters and moments (FP8: codes and scales), step after step."""
+    precision, _, master = precision.partition("-")
     results = []
     for kw in (dict(state_layout="separate"), dict(), dict(double_buffer=True)):
         torch.manual_seed(0)
         model = TinyLM().to(DEV).to(torch.bfloat16)
-        opt = ab.AdamBridge(model.parameters(), lr=3e-3, precision=precision, small_param_threshold=2000, **kw)
+        opt = ab.AdamBridge(model.parameters(), lr=3e-3, precision=precision, small_param_threshold=2000,
+                            master_precision=master or "fp32", **kw)
         if hooks:
             opt.attach_hooks(model)
         assert any(s.initialized and s.state.layout != "separate" for s in opt._ordered) or "state_layout" in kw or not opt._ordered[0].initialized
@@ -1084,15 +1086,17 @@ def test_state_layouts_give_identical_bytes(hooks, precision):
 
 
 @pytest.mark.parametrize("algo,precision", [("adamw", "bf16"), ("adamw", "fp8"), ("lion", "bf16"),
-                                            ("adamw", "fp32")])
+                                            ("adamw", "fp32"), ("adamw", "bf16-fp24")])
 def test_interleaved_checkpoint_gathered_on_host_when_the_device_is_short(algo, precision):
-    """Interleaved states (BF16 pairs, FP8 records, Lion records, FP32 records) are gathered into the reference's
-    checkpoint arrays on the device when it has room, else into host memory parameter by parameter;
-    either checkpoint loads into a fresh optimizer with identical masters and moments."""
+    """Interleaved states (BF16 pairs, FP8 records, Lion records, FP32 records, FP24-master records)
+    are gathered into the reference's checkpoint arrays on the device when it has room, else into
+    host memory parameter by parameter; either checkpoint loads into a fresh optimizer with
+    identical masters and moments."""
+    precision, _, master = precision.partition("-")
     torch.manual_seed(0)
     model = TinyLM().to(DEV).to(torch.bfloat16)
     cls = ab.LionBridge if algo == "lion" else ab.AdamBridge
-    opt = cls(model.parameters(), lr=3e-3, precision=precision)
+    opt = cls(model.parameters(), lr=3e-3, precision=precision, master_precision=master or "fp32")
     for step in range(3):
         lm_loss(model, step).backward()
         opt.step()
@@ -1116,7 +1120,8 @@ def test_interleaved_checkpoint_gathered_on_host_when_the_device_is_short(algo, 
     masters = opt.master_params()
     moments = [(s.m.to_fp32(), None if s.v is None else s.v.to_fp32()) for s in opt._ordered]
     for sd in (on_device, saved):
-        other = cls(TinyLM().to(DEV).to(torch.bfloat16).parameters(), lr=3e-3, precision=precision)
+        other = cls(TinyLM().to(DEV).to(torch.bfloat16).parameters(), lr=3e-3, precision=precision,
+                    master_precision=master or "fp32")
         other.load_state_dict(sd)
         assert all(torch.equal(x, y) for x, y in zip(masters, other.master_params()))
         for (m, v), s in zip(moments, other._ordered):
