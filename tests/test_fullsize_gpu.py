@@ -167,10 +167,11 @@ def _host(t: torch.Tensor) -> np.ndarray:
 CHUNK = 1 << 28   # elements per oracle call
 
 
-@pytest.mark.parametrize("name", ["c1", "c2", "c4", "c3p", "c3"])
+@pytest.mark.parametrize("name", ["c1", "c2", "c4", "c3p", "c3", "c3p-fp24"])
 def test_full_size_every_element(name):
     """One step after the configuration's warm-up steps, every element of every tensor against the
-    oracle: master (and its low plane), moments, FP8 block scales and the bf16 working weight."""
+    oracle: master (and its low plane), moments, FP8 block scales and the bf16 working weight.
+    'c3p-fp24': the 7B list with an FP24 master (FP24-master records)."""
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     base = torch.cuda.memory_allocated(dev)
@@ -179,13 +180,16 @@ def test_full_size_every_element(name):
 
 
 def _every_element(name: str) -> None:
-    cfg = bench.CONFIGS[name]
+    config, _, master = name.partition("-")
+    cfg = dict(bench.CONFIGS[config], master=master or "fp32")
     dev = torch.device("cuda", 0)
     opt, params = bench.build(cfg, dev)
     try:
         for _ in range(cfg.get("warm_steps", 2)):
             opt.step()
         torch.cuda.synchronize()
+        if master == "fp24":
+            assert all(s.state.layout == "f24-records" for s in opt._ordered)
         before = {s.index: {k: v.clone() for k, v in s.state.window(0, s.numel).items()} for s in opt._ordered}
         opt.step()
         torch.cuda.synchronize()
