@@ -422,12 +422,13 @@ class UpdateEngine:
                     ptrs.append(ptr)
                     if into_out:
                         buffered.append(slot)
+                arr = self.kernels.segment_array(ptrs)
+                self.kernels.set_stream(lanes.side)
                 timed = self.timing or self.launch_log is not None
                 start = torch.cuda.Event(enable_timing=True) if timed else None
-                if start is not None:
+                if start is not None:   # right before the launch: the pair brackets the library call only
                     start.record(lanes.side)
-                self.kernels.set_stream(lanes.side)
-                self.kernels.multi_step(None, self.kernels.segment_array(ptrs))
+                self.kernels.multi_step(None, arr)
             except BaseException:
                 for slot in slots:   # nothing was enqueued: the library validates and plans before launching
                     slot.step -= 1

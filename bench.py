@@ -31,6 +31,7 @@ bf16 moment.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -169,12 +170,20 @@ def gpu_bench(cfg: dict, steps: int, warmup: int, layout: str = "auto", double_b
     log: list = []
     for opt in opts:
         opt._engine.launch_log = log
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for k in range(steps):
-        opts[k % len(opts)].step()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    # No garbage collection inside the timed region (as timeit does): a collection pauses the host
+    # for tens of milliseconds, and where a launch is shorter than the host's lead (the 0.5B list:
+    # 1.6 ms) the device then idles -- between a launch's start event and the launch, inflating it.
+    gc.collect()
+    gc.disable()
+    try:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for k in range(steps):
+            opts[k % len(opts)].step()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    finally:
+        gc.enable()
     for opt in opts:
         opt._engine.launch_log = None
     durs = [a.elapsed_time(b) / 1e3 for a, b, _ in log]
