@@ -20,13 +20,13 @@ from pathlib import Path
 import torch
 
 __all__ = ["HipKernels", "HParams", "Group", "Segment", "load", "LIB_PATH", "DT_NONE", "DT_F32", "DT_BF16",
-           "DT_FP8", "DT_F24", "DT_PACKED", "DT_PACKED8", "DT_PACKED_LION", "DT_PACKED_F32", "DT_PACKED_F24", "SEG_OUT_PREVIOUS", "MOMENT_CODES", "MASTER_CODES",
+           "DT_FP8", "DT_F24", "DT_PACKED", "DT_PACKED8", "DT_PACKED_LION", "DT_PACKED_F32", "DT_PACKED_F24", "DT_PACKED_LION_F24", "SEG_OUT_PREVIOUS", "MOMENT_CODES", "MASTER_CODES",
            "ALGORITHMS", "SIMD_NAMES"]
 
 LIB_PATH = Path(__file__).resolve().with_name("libadambridge_hip.so")
 ABI_VERSION = 5
 
-DT_NONE, DT_F32, DT_BF16, DT_FP8, DT_F24, DT_PACKED, DT_PACKED8, DT_PACKED_LION, DT_PACKED_F32, DT_PACKED_F24 = range(10)
+DT_NONE, DT_F32, DT_BF16, DT_FP8, DT_F24, DT_PACKED, DT_PACKED8, DT_PACKED_LION, DT_PACKED_F32, DT_PACKED_F24, DT_PACKED_LION_F24 = range(11)
 SEG_OUT_PREVIOUS = 1   # Segment.reserved: out receives the weight of the master before the update
 _DTYPE_CODES = {torch.float32: DT_F32, torch.bfloat16: DT_BF16}
 MOMENT_CODES = {"fp32": DT_F32, "bf16": DT_BF16, "fp8": DT_FP8}

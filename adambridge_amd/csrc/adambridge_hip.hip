@@ -1182,6 +1182,75 @@ __global__ __launch_bounds__(kThreads) void k_update_f24rec(Launch L)
     else update_tile_f24rec<GT, OT, false>(s, tile, L.tile);
 }
 
+// Lion with an FP24 master and a BF16 moment in one 1280-byte record per 256 elements: the
+// record's 256 master high halves, its 256 low bytes and its 256 m values, each in element order.
+// The Lion-record kernel's lanes and arithmetic, with the FP24-master records' master access.
+constexpr int64_t kLionF24RecordBytes = 1280;
+
+template <int GT, int OT, bool SR>
+__device__ __forceinline__ void update_tile_lion_f24rec(const DevSeg& s, int64_t tile, int64_t T)
+{
+    const int64_t n = s.n;
+    const Coef c = s.c;
+    const uint8_t* __restrict__ src = static_cast<const uint8_t*>(s.p);
+    uint8_t* __restrict__ dst = s.p_lo;
+    const bool vec = (s.flags & kVec) != 0;   // g and out allow 2-element access
+    const bool prev = (s.flags & kPrev) != 0;  // uniform: out from the master as loaded
+    const int64_t lo = (tile - s.tile_begin) * T;
+    const int64_t hi = lo + T < n ? lo + T : n;
+    for (int64_t i = lo + threadIdx.x * 4; i < hi; i += kThreads * 4) {
+        // i % 4 == 0: record i / 256; high halves at 2j, low bytes at 512 + j, m at 768 + 2j
+        const int64_t rec = (i / kF24RecordElems) * kLionF24RecordBytes;
+        const int64_t j = i % kF24RecordElems;
+        const int64_t at_h = rec + 2 * j, at_l = rec + 512 + j, at_m = rec + 768 + 2 * j;
+        const uint32_t idx = s.idx0 + (uint32_t)i;
+        const u32x2 hw = ld(reinterpret_cast<const u32x2*>(src + at_h));
+        const uint32_t lw = ld(reinterpret_cast<const uint32_t*>(src + at_l));
+        const u32x2 mw = ld(reinterpret_cast<const u32x2*>(src + at_m));
+        const bool all = i + 4 <= n;
+        float g[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (vec && all) {
+            load2<GT>(s.g, i, g[0], g[1]);
+            load2<GT>(s.g, i + 2, g[2], g[3]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (i + k < n) g[k] = load1<GT>(s.g, i + k);
+        }
+        const uint32_t h_in[4] = {hw.x & 0xffffu, hw.x >> 16, hw.y & 0xffffu, hw.y >> 16};
+        const uint32_t m_in[4] = {mw.x & 0xffffu, mw.x >> 16, mw.y & 0xffffu, mw.y >> 16};
+        uint32_t p_in[4];   // the stored masters as FP32 bits: hi << 16 | lo << 8
+#pragma unroll
+        for (int k = 0; k < 4; ++k) p_in[k] = (h_in[k] << 16) | (((lw >> (8 * k)) & 0xffu) << 8);
+        if (prev) store_quad_out<OT>(s.out, i, n, vec && all, p_in);
+        uint32_t p_out[4], m_out[4], l_out = 0u;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float m = bitsf(m_in[k] << 16);
+            const float p = lion(bitsf(p_in[k]), g[k], m, c);
+            const bool in = all || i + k < n;   // padding keeps its bits
+            p_out[k] = in ? f24_round<SR>(p, SR ? hash32((idx + k) ^ s.seed_p) : 0u) : p_in[k];
+            m_out[k] = in ? bf16_store<SR>(m, SR ? hash32((idx + k) ^ s.seed_m) : 0u) : m_in[k];
+            l_out |= ((p_out[k] >> 8) & 0xffu) << (8 * k);
+        }
+        st(reinterpret_cast<u32x2*>(dst + at_h),
+           u32x2{(p_out[0] >> 16) | (p_out[1] & 0xffff0000u), (p_out[2] >> 16) | (p_out[3] & 0xffff0000u)});
+        st(reinterpret_cast<uint32_t*>(dst + at_l), l_out);
+        st(reinterpret_cast<u32x2*>(dst + at_m), u32x2{m_out[0] | (m_out[1] << 16), m_out[2] | (m_out[3] << 16)});
+        if (!prev) store_quad_out<OT>(s.out, i, n, vec && all, p_out);
+    }
+}
+
+template <int GT, int OT>
+__global__ __launch_bounds__(kThreads) void k_update_lion_f24rec(Launch L)
+{
+    const int64_t tile = block_tile(L);
+    if (tile >= L.ntiles) return;
+    const DevSeg s = find_segment(L, tile);
+    if (s.flags & kSR) update_tile_lion_f24rec<GT, OT, true>(s, tile, L.tile);
+    else update_tile_lion_f24rec<GT, OT, false>(s, tile, L.tile);
+}
+
 // ------------------------------------------------------- segment-table writer
 //
 // The allocation-free entry point keeps its segment tables in a device array
@@ -1341,6 +1410,22 @@ constexpr auto make_f24rec_table(std::integer_sequence<int, I...>)
 
 static const auto kF24Rec = make_f24rec_table(std::make_integer_sequence<int, kNumPacked>{});
 
+// Lion FP24-master record kernels follow: index kNumKernels + 5 * kNumPacked + gt * 3 + ot.
+template <int I>
+constexpr KernelFn lion_f24rec_entry()
+{
+    constexpr int ot = I % 3, gt = I / 3;
+    return &k_update_lion_f24rec<gt ? DT_BF16 : DT_F32, ot == 0 ? DT_NONE : ot == 1 ? DT_F32 : DT_BF16>;
+}
+
+template <int... I>
+constexpr auto make_lion_f24rec_table(std::integer_sequence<int, I...>)
+{
+    return std::array<KernelFn, sizeof...(I)>{lion_f24rec_entry<I>()...};
+}
+
+static const auto kLionF24Rec = make_lion_f24rec_table(std::make_integer_sequence<int, kNumPacked>{});
+
 // Kernel family of a table index: the FP8 block kernel, or a two-element-per-lane kernel.
 inline bool kernel_is_fp8(int index)
 {
@@ -1355,7 +1440,8 @@ inline KernelFn kernel_at(int index)
     if (index < kNumKernels + 2 * kNumPacked) return kPacked8[index - kNumKernels - kNumPacked];
     if (index < kNumKernels + 3 * kNumPacked) return kLionRec[index - kNumKernels - 2 * kNumPacked];
     if (index < kNumKernels + 4 * kNumPacked) return kF32Rec[index - kNumKernels - 3 * kNumPacked];
-    return kF24Rec[index - kNumKernels - 4 * kNumPacked];
+    if (index < kNumKernels + 5 * kNumPacked) return kF24Rec[index - kNumKernels - 4 * kNumPacked];
+    return kLionF24Rec[index - kNumKernels - 5 * kNumPacked];
 }
 
 inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
@@ -1370,6 +1456,8 @@ inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
         return kNumKernels + 3 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
     if (pt == DT_PACKED_F24)
         return kNumKernels + 4 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
+    if (pt == DT_PACKED_LION_F24)
+        return kNumKernels + 5 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
     const int mvi = mv == DT_F32 ? 0 : mv == DT_BF16 ? 1 : 2;
     const int pti = pt == DT_F24 ? 1 : 0;
     const int gti = gt == DT_BF16 ? 1 : 0;

@@ -22,6 +22,7 @@ fp8-records     AdamW, FP32 master, FP8 moments        768 per 128 + two FP32 sc
 lion-records    Lion, FP32 master, BF16 moment         1536 per 256 (x2 double-buffered)
 f32-records     AdamW, FP32 master, FP32 moments       3072 per 256 (x2 double-buffered)
 f24-records     AdamW, FP24 master, BF16 moments       1792 per 256 (x2 double-buffered)
+lion-f24-rec.   Lion, FP24 master, BF16 moment         1280 per 256 (x2 double-buffered)
 ==============  =====================================  ======================================
 
 The interleaved layouts turn the master and moment streams into one stream of
@@ -41,9 +42,9 @@ from . import formats as F
 from .precision import BF16Store, FP8Store, FP24Store, FP32Store, MomentStore, load_master_, make_master, make_store
 
 __all__ = ["ParamState", "SeparateState", "PairState", "AdamRecordState", "LionRecordState", "F32RecordState",
-           "F24RecordState", "choose_layout", "new_state", "new_states", "arena_plan", "arena_memory", "LAYOUTS"]
+           "F24RecordState", "LionF24RecordState", "choose_layout", "new_state", "new_states", "arena_plan", "arena_memory", "LAYOUTS"]
 
-LAYOUTS = ("separate", "pairs", "fp8-records", "lion-records", "f32-records", "f24-records")
+LAYOUTS = ("separate", "pairs", "fp8-records", "lion-records", "f32-records", "f24-records", "lion-f24-records")
 
 # Arenas of at least this many bytes follow an allocate/free of their own size (new_states); None: never.
 RECYCLE_MIN_BYTES: int | None = 256 << 20
@@ -56,7 +57,8 @@ def choose_layout(algorithm: str, precision: str, master_precision: str, request
     if requested == "separate" or master_is_param:
         return "separate"
     if master_precision == "fp24":
-        return "f24-records" if (algorithm, precision) == ("adamw", "bf16") else "separate"
+        return {("adamw", "bf16"): "f24-records", ("lion", "bf16"): "lion-f24-records"}.get((algorithm, precision),
+                                                                                          "separate")
     return {("adamw", "bf16"): "pairs", ("adamw", "fp8"): "fp8-records", ("adamw", "fp32"): "f32-records",
             ("lion", "bf16"): "lion-records"}.get((algorithm, precision), "separate")
 
@@ -468,6 +470,33 @@ class F24RecordState(_Interleaved):
                 "m": self._column("m").reshape(-1)[lo:hi], "v": self._column("v").reshape(-1)[lo:hi]}
 
 
+class LionF24RecordState(F24RecordState):
+    """Lion, FP24 master, BF16 moment: 1280-byte records of 256 elements, the 256 master high halves,
+    the 256 low bytes and the 256 m values, each in element order (ADAMBRIDGE_DT_PACKED_LION_F24)."""
+
+    layout = "lion-f24-records"
+    RECORD = 1280
+
+    def __init__(self, numel, device, double_buffer: bool = False, memory: list[torch.Tensor] | None = None):
+        records = max(1, -(-int(numel) // 256))
+        bufs = [m.view(records, self.RECORD) for m in memory] if memory else \
+            [torch.zeros(records, self.RECORD, dtype=torch.uint8, device=device) for _ in range(2 if double_buffer else 1)]
+        _Interleaved.__init__(self, numel, device, ("m",), bufs)
+
+    @staticmethod
+    def buffer_bytes(numel: int) -> int:
+        return max(1, -(-int(numel) // 256)) * LionF24RecordState.RECORD
+
+    def bind(self, seg):
+        super().bind(seg)
+        seg.p_dtype = _hip.DT_PACKED_LION_F24
+
+    def window(self, lo, hi):
+        w = super().window(lo, hi)
+        del w["v"]
+        return w
+
+
 class AdamRecordState(_Interleaved):
     """AdamW, FP32 master, FP8 moments: one 768-byte record per 128-element block
     (ADAMBRIDGE_DT_PACKED_FP8) -- lane l's elements 8l .. 8l + 7 keep their masters at 16l (first
@@ -542,7 +571,7 @@ def _bf16_bits(store: MomentStore, device) -> torch.Tensor:
 # -------------------------------------------------------------------- building
 
 _INTERLEAVED = {"pairs": PairState, "lion-records": LionRecordState, "fp8-records": AdamRecordState,
-                "f32-records": F32RecordState, "f24-records": F24RecordState}
+                "f32-records": F32RecordState, "f24-records": F24RecordState, "lion-f24-records": LionF24RecordState}
 ARENA_ALIGN = 2 << 20
 SMALL_ALIGN = 256
 

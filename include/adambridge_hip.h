@@ -39,7 +39,8 @@ extern "C" {
  * SIMD levels reproduced, kernels.c:74: 0 scalar, 1 AVX2 (8 lanes), 2 AVX-512 (16 lanes). */
 enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, ADAMBRIDGE_DT_FP8 = 3,
        ADAMBRIDGE_DT_F24 = 4, ADAMBRIDGE_DT_PACKED = 5, ADAMBRIDGE_DT_PACKED_FP8 = 6,
-       ADAMBRIDGE_DT_PACKED_LION = 7, ADAMBRIDGE_DT_PACKED_F32 = 8, ADAMBRIDGE_DT_PACKED_F24 = 9 };
+       ADAMBRIDGE_DT_PACKED_LION = 7, ADAMBRIDGE_DT_PACKED_F32 = 8, ADAMBRIDGE_DT_PACKED_F24 = 9,
+       ADAMBRIDGE_DT_PACKED_LION_F24 = 10 };
 
 /* ADAMBRIDGE_DT_PACKED (p_dtype; no counterpart in the reference): an HBM layout for
  * AdamW with an FP32 master and BF16 moments (mv_dtype DT_BF16).  p points at 16-byte
@@ -84,6 +85,9 @@ enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, AD
  * Slots past n are padding, written back unchanged.  p_lo is NULL (update in place) or a second
  * buffer of the same layout that receives the new state; m, v and the scales are unused.  Same
  * arithmetic, rounding and rounding streams as the separate layout with an FP24 master. */
+/* ADAMBRIDGE_DT_PACKED_LION_F24 (p_dtype; no counterpart in the reference): the same for Lion with an
+ * FP24 master and a BF16 moment: one 1280-byte record per 256 elements, the 256 master high halves
+ * (bytes 0 .. 511), the 256 low bytes (512 .. 767) and the 256 m values (768 .. 1279). */
 enum { ADAMBRIDGE_ALGO_ADAMW = 0, ADAMBRIDGE_ALGO_LION = 1 };
 
 /* Error codes (kernels.c:1537-1553, 1582-1584, 1620-1621), plus the HIP-side ones. */
@@ -140,9 +144,10 @@ typedef struct adambridge_group {
 typedef struct adambridge_segment {
     void* p;                 /* FP32 master, the FP24 hi plane (uint16) when p_dtype is DT_F24, or the
                                 packed state when p_dtype is DT_PACKED / DT_PACKED_FP8 / DT_PACKED_LION /
-                                DT_PACKED_F32 / DT_PACKED_F24 */
+                                DT_PACKED_F32 / DT_PACKED_F24 / DT_PACKED_LION_F24 */
     uint8_t* p_lo;           /* FP24 lo plane (one byte per element); NULL for FP32; DT_PACKED,
-                                DT_PACKED_LION, DT_PACKED_F32 and DT_PACKED_F24: the destination state
+                                DT_PACKED_LION, DT_PACKED_F32, DT_PACKED_F24 and DT_PACKED_LION_F24: the
+                                destination state
                                 (NULL: in place) */
     const void* g;           /* gradient, g_dtype */
     void* m;                 /* first moment, mv_dtype (FP8: E4M3 codes, padded to 128 per block) */
@@ -160,7 +165,7 @@ typedef struct adambridge_segment {
     int32_t out_dtype;
     int32_t algorithm;
     int32_t p_dtype;         /* DT_F32 (or 0), DT_F24, DT_PACKED, DT_PACKED_FP8, DT_PACKED_LION, DT_PACKED_F32
-                                or DT_PACKED_F24 */
+                                DT_PACKED_F24 or DT_PACKED_LION_F24 */
     int32_t reserved;        /* 0, or ADAMBRIDGE_SEG_OUT_PREVIOUS */
 } adambridge_segment;
 

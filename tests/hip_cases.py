@@ -411,6 +411,11 @@ def unpack_f32_records(case: O.Case, rec: np.ndarray) -> list[np.ndarray]:
     return pads
 
 
+# FP24-master record columns: key, byte range, element type, padding fill
+F24_COLUMNS = (("p", (0, 512), np.uint16, 0x7FA5), ("p_lo", (512, 768), np.uint8, 0xA5),
+               ("m", (768, 1280), np.uint16, 0x7FA6), ("v", (1280, 1792), np.uint16, 0x7FA7))
+
+
 def pack_f24_records(case: O.Case) -> np.ndarray:
     """Separate FP24 master planes, BF16 m and v -> ADAMBRIDGE_DT_PACKED_F24 records (records x 1792
     bytes): per 256 elements, the 256 hi halves, the 256 lo bytes, the 256 m, the 256 v, each in
@@ -418,9 +423,9 @@ def pack_f24_records(case: O.Case) -> np.ndarray:
     unchanged."""
     n = case.n
     nr = max(1, -(-n // 256))
-    rec = np.zeros((nr, 1792), np.uint8)
-    for key, (a, b), dt, fill in (("p", (0, 512), np.uint16, 0x7FA5), ("p_lo", (512, 768), np.uint8, 0xA5),
-                                  ("m", (768, 1280), np.uint16, 0x7FA6), ("v", (1280, 1792), np.uint16, 0x7FA7)):
+    size = 1280 if case.algorithm == O.LION else 1792   # Lion (ADAMBRIDGE_DT_PACKED_LION_F24): no v
+    rec = np.zeros((nr, size), np.uint8)
+    for key, (a, b), dt, fill in F24_COLUMNS[: 3 if case.algorithm == O.LION else 4]:
         col = np.full(nr * 256, fill, dt)
         col[:n] = case.arrays[key].view(dt)
         rec[:, a:b] = col.reshape(nr, 256).view(np.uint8).reshape(nr, b - a)
@@ -431,24 +436,28 @@ def unpack_f24_records(case: O.Case, rec: np.ndarray) -> list[np.ndarray]:
     """ADAMBRIDGE_DT_PACKED_F24 records -> the case's separate planes, m and v (in place); returns
     the padding slots past n of each."""
     n = case.n
-    rec = np.ascontiguousarray(rec).reshape(-1, 1792)
+    rec = np.ascontiguousarray(rec).reshape(-1, 1280 if case.algorithm == O.LION else 1792)
     pads = []
-    for key, (a, b), dt in (("p", (0, 512), np.uint16), ("p_lo", (512, 768), np.uint8),
-                            ("m", (768, 1280), np.uint16), ("v", (1280, 1792), np.uint16)):
+    for key, (a, b), dt, _ in F24_COLUMNS[: 3 if case.algorithm == O.LION else 4]:
         col = np.ascontiguousarray(rec[:, a:b]).view(dt).reshape(-1)
         case.arrays[key] = col[:n].view(case.arrays[key].dtype).copy()
         pads.append(col[n:].copy())
     return pads
 
 
-# record kind -> (p_dtype code, moment dtype, master dtype, pack, unpack)
-_RECORDS = {"f32": (_hip.DT_PACKED_F32, O.DT_F32, O.DT_F32, pack_f32_records, unpack_f32_records),
-            "f24": (_hip.DT_PACKED_F24, O.DT_BF16, O.DT_F24, pack_f24_records, unpack_f24_records)}
+# record kind -> (p_dtype code, moment dtype, master dtype, pack, unpack, algorithm)
+_RECORDS = {"f32": (_hip.DT_PACKED_F32, O.DT_F32, O.DT_F32, pack_f32_records, unpack_f32_records, O.ADAMW),
+            "f24": (_hip.DT_PACKED_F24, O.DT_BF16, O.DT_F24, pack_f24_records, unpack_f24_records, O.ADAMW),
+            "lion-f24": (_hip.DT_PACKED_LION_F24, O.DT_BF16, O.DT_F24, pack_f24_records, unpack_f24_records,
+                         O.LION)}
 
 
 def run_hip_f24_records(cases: list[O.Case], width: int = 16, **kw) -> list[O.Case]:
-    """run_hip through ADAMBRIDGE_DT_PACKED_F24 records (AdamW, FP24 master, BF16 moments)."""
-    return run_hip_f32_records(cases, width, kind="f24", **kw)
+    """run_hip through FP24-master records: ADAMBRIDGE_DT_PACKED_F24 (AdamW, BF16 moments) or, for
+    Lion cases, ADAMBRIDGE_DT_PACKED_LION_F24 (BF16 moment)."""
+    lion = [c.algorithm == O.LION for c in cases]
+    assert all(lion) or not any(lion)
+    return run_hip_f32_records(cases, width, kind="lion-f24" if any(lion) else "f24", **kw)
 
 
 def run_hip_f32_records(cases: list[O.Case], width: int = 16, double_buffer: bool = False,
@@ -459,13 +468,13 @@ def run_hip_f32_records(cases: list[O.Case], width: int = 16, double_buffer: boo
     (ADAMBRIDGE_DT_PACKED_F24, 'f24'): pack on the host, one call, unpack the result.
     ``misalign_g`` elements shift the gradient off its allocation's alignment; ``padding`` receives
     each case's padding slots after the call."""
-    p_code, mv_dt, pt, pack, unpack = _RECORDS[kind]
+    p_code, mv_dt, pt, pack, unpack, algo = _RECORDS[kind]
     kernels = _hip.load()
     work = [c.copy() for c in cases]
     entries, segs = [], []
     by_group = all(c.group is not None for c in work)
     for c in work:
-        assert c.algorithm == O.ADAMW and c.mv_dtype == mv_dt and c.p_dtype == pt
+        assert c.algorithm == algo and c.mv_dtype == mv_dt and c.p_dtype == pt
         O.check_sizes(c)
         rec = torch.from_numpy(pack(c)).cuda()
         dst = torch.full_like(rec, 0x5A) if double_buffer else None
@@ -486,7 +495,7 @@ def run_hip_f32_records(cases: list[O.Case], width: int = 16, double_buffer: boo
                                  g=g.data_ptr(), m=None, v=None, out=out.data_ptr() if out is not None else None,
                                  group=ctypes.pointer(grp) if grp is not None else None, n=c.n, step=c.step,
                                  index=c.index, offset=c.offset, g_dtype=c.g_dtype, mv_dtype=mv_dt,
-                                 out_dtype=c.out_dtype, algorithm=O.ADAMW, p_dtype=p_code,
+                                 out_dtype=c.out_dtype, algorithm=algo, p_dtype=p_code,
                                  reserved=seg_flags))
     arr = kernels.segment_array([ctypes.pointer(s) for s in segs])
     kernels.set_simd_level(WIDTH_LEVEL[width])

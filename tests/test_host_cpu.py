@@ -654,14 +654,15 @@ def test_layout_choice_for_every_algorithm_precision_and_master():
             ("lion", "bf16"): "lion-records", ("lion", "fp8"): "separate", ("lion", "fp32"): "separate"}
     for (algo, prec), layout in want.items():
         assert choose_layout(algo, prec, "fp32") == layout, (algo, prec)
-        assert choose_layout(algo, prec, "fp24") == ("f24-records" if (algo, prec) == ("adamw", "bf16")
-                                                     else "separate")
+        assert choose_layout(algo, prec, "fp24") == {("adamw", "bf16"): "f24-records",
+                                                     ("lion", "bf16"): "lion-f24-records"}.get((algo, prec), "separate")
         assert choose_layout(algo, prec, "fp24", requested="separate") == "separate"
         assert choose_layout(algo, prec, "fp32", master_is_param=True) == "separate"
         assert choose_layout(algo, prec, "fp32", requested="separate") == "separate"
 
 
-@pytest.mark.parametrize("layout", ["pairs", "fp8-records", "lion-records", "f32-records", "f24-records"])
+@pytest.mark.parametrize("layout", ["pairs", "fp8-records", "lion-records", "f32-records", "f24-records",
+                                    "lion-f24-records"])
 def test_arena_plan_aligns_large_buffers_and_packs_small_ones(layout):
     """Buffers of 2 MiB or more start on 2 MiB boundaries, smaller ones on 256-byte boundaries (16-byte
     state access needs 16); no two buffers overlap, and many small tensors take little more than

@@ -476,17 +476,19 @@ def test_f32_records_multi_step_groups_and_steps():
 F24_PADDING = (0x7FA5, 0xA5, 0x7FA6, 0x7FA7)   # hi, lo, m, v fill of pack_f24_records
 
 
+@pytest.mark.parametrize("algo", [O.ADAMW, O.LION])
 @pytest.mark.parametrize("double_buffer", [False, True])
-def test_f24_records_match_oracle(double_buffer):
+def test_f24_records_match_oracle(double_buffer, algo):
     """ADAMBRIDGE_DT_PACKED_F24 (FP24 master planes and BF16 m, v in 1792-byte records) gives the
     separate FP24 layout's bytes: sizes around the record and the lane's 4 elements, the reproduced
     SIMD widths' tails, offsets, stochastic and nearest rounding, every grad/out dtype, delayed
     (previous-weight) output; in place, the padding slots of the last record keep their bits."""
-    rng = np.random.default_rng(61)
+    rng = np.random.default_rng(61 + algo)
     cases = []
     for gt, ot, n in itertools.product([O.DT_BF16, O.DT_F32], [O.DT_NONE, O.DT_F32, O.DT_BF16],
                                        [1, 2, 3, 4, 5, 15, 16, 17, 255, 256, 257, 1000, 2048 + 77, 5001]):
-        cases.append(O.make_case(rng, n, mv_dtype=O.DT_BF16, p_dtype=O.DT_F24, g_dtype=gt, out_dtype=ot,
+        cases.append(O.make_case(rng, n, algorithm=algo, mv_dtype=O.DT_BF16, p_dtype=O.DT_F24, g_dtype=gt,
+                                 out_dtype=ot,
                                  stochastic=bool(rng.integers(0, 2)), offset=int(rng.integers(0, 2**32)),
                                  index=int(rng.integers(0, 999)), step=int(rng.integers(1, 30))))
     for width in (16, 8, 0):
@@ -501,11 +503,12 @@ def test_f24_records_match_oracle(double_buffer):
                     assert (col == fill).all(), f"padding changed at n={c.n}"
 
 
-def test_f24_records_misaligned_gradient_specials_and_steps():
+@pytest.mark.parametrize("algo", [O.ADAMW, O.LION])
+def test_f24_records_misaligned_gradient_specials_and_steps(algo):
     """Gradients shifted by one element and by two, non-finite inputs, several segments through the
     group path, and three consecutive steps of one segment."""
-    rng = np.random.default_rng(62)
-    cases = [O.make_case(rng, n, mv_dtype=O.DT_BF16, p_dtype=O.DT_F24, special=sp, stochastic=sr)
+    rng = np.random.default_rng(62 + algo)
+    cases = [O.make_case(rng, n, algorithm=algo, mv_dtype=O.DT_BF16, p_dtype=O.DT_F24, special=sp, stochastic=sr)
              for n, sp, sr in ((999, False, True), (4096, False, False), (4096, True, True), (5001, True, False))]
     want = O.run_many(cases, "oracle", 16)
     for shift in (1, 2):
@@ -513,11 +516,11 @@ def test_f24_records_misaligned_gradient_specials_and_steps():
         for w, g in zip(want, got):
             bad = O.outputs_equal(w, g, nan_equiv=True)
             assert not bad, (shift, bad)
-    cases = [O.make_case(rng, 3000 + 64 * k + 3, mv_dtype=O.DT_BF16, p_dtype=O.DT_F24, explicit=False, index=k,
-                         step=k + 2, seed=5) for k in range(12)]
+    cases = [O.make_case(rng, 3000 + 64 * k + 3, algorithm=algo, mv_dtype=O.DT_BF16, p_dtype=O.DT_F24,
+                         explicit=False, index=k, step=k + 2, seed=5) for k in range(12)]
     for w, g in zip(O.run_many(cases, "oracle", 16), run_hip_f24_records(cases, 16)):
         check(w, g)
-    case = O.make_case(rng, 5000, mv_dtype=O.DT_BF16, p_dtype=O.DT_F24)
+    case = O.make_case(rng, 5000, algorithm=algo, mv_dtype=O.DT_BF16, p_dtype=O.DT_F24)
     grads = [O.make_case(rng, 5000, mv_dtype=O.DT_BF16).arrays["g"] for _ in range(3)]
     check(run_steps(case, grads, oracle_runner, 16), run_steps(case, grads, run_hip_f24_records, 16))
 
@@ -689,7 +692,8 @@ def _previous_weight(case):
     return O.bf16_bits(old) if case.out_dtype == O.DT_BF16 else old.astype(np.float32)
 
 
-@pytest.mark.parametrize("layout", ["separate", "pairs", "fp8-records", "lion-records", "f32-records", "f24-records"])
+@pytest.mark.parametrize("layout", ["separate", "pairs", "fp8-records", "lion-records", "f32-records", "f24-records",
+                                    "lion-f24-records"])
 def test_out_previous_writes_the_weight_from_before_the_update(layout):
     """ADAMBRIDGE_SEG_OUT_PREVIOUS (delayed updates): out receives the weight of the master as stored
     before the update -- FP32, or bf16 by the kernels' rounding of FP32 and decoded FP24 masters,
@@ -701,10 +705,10 @@ def test_out_previous_writes_the_weight_from_before_the_update(layout):
     combos = {"separate": [(a, mv, pt) for a in ALGOS for mv in MVS for pt in PTS],
               "pairs": [(O.ADAMW, O.DT_BF16, O.DT_F32)], "fp8-records": [(O.ADAMW, O.DT_FP8, O.DT_F32)],
               "lion-records": [(O.LION, O.DT_BF16, O.DT_F32)], "f32-records": [(O.ADAMW, O.DT_F32, O.DT_F32)],
-              "f24-records": [(O.ADAMW, O.DT_BF16, O.DT_F24)]}[layout]
+              "f24-records": [(O.ADAMW, O.DT_BF16, O.DT_F24)], "lion-f24-records": [(O.LION, O.DT_BF16, O.DT_F24)]}[layout]
     runner = {"separate": run_hip, "pairs": run_hip_packed, "fp8-records": run_hip_records,
               "lion-records": run_hip_lion_records, "f32-records": run_hip_f32_records,
-              "f24-records": run_hip_f24_records}[layout]
+              "f24-records": run_hip_f24_records, "lion-f24-records": run_hip_f24_records}[layout]
     cases = []
     for (algo, mv, pt), gt, ot, sr, n in itertools.product(combos, [O.DT_BF16, O.DT_F32], [O.DT_F32, O.DT_BF16],
                                                              [True, False], [1, 15, 17, 129, 1000, 8192 + 77]):

@@ -950,7 +950,7 @@ def _oracle_state_after(params_bf16, grads_seq, precision, master, lr, wd, betas
 
 
 @pytest.mark.parametrize("precision,master,lion", [("bf16", "fp32", False), ("fp32", "fp32", False),
-                                                   ("fp8", "fp24", False), ("bf16", "fp24", True),
+                                                   ("fp8", "fp24", False), ("bf16", "fp24", True), ("bf16", "fp24", False),
                                                    ("fp8", "fp32", True), ("fp8", "fp32", False)])
 @pytest.mark.parametrize("hooks", [False, True])
 def test_api_updates_are_bit_exact_against_the_oracle(precision, master, lion, hooks):
@@ -991,7 +991,8 @@ def test_api_updates_are_bit_exact_against_the_oracle(precision, master, lion, h
         assert np.array_equal(m_data.view(torch.uint8).numpy().view(want_m.dtype).reshape(want_m.shape), want_m), \
             f"param {k} m"
         if master == "fp24":
-            hi, lo = slot.state.master.native_buffers
+            planes = slot.state.window(0, slot.numel)   # separate arrays or FP24-master records
+            hi, lo = planes["p"].contiguous(), planes["p_lo"].contiguous()
             assert np.array_equal(hi.cpu().view(torch.int16).numpy().view(np.uint16), c.arrays["p"])
             assert np.array_equal(lo.cpu().numpy(), c.arrays["p_lo"])
         else:
@@ -1086,7 +1087,7 @@ def test_state_layouts_give_identical_bytes(hooks, precision):
 
 
 @pytest.mark.parametrize("algo,precision", [("adamw", "bf16"), ("adamw", "fp8"), ("lion", "bf16"),
-                                            ("adamw", "fp32"), ("adamw", "bf16-fp24")])
+                                            ("adamw", "fp32"), ("adamw", "bf16-fp24"), ("lion", "bf16-fp24")])
 def test_interleaved_checkpoint_gathered_on_host_when_the_device_is_short(algo, precision):
     """Interleaved states (BF16 pairs, FP8 records, Lion records, FP32 records, FP24-master records)
     are gathered into the reference's checkpoint arrays on the device when it has room, else into
