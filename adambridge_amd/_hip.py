@@ -19,7 +19,7 @@ from pathlib import Path
 
 import torch
 
-__all__ = ["HipKernels", "HParams", "Group", "Segment", "load", "LIB_PATH", "DT_NONE", "DT_F32", "DT_BF16",
+__all__ = ["HipKernels", "HParams", "Group", "Segment", "Plane", "plane_of", "fp24_plane", "load", "LIB_PATH", "DT_NONE", "DT_F32", "DT_BF16",
            "DT_FP8", "DT_F24", "DT_PACKED", "DT_PACKED8", "DT_PACKED_LION", "DT_PACKED_F32", "DT_PACKED_F24", "DT_PACKED_LION_F24", "SEG_OUT_PREVIOUS", "MOMENT_CODES", "MASTER_CODES",
            "ALGORITHMS", "SIMD_NAMES"]
 
@@ -62,6 +62,33 @@ class Segment(ctypes.Structure):
                 ("reserved", ctypes.c_int32)]
 
 
+class Plane(ctypes.Structure):
+    """adambridge_plane: element i at data + (i >> group_log2) * stride + (i mod 2^group_log2) * size
+    (stride 0: contiguous); an FP24 plane's low bytes likewise from ``lo`` (no reference counterpart)."""
+    _fields_ = [("data", ctypes.c_void_p), ("lo", ctypes.c_void_p), ("stride", ctypes.c_int64),
+                ("dtype", ctypes.c_int32), ("group_log2", ctypes.c_int32)]
+
+
+CONVERT_STOCHASTIC = 1
+CAPABILITIES = {"packed_layouts": 0x01, "out_previous": 0x02, "noalloc": 0x04, "convert": 0x08,
+                "convert_plane": 0x10, "stream_copy": 0x20}
+
+
+def plane_of(t: torch.Tensor) -> Plane:
+    """The plane of a contiguous float32 or bfloat16 device tensor."""
+    if not t.is_contiguous() or t.dtype not in _DTYPE_CODES:
+        raise ValueError(f"a plane is a contiguous float32 or bfloat16 tensor, got {t.dtype}"
+                         f"{'' if t.is_contiguous() else ' (strided)'}")
+    return Plane(t.data_ptr(), None, 0, _DTYPE_CODES[t.dtype], 0)
+
+
+def fp24_plane(hi: torch.Tensor, lo: torch.Tensor) -> Plane:
+    """The plane of an FP24 master's contiguous hi (BF16 bits) and lo (uint8) tensors."""
+    if not (hi.is_contiguous() and lo.is_contiguous()) or hi.element_size() != 2 or lo.element_size() != 1:
+        raise ValueError("an FP24 plane is a contiguous 2-byte hi tensor and a contiguous 1-byte lo tensor")
+    return Plane(hi.data_ptr(), lo.data_ptr(), 0, DT_F24, 0)
+
+
 _SegArray = ctypes.POINTER(ctypes.POINTER(Segment))
 
 # Every symbol include/adambridge_hip.h declares.
@@ -73,6 +100,7 @@ EXPORTS = (
     "adambridge_pool_sync", "adambridge_set_stream", "adambridge_last_error", "adambridge_backend",
     "adambridge_check_conversions", "adambridge_convert", "adambridge_plan_launches",
     "adambridge_multi_step_noalloc", "adambridge_stream_copy", "adambridge_recycle_device_memory",
+    "adambridge_convert_plane", "adambridge_capabilities",
 )
 
 
@@ -110,6 +138,9 @@ def open_library(path: Path = LIB_PATH) -> ctypes.CDLL:
         "adambridge_multi_step_noalloc": (ctypes.c_int, [vp, _SegArray, i32]),
         "adambridge_stream_copy": (ctypes.c_int, [vp, vp, i64]),
         "adambridge_recycle_device_memory": (ctypes.c_int, [i64]),
+        "adambridge_convert_plane": (ctypes.c_int, [ctypes.POINTER(Plane), ctypes.POINTER(Plane), i64, u64,
+                                                    ctypes.c_uint32, i32]),
+        "adambridge_capabilities": (ctypes.c_uint32, []),
     }
     for name in EXPORTS:
         fn = getattr(lib, name)
@@ -291,6 +322,28 @@ class HipKernels:
                                               dst_scale.data_ptr() if codes[1] == DT_FP8 else None, codes[1], n,
                                               0 if role == "m" else 1)
         self._check(rc, "adambridge_convert")
+
+    @property
+    def capabilities(self) -> set[str]:
+        """What the library adds to the reference's ABI (adambridge_capabilities), by name."""
+        bits = self._lib.adambridge_capabilities()
+        return {name for name, bit in CAPABILITIES.items() if bits & bit}
+
+    def convert_plane(self, src: Plane, dst: Plane, n: int, device: torch.device, offset: int = 0,
+                      seed: int | None = None) -> None:
+        """Copy ``n`` values from plane ``src`` to plane ``dst`` on ``device``'s current stream,
+        converting between their types (adambridge_convert_plane): exact where the destination
+        represents the value, else rounded as the kernels round -- to nearest, or stochastically with
+        the 32-bit stream ``seed`` and element index ``offset + i``.  The planes' memory must stay
+        alive until the stream has run the copy."""
+        if n < 0:
+            raise ValueError(f"convert_plane: n = {n}")
+        with torch.cuda.device(device):
+            self._lib.adambridge_set_stream(torch.cuda.current_stream(device).cuda_stream)
+            rc = self._lib.adambridge_convert_plane(ctypes.byref(src), ctypes.byref(dst), int(n), int(offset),
+                                                    0 if seed is None else seed & 0xFFFFFFFF,
+                                                    0 if seed is None else CONVERT_STOCHASTIC)
+        self._check(rc, "adambridge_convert_plane")
 
     def fused_adamw(self, master: torch.Tensor, grad: torch.Tensor, m: torch.Tensor, v: torch.Tensor,
                     out: torch.Tensor | None, hp: HParams, lo: int, hi: int) -> None:

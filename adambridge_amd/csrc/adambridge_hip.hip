@@ -1562,6 +1562,106 @@ inline ConvertFn convert_kernel(int src, int dst, bool v)
     }
 }
 
+// --------------------------------------------------------- plane conversion kernel
+//
+// Master weights (or any FP32 / BF16 / FP24 values) from one plane to another: the FP24 master's
+// rounding on load (kernels.c:145-160; precision.py:421-480), its expansion to FP32, and the bf16
+// working weight of a master (kernels.c:108-112), each in one pass with no temporaries.  A plane
+// is a base address and a group structure: element i lives at data + (i >> shift) * stride +
+// (i & (2^shift - 1)) * size (stride 0: contiguous), which describes the separate arrays and the
+// master columns of the interleaved layouts alike; DT_PACKED8 names the masters of FP8 block
+// records (record_master_offset).  One element per lane, grid-stride.
+
+struct DevPlane {
+    uint8_t* data;
+    uint8_t* lo;
+    int64_t stride;
+    int32_t dtype;
+    int32_t shift;
+};
+
+// Byte offset of element i in plane q for values of `size` bytes.
+__device__ __forceinline__ int64_t plane_at(const DevPlane& q, int64_t i, int64_t size)
+{
+    if (q.stride == 0) return i * size;
+    return (i >> q.shift) * q.stride + (i & (((int64_t)1 << q.shift) - 1)) * size;
+}
+
+// The FP32 bits of element i of a plane of type DT.
+template <int DT>
+__device__ __forceinline__ uint32_t plane_load(const DevPlane& q, int64_t i)
+{
+    if constexpr (DT == DT_F32) return ld(reinterpret_cast<const uint32_t*>(q.data + plane_at(q, i, 4)));
+    else if constexpr (DT == DT_PACKED8) return ld(reinterpret_cast<const uint32_t*>(q.data + record_master_offset(i)));
+    else if constexpr (DT == DT_BF16) return (uint32_t)ld(reinterpret_cast<const uint16_t*>(q.data + plane_at(q, i, 2))) << 16;
+    else
+        return ((uint32_t)ld(reinterpret_cast<const uint16_t*>(q.data + plane_at(q, i, 2))) << 16) |
+               ((uint32_t)ld(q.lo + plane_at(q, i, 1)) << 8);
+}
+
+// FP32 bits b stored as element i of a plane of type DT; `exact`: b is representable in DT
+// (copied bit for bit), else rounded -- stochastically with r when SR, to nearest otherwise.
+template <int DT, bool SR>
+__device__ __forceinline__ void plane_store(const DevPlane& q, int64_t i, uint32_t b, bool exact, uint32_t r)
+{
+    if constexpr (DT == DT_F32) st(reinterpret_cast<uint32_t*>(q.data + plane_at(q, i, 4)), b);
+    else if constexpr (DT == DT_PACKED8) st(reinterpret_cast<uint32_t*>(q.data + record_master_offset(i)), b);
+    else if constexpr (DT == DT_BF16) {
+        const uint32_t h = exact ? b >> 16 : bf16_store<SR>(bitsf(b), r);   // nearest: the working weight's rule
+        st(reinterpret_cast<uint16_t*>(q.data + plane_at(q, i, 2)), (uint16_t)h);
+    } else {
+        const uint32_t t = exact ? b : f24_round<SR>(bitsf(b), r);
+        st(reinterpret_cast<uint16_t*>(q.data + plane_at(q, i, 2)), (uint16_t)(t >> 16));
+        st(q.lo + plane_at(q, i, 1), (uint8_t)(t >> 8));
+    }
+}
+
+// Whether every value of type SRC is representable in type DST.
+constexpr bool plane_exact(int src, int dst)
+{
+    const int w = [](int d) { return d == DT_BF16 ? 16 : d == DT_F24 ? 24 : 32; }(src);
+    const int v = [](int d) { return d == DT_BF16 ? 16 : d == DT_F24 ? 24 : 32; }(dst);
+    return w <= v;
+}
+
+template <int SRC, int DST, bool SR>
+__global__ __launch_bounds__(kThreads) void k_convert_plane(DevPlane src, DevPlane dst, int64_t n, uint32_t idx0,
+                                                            uint32_t seed)
+{
+    constexpr bool kExact = plane_exact(SRC, DST);
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+        const uint32_t b = plane_load<SRC>(src, i);
+        const uint32_t r = (SR && !kExact) ? hash32((idx0 + (uint32_t)i) ^ seed) : 0u;
+        plane_store<DST, SR>(dst, i, b, kExact, r);
+    }
+}
+
+using PlaneFn = void (*)(DevPlane, DevPlane, int64_t, uint32_t, uint32_t);
+
+// Plane types by index: 0 F32, 1 BF16, 2 F24, 3 FP8-record masters.
+constexpr int kPlaneTypes[4] = {DT_F32, DT_BF16, DT_F24, DT_PACKED8};
+
+template <int I>
+constexpr PlaneFn plane_entry()
+{
+    constexpr int s = (I / 2) / 4, d = (I / 2) % 4;
+    return &k_convert_plane<kPlaneTypes[s], kPlaneTypes[d], (I % 2) == 1>;
+}
+
+template <int... I>
+constexpr auto make_plane_table(std::integer_sequence<int, I...>)
+{
+    return std::array<PlaneFn, sizeof...(I)>{plane_entry<I>()...};
+}
+
+static const auto kPlaneKernels = make_plane_table(std::make_integer_sequence<int, 32>{});
+
+inline int plane_type_index(int dtype)
+{
+    return dtype == DT_F32 ? 0 : dtype == DT_BF16 ? 1 : dtype == DT_F24 ? 2 : dtype == DT_PACKED8 ? 3 : -1;
+}
+
 // ------------------------------------------------------ conversion self-check
 
 // Every FP32 bit pattern through the conversion instructions the kernels use, compared with the

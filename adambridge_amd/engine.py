@@ -39,7 +39,6 @@ from dataclasses import dataclass, field
 import torch
 
 from . import _hip
-from .formats import bf16_weight
 from .precision import MomentStore, make_store
 from .state import ParamState, arena_memory, choose_layout, new_states
 
@@ -498,10 +497,8 @@ class UpdateEngine:
                 for ev in {id(s.done_ev): s.done_ev for s in members if s.done_ev is not None}.values():
                     lanes.wb.wait_event(ev)
                 with torch.cuda.stream(lanes.wb), torch.no_grad():
-                    for slot in members:
-                        master = slot.state.master_fp32()
-                        weight = master if slot.param.dtype == torch.float32 else bf16_weight(master)
-                        slot.param.copy_(weight.view(slot.param.shape))
+                    for slot in members:   # one conversion pass each, straight into the parameter
+                        slot.state.write_weights(slot.param)
             self._used.add(device)
 
     # ---------------------------------------------------------- synchronizing

@@ -23,9 +23,11 @@ xor the stream's 32-bit seed.
 On the optimizer's step path every format is encoded and decoded by the HIP
 kernels.  What runs here is the work off that path -- initial state,
 ``set_precision``, checkpoints -- and the functions are written so that a
-device tensor is encoded to nearest by the library's conversion kernel
-(``adambridge_convert``, one pass over HBM) and a host tensor by torch casts;
-both give the kernels' bits (tests/test_host_cpu.py, tests/test_convert_gpu.py).
+device tensor is converted by the library's kernels in one pass over HBM --
+moments to nearest by ``adambridge_convert``, FP24 masters (both ways) and
+bf16 working weights by ``adambridge_convert_plane`` -- and a host tensor by
+torch casts and integer operations; both give the kernels' bits
+(tests/test_host_cpu.py, tests/test_convert_gpu.py).
 """
 
 from __future__ import annotations
@@ -38,8 +40,8 @@ import torch
 __all__ = [
     "PRECISIONS", "MASTER_PRECISIONS", "FP8_BLOCK", "Fp8Format", "FP8_FORMATS", "canonical_precision",
     "canonical_master_precision", "moment_bytes", "bytes_per_param", "lowbias32", "stream_seed", "counter_hash",
-    "round_bits_stochastic", "bf16_encode", "bf16_weight", "fp8_blocks", "fp8_encode", "fp8_decode", "fp24_round", "fp24_split",
-    "fp24_join",
+    "round_bits_stochastic", "bf16_encode", "bf16_weight", "fp8_blocks", "fp8_encode", "fp8_decode", "fp24_encode",
+    "fp24_round", "fp24_split", "fp24_join", "convert_plane",
 ]
 
 # Accepted spellings (case-insensitive) -> canonical name: the reference's tables,
@@ -164,6 +166,28 @@ def _device_convert(src: torch.Tensor, dst: torch.Tensor, dst_scale: torch.Tenso
     _hip.load().convert(x, None, dst, dst_scale, n, role)
 
 
+def _on_device(x: torch.Tensor) -> bool:
+    """Whether ``x``'s conversions run as the library's plane-conversion kernel (device memory)
+    rather than as torch integer operations (host memory)."""
+    return x.is_cuda
+
+
+def _values(x: torch.Tensor) -> torch.Tensor:
+    """``x`` flat and contiguous, as float32 unless it is bfloat16 (both are planes the kernel reads)."""
+    flat = x.detach().reshape(-1)
+    if flat.dtype not in (torch.float32, torch.bfloat16):
+        flat = flat.to(torch.float32)
+    return flat.contiguous()
+
+
+def convert_plane(src, dst, n: int, device, offset: int = 0, seed: int | None = None) -> None:
+    """``n`` values from plane ``src`` into plane ``dst`` by the library's plane-conversion kernel
+    (adambridge_convert_plane) on ``device``'s current stream; planes are ``_hip.Plane`` structs."""
+    from . import _hip
+
+    _hip.load().convert_plane(src, dst, n, torch.device(device), offset, seed)
+
+
 # --------------------------------------------------------------------- BF16
 
 def bf16_encode(x: torch.Tensor, seed: int | None = None, start: int = 0) -> torch.Tensor:
@@ -182,7 +206,16 @@ def bf16_encode(x: torch.Tensor, seed: int | None = None, start: int = 0) -> tor
 
 def bf16_weight(x: torch.Tensor) -> torch.Tensor:
     """FP32 ``x`` as the bf16 working weight the kernels write (kernels.c:108-112): nearest-even,
-    a NaN kept with its sign and payload and made quiet.  A new flat tensor on x's device."""
+    a NaN kept with its sign and payload and made quiet.  A new flat tensor on x's device (there
+    written by the plane-conversion kernel, with no temporaries)."""
+    if _on_device(x):
+        from . import _hip
+
+        src = _values(x)
+        out = torch.empty(src.numel(), dtype=torch.bfloat16, device=src.device)
+        if src.numel():
+            convert_plane(_hip.plane_of(src), _hip.plane_of(out), src.numel(), src.device)
+        return out
     bits = _as_u32(x)
     nan = bits.bitwise_and(0x7FFFFFFF) > 0x7F800000
     rounded = (bits + 0x7FFF + bits.bitwise_right_shift(16).bitwise_and_(1)).bitwise_and_(_U32)
@@ -240,9 +273,37 @@ def fp8_decode(codes: torch.Tensor, scales: torch.Tensor, role: str, n: int) -> 
 
 # --------------------------------------------------------------------- FP24
 
+def fp24_encode(x: torch.Tensor, seed: int | None = None, start: int = 0,
+                out: tuple[torch.Tensor, torch.Tensor] | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """FP32 ``x`` rounded to its top 24 bits (kernels.c:145-160) and split into the FP24 planes (hi:
+    BF16 bits as bfloat16, lo: the next byte as uint8): stochastic with stream ``seed`` (element i
+    at stream index ``start + i``), else nearest-even with a NaN kept NaN (quiet bit set).  ``out``:
+    contiguous planes to write (new ones otherwise).  On the device one pass of the plane-conversion
+    kernel; in host memory torch integer operations."""
+    src = _values(x)
+    n = src.numel()
+    if out is None:
+        out = (torch.empty(n, dtype=torch.bfloat16, device=src.device), torch.empty(n, dtype=torch.uint8, device=src.device))
+    hi, lo = out
+    if _on_device(src):
+        from . import _hip
+
+        if src.dtype != torch.float32:   # the FP32 value is what is rounded (a BF16 NaN is quietened too)
+            src = src.to(torch.float32)
+        if n:
+            convert_plane(_hip.plane_of(src), _hip.fp24_plane(hi, lo), n, src.device, start, seed)
+        return hi, lo
+    h, low = fp24_split(fp24_round(src, seed, start))
+    hi.copy_(h)
+    lo.copy_(low)
+    return hi, lo
+
+
 def fp24_round(x: torch.Tensor, seed: int | None = None, start: int = 0) -> torch.Tensor:
     """FP32 ``x`` rounded to its top 24 bits (kernels.c:145-160), as a new flat FP32 tensor:
-    stochastic with stream ``seed``, else nearest-even with a NaN kept NaN (quiet bit set)."""
+    stochastic with stream ``seed``, else nearest-even with a NaN kept NaN (quiet bit set, its low
+    byte kept).  The reference's torch helpers' rule (precision.py:191-204), for the store API's
+    functions of that name; the optimizer's own state goes through fp24_encode."""
     if seed is not None:
         return round_bits_stochastic(x, 8, start, seed)
     bits = _as_u32(x)
@@ -253,12 +314,22 @@ def fp24_round(x: torch.Tensor, seed: int | None = None, start: int = 0) -> torc
 
 def fp24_split(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Planes of FP32 values already rounded to 24 bits: (BF16 bits as bfloat16, next byte as uint8)."""
+    if _on_device(x):
+        return fp24_encode(x)   # nearest-even leaves a 24-bit value as it is
     bits = _as_u32(x)
     hi = ((bits >> 16) - (((bits >> 31) & 1) << 16)).to(torch.int16).view(torch.bfloat16)
     return hi, ((bits >> 8) & 0xFF).to(torch.uint8)
 
 
 def fp24_join(hi: torch.Tensor, lo: torch.Tensor) -> torch.Tensor:
-    """FP32 values from the two FP24 planes."""
+    """FP32 values from the two FP24 planes (on the device, one pass of the plane-conversion kernel)."""
+    if _on_device(hi):
+        from . import _hip
+
+        h, low = hi.reshape(-1).contiguous(), lo.reshape(-1).contiguous()
+        out = torch.empty(h.numel(), dtype=torch.float32, device=h.device)
+        if h.numel():
+            convert_plane(_hip.fp24_plane(h, low), _hip.plane_of(out), h.numel(), h.device)
+        return out
     top = hi.reshape(-1).contiguous().view(torch.int16).to(torch.int64).bitwise_and_(0xFFFF)
     return _from_u32((top << 16) | (lo.reshape(-1).to(torch.int64) << 8))

@@ -21,6 +21,9 @@ The parts:
 * ``_StepWindow`` -- what the gradient hooks may do in the current step:
   ``no_sync`` nesting, gradient-accumulation micro-batches;
 * ``_HookSet`` -- the post-accumulate-grad hooks;
+* ``_LaunchPoints`` -- where a backward pass launches the hooked updates: at the
+  start of the next hooked module's backward (its GEMMs), not beside the
+  elementwise work that follows a weight gradient;
 * ``_CheckpointReader`` -- validates a whole checkpoint before anything changes.
 
 Host-side knobs of the reference with nothing to act on here -- NUMA
@@ -208,6 +211,54 @@ class _HookSet:
         self.active = False
 
 
+class _LaunchPoints:
+    """Where a backward pass launches the hooked updates it has deferred: at the start of the backward
+    of each module that owns hooked parameters, and at the end of the pass.
+
+    A parameter's gradient is ready right after its weight-gradient GEMM; what the backward runs next
+    is usually elementwise work bound by HBM (an activation's or a norm's backward), which an update
+    started then -- itself bound by HBM -- slows by about as much as it saves.  The backward of the
+    next module that owns hooked parameters begins with its GEMMs, which leave most of HBM's
+    bandwidth unused, so the update is launched there instead: a forward hook on each such module
+    registers a hook on the gradient of the module's output, which fires when that gradient is
+    computed and before the module's own backward kernels are enqueued.  A forward pass that ran
+    under compilation (or without gradients) registers nothing, and its backward launches each
+    update at its parameter's hook.  Hooks reach the optimizer through a weak reference, as
+    :class:`_HookSet`'s do."""
+
+    def __init__(self, launch: Callable[[], None]):
+        target = weakref.WeakMethod(launch)
+
+        def fire(*_grad) -> None:   # a gradient hook: leaves the gradient as it is
+            bound = target()
+            if bound is not None:
+                bound()
+
+        self.fire = torch.compiler.disable(fire)
+        self.armed = False          # this step's forward registered launch points
+        self._handles: list = []
+
+        def on_forward(module, inputs, output) -> None:
+            if torch.compiler.is_compiling() or not torch.is_grad_enabled():
+                return
+            out = output
+            if isinstance(out, (tuple, list)):
+                out = next((t for t in out if isinstance(t, torch.Tensor) and t.requires_grad), None)
+            if isinstance(out, torch.Tensor) and out.requires_grad:
+                out.register_hook(self.fire)
+                self.armed = True
+
+        self._on_forward = on_forward
+
+    def add(self, modules: Iterable[torch.nn.Module]) -> None:
+        self._handles += [m.register_forward_hook(self._on_forward) for m in modules]
+
+    def clear(self) -> None:
+        while self._handles:
+            self._handles.pop().remove()
+        self.armed = False
+
+
 class _CheckpointReader:
     """A checkpoint's per-parameter entries, validated as a whole before anything is changed (a
     checkpoint may come from another model, another version or an untrusted source)."""
@@ -339,6 +390,9 @@ class AdamBridge(torch.optim.Optimizer):
         self._registry = _Registry()
         self._window = _StepWindow(accumulation_steps)
         self._hooks = _HookSet(self._on_grad_ready)
+        self._points = _LaunchPoints(self._launch_deferred)
+        self._deferred: list[tuple[ParamSlot, torch.Tensor]] = []   # hooked updates waiting for a launch point
+        self._end_queued = False     # the current backward pass launches what is left at its end
         self._autotune_log: list[str] = []
         if autotune:
             self._autotune_log.append("autotune: nothing to tune on the GPU (no host threads, one kernel launch)")
@@ -393,10 +447,14 @@ class AdamBridge(torch.optim.Optimizer):
             self._hooks.add(targets)
             self._hooks.active = True
             self._engine.hooked_slots = [self._registry.by_param[p] for p in targets]
+            if model is not None:   # launch points: the start of each owner's backward (_LaunchPoints)
+                ids = {id(p) for p in targets}
+                self._points.add(m for m in model.modules() if any(id(p) in ids for p in m.parameters(recurse=False)))
         return self
 
     def detach_hooks(self) -> None:
         self._hooks.clear()
+        self._points.clear()
 
     @property
     def _hooked(self) -> bool:
@@ -407,18 +465,51 @@ class AdamBridge(torch.optim.Optimizer):
         return self._window.suppress()
 
     def _on_grad_ready(self, p: torch.Tensor) -> None:
-        """The hook (optimizer.py:291-304): update ``p`` now, unless the step window says otherwise."""
-        if p.grad is not None and self._window.hook_may_update():
-            self._submit([self._registry.by_param[p]], [p.grad], hooked=True, release=self.release_grads)
+        """The hook (optimizer.py:291-304): update ``p`` with this gradient, unless the step window says
+        otherwise -- launched at the next launch point of this backward pass when its forward
+        registered them (_LaunchPoints), else now."""
+        if p.grad is None or not self._window.hook_may_update():
+            return
+        slot = self._registry.by_param[p]
+        if not self._points.armed:
+            self._submit([slot], [p.grad], hooked=True, release=self.release_grads)
+            return
+        self._check_submission([slot], [p.grad])
+        self._deferred.append((slot, p.grad))
+        slot.submitted = True
+        if self.release_grads:
+            p.grad = None   # the update holds the gradient until it is launched
+        if not self._end_queued:   # whatever no later launch point takes is launched when the pass ends
+            torch.autograd.Variable._execution_engine.queue_callback(self._end_of_backward)
+            self._end_queued = True
 
-    def _submit(self, slots: list[ParamSlot], grads: list[torch.Tensor], hooked: bool, release: bool) -> None:
-        """One launch for ``slots`` (optimizer.py:310-321, batched)."""
+    def _launch_deferred(self) -> None:
+        """Launch the deferred hooked updates (one launch per device), ordered after the work enqueued
+        so far on the current stream."""
+        todo, self._deferred = self._deferred, []
+        if todo:
+            try:
+                self._engine.update([s for s, _ in todo], [g for _, g in todo], hooked=True)
+            except Exception as exc:
+                raise RuntimeError(f"adambridge update failed: {exc}") from exc
+
+    def _end_of_backward(self) -> None:
+        self._end_queued = False
+        self._points.armed = False   # the next forward registers new launch points
+        self._launch_deferred()
+
+    @staticmethod
+    def _check_submission(slots: list[ParamSlot], grads: list[torch.Tensor]) -> None:
         if any(s.submitted for s in slots):
             raise RuntimeError(
                 "AdamBridge: parameter received a second gradient before step_sync(); "
                 "run extra backward passes inside optimizer.no_sync() to accumulate gradients")
         if any(g.is_sparse for g in grads):
             raise RuntimeError("AdamBridge does not support sparse gradients")
+
+    def _submit(self, slots: list[ParamSlot], grads: list[torch.Tensor], hooked: bool, release: bool) -> None:
+        """One launch for ``slots`` (optimizer.py:310-321, batched)."""
+        self._check_submission(slots, grads)
         try:
             self._engine.update(slots, grads, hooked=hooked)
         except Exception as exc:   # surfaced as the reference surfaces its workers' errors (engine.py:1150-1158)
@@ -432,6 +523,8 @@ class AdamBridge(torch.optim.Optimizer):
         """Close the step (optimizer.py:332-355): update what the hooks left -- the small parameters,
         and with gradient accumulation any parameter whose window the step cut short -- then order
         every update before subsequent work on the current stream (a stream wait, not a host wait)."""
+        self._launch_deferred()   # normally launched by their backward pass already
+        self._points.armed = False
         with self._window.closing(self._registry):
             if not self._window.suppressed:
                 self._update_leftovers()
@@ -501,7 +594,11 @@ class AdamBridge(torch.optim.Optimizer):
         return self._engine.kernels.backend
 
     def memory_report(self) -> dict[str, int]:
-        """Device bytes held by the optimizer, by category (optimizer.py:496-513)."""
+        """Bytes held by the optimizer, by category (optimizer.py:496-513): ``master``, ``moments``,
+        ``staging`` (write-back buffers) and ``reserved`` (arena memory the first gradient hook set
+        aside for hooked parameters whose state is not built yet), and their sum ``total``.  Every
+        byte is device memory, so ``gpu_state`` -- in the reference the state kept on the GPU apart
+        from its host-memory ``total`` -- equals ``total`` here; no host memory is held."""
         master = moments = staging = 0
         for slot in self._ordered:
             if slot.state is None:
@@ -509,8 +606,10 @@ class AdamBridge(torch.optim.Optimizer):
             a, b = slot.state.footprint()
             master, moments = master + a, moments + b
             staging += 0 if slot.out is None else slot.out.nbytes
-        total = master + moments + staging
-        return {"master": master, "moments": moments, "staging": staging, "total": total, "gpu_state": total}
+        reserved = sum(t.nbytes for bufs in self._engine._reserved.values() for t in bufs)
+        total = master + moments + staging + reserved
+        return {"master": master, "moments": moments, "staging": staging, "reserved": reserved, "total": total,
+                "gpu_state": total}
 
     def expected_bytes_per_param(self) -> float:
         return bytes_per_param(self.precision, 1 if self._algorithm == "lion" else 2, master=self.master_precision)

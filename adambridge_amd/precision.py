@@ -268,6 +268,9 @@ class FP24Store(MomentStore):
             self.hi.copy_(flat)
             self.lo.zero_()
             return
+        if self.device.type == "cuda" and flat.dtype == torch.float32:   # one pass, no temporaries
+            self.write(0, self.numel, flat)
+            return
         for a in range(0, self.numel, self.INIT_CHUNK):
             b = min(self.numel, a + self.INIT_CHUNK)
             self.write(a, b, flat[a:b])
@@ -276,9 +279,7 @@ class FP24Store(MomentStore):
         return F.fp24_join(self.hi[lo:hi], self.lo[lo:hi])
 
     def write(self, lo, hi, x, seed=None):
-        h, low = F.fp24_split(F.fp24_round(_flat_fp32(x, self.device), seed, lo))
-        self.hi[lo:hi].copy_(h)
-        self.lo[lo:hi].copy_(low)
+        F.fp24_encode(_flat_fp32(x, self.device), seed, lo, out=(self.hi[lo:hi], self.lo[lo:hi]))
 
     def to_fp32(self):
         return self.read(0, self.numel)
@@ -347,8 +348,8 @@ def check_master_state(saved: Any, numel: int, what: str) -> None:
 
 def master_to_fp32(saved: Any, numel: int, device=None) -> torch.Tensor:
     """Validated checkpoint master weights as a flat FP32 tensor on ``device``."""
-    if isinstance(saved, dict) and saved.get("precision") == "fp24":
-        return F.fp24_join(saved["hi"], saved["lo"]).to(device)
+    if isinstance(saved, dict) and saved.get("precision") == "fp24":   # joined where the values go
+        return F.fp24_join(saved["hi"].to(device), saved["lo"].to(device))
     values = saved if isinstance(saved, torch.Tensor) else saved["data"]
     return values.detach().reshape(-1).to(device=device, dtype=torch.float32)
 

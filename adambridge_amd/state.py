@@ -97,6 +97,22 @@ class ParamState:
         """The master weights as a flat FP32 tensor (a copy unless they are stored as one)."""
         raise NotImplementedError
 
+    def master_plane(self) -> _hip.Plane:
+        """Where the master weights lie, as the plane-conversion kernel addresses them
+        (adambridge_plane: the separate arrays, or the master column of the interleaved layout)."""
+        raise NotImplementedError
+
+    def write_weights(self, param: torch.Tensor) -> None:
+        """Write the working weights the masters give (kernels.c:108-112; FP32 parameters take the
+        master's value) into ``param`` on the device's current stream: one pass of the
+        plane-conversion kernel, no temporaries for a contiguous parameter."""
+        dst = param.data
+        flat = dst.view(-1) if dst.is_contiguous() else torch.empty(self.numel, dtype=dst.dtype, device=dst.device)
+        if self.numel:
+            F.convert_plane(self.master_plane(), _hip.plane_of(flat), self.numel, self.device)
+        if flat.data_ptr() != dst.data_ptr() or not dst.is_contiguous():
+            dst.copy_(flat.view(dst.shape))
+
     def moment(self, role: str) -> MomentStore:
         """Moment ``role`` as a store of the reference's API (a copy for interleaved layouts)."""
         raise NotImplementedError
@@ -148,6 +164,23 @@ def _as_master_values(master: Any, numel: int, device) -> torch.Tensor:
     return master_to_fp32(master, numel, device)
 
 
+def _master_source(master: Any, numel: int, device) -> _hip.Plane:
+    """Checkpoint master weights (tensor or store dictionary) or plain values as a device plane the
+    plane-conversion kernel reads: FP24 planes, or the values as float32 / bfloat16 (others are
+    cast to float32), flat and contiguous on ``device``.  Returns the plane and the tensors that
+    hold its memory (to keep alive until the kernel has run)."""
+    if isinstance(master, dict) and master.get("precision") == "fp24":
+        hi = master["hi"].reshape(-1).to(device).contiguous()
+        lo = master["lo"].reshape(-1).to(device).contiguous()
+        return _hip.fp24_plane(hi, lo), (hi, lo)
+    values = master if isinstance(master, torch.Tensor) else master["data"]
+    flat = values.detach().reshape(-1).to(device)
+    if flat.dtype not in (torch.float32, torch.bfloat16):
+        flat = flat.to(torch.float32)
+    flat = flat.contiguous()
+    return _hip.plane_of(flat), (flat,)
+
+
 # ------------------------------------------------------------------- separate
 
 class SeparateState(ParamState):
@@ -178,6 +211,11 @@ class SeparateState(ParamState):
 
     def master_fp32(self):
         return self.master.data if isinstance(self.master, FP32Store) else self.master.to_fp32()
+
+    def master_plane(self):
+        if isinstance(self.master, FP24Store):
+            return _hip.fp24_plane(self.master.hi, self.master.lo)
+        return _hip.plane_of(self.master.data.view(-1))
 
     def export_master(self):
         return self.master.data if isinstance(self.master, FP32Store) else self.master.state_dict()
@@ -268,8 +306,33 @@ class _Interleaved(ParamState):
         flat[: self.numel] = values.reshape(-1)[: self.numel].to(self.device)
         column.copy_(flat.view(column.shape))
 
+    # The master column, the plane-conversion kernel's view of it: (stride in bytes, log2 of the
+    # elements per group) of an FP32 master; the FP24-master and FP8-record layouts override master_plane.
+    PLANE: tuple[int, int] = (0, 0)
+
+    def master_plane(self):
+        stride, log2 = self.PLANE
+        return _hip.Plane(self.current.data_ptr(), None, stride, _hip.DT_F32, log2)
+
+    def _load_master(self, master: Any) -> None:
+        """Checkpoint master weights or plain values into the master column: on the device one pass
+        of the plane-conversion kernel (FP24 rounds to nearest; padding slots keep their bits), in
+        host memory a torch copy."""
+        if self.device.type != "cuda":
+            self._put("p", _as_master_values(master, self.numel, self.device))
+            return
+        src, keep = _master_source(master, self.numel, self.device)   # keep: alive until enqueued
+        if self.numel:
+            F.convert_plane(src, self.master_plane(), self.numel, self.device)
+        del keep   # memory made on this stream and freed to it: reused only after the copy
+
     def master_fp32(self):
-        return self._column("p").reshape(-1)[: self.numel].clone()
+        if self.device.type != "cuda":
+            return self._column("p").reshape(-1)[: self.numel].clone()
+        out = torch.empty(self.numel, dtype=torch.float32, device=self.device)
+        if self.numel:
+            F.convert_plane(self.master_plane(), _hip.plane_of(out), self.numel, self.device)
+        return out
 
     def footprint(self):
         total = sum(b.nbytes for b in self.buffers)
@@ -283,6 +346,7 @@ class PairState(_Interleaved):
 
     layout = "pairs"
     precision = "bf16"
+    PLANE = (16, 1)   # element i's master at 16 (i >> 1) + 4 (i & 1)
 
     def __init__(self, numel, device, double_buffer: bool = False, memory: list[torch.Tensor] | None = None):
         pairs = max(1, (int(numel) + 1) // 2)
@@ -312,7 +376,7 @@ class PairState(_Interleaved):
 
     def load(self, master=None, moments=None):
         if master is not None:
-            self._put("p", _as_master_values(master, self.numel, self.device))
+            self._load_master(master)
         for role, store in (moments or {}).items():
             self._put(role, _bf16_bits(store, self.device))
 
@@ -327,6 +391,7 @@ class LionRecordState(_Interleaved):
 
     layout = "lion-records"
     precision = "bf16"
+    PLANE = (1536, 8)
 
     def __init__(self, numel, device, double_buffer: bool = False, memory: list[torch.Tensor] | None = None):
         records = max(1, -(-int(numel) // 256))
@@ -355,7 +420,7 @@ class LionRecordState(_Interleaved):
 
     def load(self, master=None, moments=None):
         if master is not None:
-            self._put("p", _as_master_values(master, self.numel, self.device))
+            self._load_master(master)
         if moments and "m" in moments:
             self._put("m", _bf16_bits(moments["m"], self.device))
 
@@ -369,6 +434,7 @@ class F32RecordState(_Interleaved):
 
     layout = "f32-records"
     precision = "fp32"
+    PLANE = (3072, 8)
 
     def __init__(self, numel, device, double_buffer: bool = False, memory: list[torch.Tensor] | None = None):
         records = max(1, -(-int(numel) // 256))
@@ -394,7 +460,7 @@ class F32RecordState(_Interleaved):
 
     def load(self, master=None, moments=None):
         if master is not None:
-            self._put("p", _as_master_values(master, self.numel, self.device))
+            self._load_master(master)
         for role, store in (moments or {}).items():
             self._put(role, store.to_fp32().to(self.device))
 
@@ -433,14 +499,26 @@ class F24RecordState(_Interleaved):
         k = {"p": 0, "m": 768, "v": 1280}[role]
         return self.current[:, k:k + 512].view(torch.bfloat16)
 
+    RECORD = 1792
+
+    def master_plane(self):
+        base = self.current.data_ptr()
+        return _hip.Plane(base, base + 512, self.RECORD, _hip.DT_F24, 8)
+
     def _planes(self) -> FP24Store:
         """The master as an FP24 store (a copy of the two planes)."""
         store = FP24Store(self.numel, device=self.device)
+        if self.device.type == "cuda":
+            if self.numel:   # bit for bit: FP24 into FP24
+                F.convert_plane(self.master_plane(), _hip.fp24_plane(store.hi, store.lo), self.numel, self.device)
+            return store
         store.hi.copy_(self._column("p").reshape(-1)[: self.numel])
         store.lo.copy_(self._column("lo").reshape(-1)[: self.numel])
         return store
 
     def master_fp32(self):
+        if self.device.type == "cuda":
+            return super().master_fp32()   # one pass: the record's planes expanded to FP32
         return self._planes().to_fp32()
 
     def export_master(self):
@@ -453,10 +531,13 @@ class F24RecordState(_Interleaved):
 
     def load(self, master=None, moments=None):
         if master is not None:
-            planes = FP24Store(self.numel, device=self.device)
-            load_master_(planes, master)   # FP24 planes as they are; other values rounded to nearest
-            self._put("p", planes.hi)
-            self._put("lo", planes.lo)
+            if self.device.type == "cuda":
+                self._load_master(master)   # FP24 planes bit for bit; other values rounded to nearest
+            else:
+                planes = FP24Store(self.numel, device=self.device)
+                load_master_(planes, master)   # FP24 planes as they are; other values rounded to nearest
+                self._put("p", planes.hi)
+                self._put("lo", planes.lo)
         for role, store in (moments or {}).items():
             self._put(role, _bf16_bits(store, self.device))
 
@@ -475,7 +556,7 @@ class LionF24RecordState(F24RecordState):
     the 256 low bytes and the 256 m values, each in element order (ADAMBRIDGE_DT_PACKED_LION_F24)."""
 
     layout = "lion-f24-records"
-    RECORD = 1280
+    RECORD = 1280   # master_plane's record stride too
 
     def __init__(self, numel, device, double_buffer: bool = False, memory: list[torch.Tensor] | None = None):
         records = max(1, -(-int(numel) // 256))
@@ -528,6 +609,9 @@ class AdamRecordState(_Interleaved):
         k = 0 if role == "m" else 8
         return self.current[:, 512:].view(self.blocks, 16, 16)[:, :, k:k + 8]
 
+    def master_plane(self):
+        return _hip.Plane(self.current.data_ptr(), None, 0, _hip.DT_PACKED8, 0)
+
     def _codes(self, role: str) -> torch.Tensor:
         return self._column(role).reshape(-1).view(F.FP8_FORMATS[role].dtype)
 
@@ -539,7 +623,7 @@ class AdamRecordState(_Interleaved):
 
     def load(self, master=None, moments=None):
         if master is not None:
-            self._put("p", _as_master_values(master, self.numel, self.device))
+            self._load_master(master)
         for role, store in (moments or {}).items():
             if not isinstance(store, FP8Store) or store.role != role or store.block != F.FP8_BLOCK:
                 store = FP8Store(self.numel, role, init=store.to_fp32(), device=self.device)
@@ -650,7 +734,7 @@ def new_states(layout: str, algorithm: str, precision: str, master_precision: st
     states = []
     for n, mem, values in zip(sizes, memory, masters):
         state = cls(n, device, double_buffer, memory=mem)
-        state.load(master=values.detach().reshape(-1).to(device=device, dtype=torch.float32))
+        state.load(master=values.detach().reshape(-1))   # bf16 or fp32, read as it is by the conversion
         states.append(state)
     return states
 

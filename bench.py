@@ -8,8 +8,10 @@ configuration: one kernel launch that reads every gradient, master and moment
 once and writes the master, the moments and the bf16 working weights.  Inputs
 are synthetic and already resident in HBM when the timed region starts (bf16
 weights ~ N(0, 0.02), bf16 gradients ~ N(0, 1) times a per-tensor scale drawn
-log-uniformly; the same gradients every step -- the kernel has no
-data-dependent branches).
+log-uniformly from a seeded generator, the same gradients every step; c1 as
+BASELINE.json specifies it: an FP32 master ~ N(0, 0.02) and a gradient
+~ N(0, 1e-3) regenerated for every step from (seed, step), all made before
+the timed region).
 
 Prints ONE JSON line: ``value`` = parameters updated per second (wall clock
 over the K timed steps, bracketed by device synchronisations); ``roofline``
@@ -82,7 +84,7 @@ def llama7b() -> list[tuple[str, tuple]]:
 CONFIGS = {
     "c1": dict(desc="AdamW, FP32 moments, one flat tensor of 16,777,216 params", shapes=lambda: [("flat", (1 << 24,))],
                algo="adamw", precision="fp32", lr=1e-4, betas=(0.9, 0.999), wd=0.01, gscale=(1e-3, 1e-3),
-               warm_steps=5, rotate=4),
+               warm_steps=5, rotate=4, master_init="fp32", grads_per_step=True),
     "c2": dict(desc="AdamW, bf16 moments, Qwen2.5-0.5B parameter list",
                shapes=lambda: qwen_like(151936, 896, 4864, 24, 128),
                algo="adamw", precision="bf16", lr=2e-5, betas=(0.9, 0.999), wd=0.01, gscale=(1e-5, 1e-2),
@@ -116,23 +118,59 @@ def build(cfg: dict, device, seed: int = 0, layout: str = "auto", double_buffer:
     # step.
     gen = torch.Generator(device=device).manual_seed(seed)
     shapes = [shape for _, shape in cfg["shapes"]()]
-    params = [torch.nn.Parameter(torch.randn(shape, generator=gen, device=device, dtype=torch.bfloat16).mul_(0.02))
-              for shape in shapes]
-    grads = [None] * len(shapes)
-    for k in reversed(range(len(shapes))):
-        grads[k] = synthetic_grad(cfg, k, shapes[k], gen, device)
+    masters = None
+    if cfg.get("master_init") == "fp32":   # c1: an FP32 master ~ N(0, 0.02), the weights its bf16
+        masters = [torch.randn(shape, generator=gen, device=device, dtype=torch.float32).mul_(0.02) for shape in shapes]
+        params = [torch.nn.Parameter(m.to(torch.bfloat16)) for m in masters]
+    else:
+        params = [torch.nn.Parameter(torch.randn(shape, generator=gen, device=device, dtype=torch.bfloat16).mul_(0.02))
+                  for shape in shapes]
+    grads = step_grads(cfg, params, 1, seed)
+    if grads is None:
+        grads = [None] * len(shapes)
+        for k in reversed(range(len(shapes))):
+            grads[k] = synthetic_grad(cfg, k, shapes[k], gen, device, seed)
     kw = dict(lr=cfg["lr"], betas=cfg["betas"], weight_decay=cfg["wd"], precision=cfg["precision"],
               master_precision=cfg.get("master", "fp32"), state_layout=layout, double_buffer=double_buffer)
     opt = ab.LionBridge(params, **kw) if cfg["algo"] == "lion" else ab.AdamBridge(params, **kw)
+    if masters is not None:   # the state built now (lazily it would take the bf16 weights), masters loaded
+        opt._engine.initialize(list(opt._ordered))
+        for slot, m in zip(opt._ordered, masters):
+            slot.state.load(master=m.reshape(-1))
+        del masters
     for p, g in zip(params, grads):
         p.grad = g
     return opt, params
 
 
-def synthetic_grad(cfg: dict, k: int, shape, gen, device):
-    """Tensor k's bf16 gradient.  Default: N(0, 1) times one scale per tensor, log-uniform over
-    cfg['gscale'] (c2, c3).  grads='elementwise' (c4): every element's magnitude log-uniform over
-    cfg['gscale'], a random sign, and exact zeros at density cfg['zeros'] (sign(0) = 0 in Lion)."""
+def step_grads(cfg: dict, params, t: int, seed: int = 0):
+    """The gradients of step ``t`` (1, 2, ...) where a configuration regenerates them every step
+    (cfg['grads_per_step'], c1: N(0, 1e-3) from a generator seeded by (seed, t)); None where the
+    build's gradients serve every step."""
+    if not cfg.get("grads_per_step"):
+        return None
+    import torch
+
+    device = params[0].device
+    gen = torch.Generator(device=device).manual_seed((seed << 32) + t)
+    return [synthetic_grad(cfg, k, tuple(p.shape), gen, device, seed) for k, p in enumerate(params)]
+
+
+def use_step_grads(cfg: dict, params, t: int, seed: int = 0) -> None:
+    """Point the parameters' gradients at step ``t``'s (step_grads) where the configuration regenerates
+    them every step; otherwise leave the build's in place."""
+    grads = step_grads(cfg, params, t, seed)
+    if grads is not None:
+        for p, g in zip(params, grads):
+            p.grad = g
+
+
+def synthetic_grad(cfg: dict, k: int, shape, gen, device, seed: int = 0):
+    """Tensor k's bf16 gradient.  Default: N(0, 1) times one scale per tensor, drawn log-uniformly over
+    cfg['gscale'] from a generator seeded by (seed, k) (c2, c3).  grads='elementwise' (c4): every
+    element's magnitude log-uniform over cfg['gscale'], a random sign, and exact zeros at density
+    cfg['zeros'] (sign(0) = 0 in Lion)."""
+    import numpy as np
     import torch
 
     lo, hi = cfg["gscale"]
@@ -143,7 +181,7 @@ def synthetic_grad(cfg: dict, k: int, shape, gen, device):
         g = torch.where(sign, -g, g)
         g[torch.rand(shape, generator=gen, device=device) < cfg.get("zeros", 0.0)] = 0.0
         return g.to(torch.bfloat16)
-    u = (k * 0.6180339887) % 1.0
+    u = float(np.random.default_rng((seed, k)).random())
     scale = math.exp(math.log(lo) + u * (math.log(hi) - math.log(lo)))
     return torch.randn(shape, generator=gen, device=device, dtype=torch.bfloat16).mul_(scale)
 
@@ -164,8 +202,23 @@ def gpu_bench(cfg: dict, steps: int, warmup: int, layout: str = "auto", double_b
               for k in range(cfg.get("rotate", 1))]
     opts = [opt for opt, _ in copies]
     n = sum(p.numel() for p in copies[0][1])
-    for k in range(warmup * len(opts)):
+    # per-step gradients (c1): made before timing, for every copy's warm-up and timed steps; a step
+    # only points its parameters' .grad at them
+    per_step = {}
+    if cfg.get("grads_per_step"):
+        for k in range(warmup * len(opts) + steps):
+            c, t = k % len(opts), k // len(opts) + 1
+            per_step[k] = step_grads(cfg, copies[c][1], t, seed=c) if t > 1 else [p.grad for p in copies[c][1]]
+
+    def step(k: int) -> None:
+        grads = per_step.get(k)
+        if grads is not None:
+            for p, g in zip(copies[k % len(opts)][1], grads):
+                p.grad = g
         opts[k % len(opts)].step()
+
+    for k in range(warmup * len(opts)):
+        step(k)
     torch.cuda.synchronize()
     log: list = []
     for opt in opts:
@@ -179,7 +232,7 @@ def gpu_bench(cfg: dict, steps: int, warmup: int, layout: str = "auto", double_b
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for k in range(steps):
-            opts[k % len(opts)].step()
+            step(warmup * len(opts) + k)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
     finally:
@@ -277,31 +330,47 @@ def copy_ceiling(total_bytes: float, reps: int = 10) -> dict:
 PIPELINE = dict(layers=24, hidden=2048, inter=8192, batch=8, seq=512, lr=1e-4, wd=0.01)
 
 
-def pipeline_model(device):
-    """24 x [Linear(2048 -> 8192) + GELU + Linear(8192 -> 2048)] with a residual, bf16: 805,552,128
-    parameters (48 weight matrices with a hook each, 48 biases batched at step_sync)."""
+def pipeline_model(device, dtype=None):
+    """24 x [LayerNorm(2048) -> Linear(2048 -> 8192) -> GELU -> Linear(8192 -> 2048)] with a residual,
+    the reference's benchmark block (benchmarks/bench_pipeline.py:20-28), bf16 by default:
+    805,650,432 parameters (48 weight matrices with a hook each; 48 biases and 48 LayerNorm weights
+    and biases batched at step_sync)."""
     import torch
 
     class Block(torch.nn.Module):
         def __init__(self, h, i):
             super().__init__()
+            self.norm = torch.nn.LayerNorm(h)
             self.up = torch.nn.Linear(h, i)
             self.down = torch.nn.Linear(i, h)
 
         def forward(self, x):
-            return x + self.down(torch.nn.functional.gelu(self.up(x)))
+            return x + self.down(torch.nn.functional.gelu(self.up(self.norm(x))))
 
     torch.manual_seed(0)
     c = PIPELINE
     return torch.nn.Sequential(*[Block(c["hidden"], c["inter"]) for _ in range(c["layers"])]).to(
-        device=device, dtype=torch.bfloat16)
+        device=device, dtype=dtype or torch.bfloat16)
 
 
-def pipeline_bench(steps: int, warmup: int) -> dict:
-    """Training-step wall time of the c5 stack with: no optimizer (the floor), torch's fused AdamW,
-    AdamBridge.step() after backward, attach_hooks + step_sync, and attach_hooks + delay_updates;
-    plus, for the hooked runs, the GPU time of the updates and the exposed tail (last gradient ready
-    -> last update done), from the side stream's events."""
+PIPELINE_RUNS = {
+    "floor": "fwd+bwd only",
+    "torch": "torch.optim.AdamW(fused=True), bf16 params and state, no master",
+    "torch-fp32": "torch.optim.AdamW(fused=True), fp32 params + bf16 autocast",
+    "step": "AdamBridge bf16 step()",
+    "hooked": "AdamBridge bf16 attach_hooks + step_sync",
+    "delayed": "AdamBridge bf16 attach_hooks + delay_updates",
+}
+
+
+def pipeline_bench(steps: int, warmup: int, runs=None) -> dict:
+    """Training-step wall time of the c5 stack (reference benchmarks/bench_pipeline.py:58-128) with:
+    no optimizer (the floor), torch's fused AdamW on the bf16 model, torch's fused AdamW on an fp32
+    model under bf16 autocast (the reference's GPU baseline), AdamBridge.step() after backward,
+    attach_hooks + step_sync, and attach_hooks + delay_updates; each with the peak device memory
+    allocated during its steps (bench_pipeline.py:37-50), and, for the hooked runs, the GPU time of
+    the updates and the exposed tail (last gradient ready -> last update done) from the side
+    stream's events.  ``runs``: the keys of PIPELINE_RUNS to time (default: all, in that order)."""
     import statistics
 
     import torch
@@ -319,6 +388,8 @@ def pipeline_bench(steps: int, warmup: int) -> dict:
 
     def timed(step, stats_of=None):
         times, upd, tail, bwd = [], [], [], []
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats(device)
         for i in range(warmup + steps):
             torch.cuda.synchronize()
             t0 = time.perf_counter()
@@ -330,54 +401,66 @@ def pipeline_bench(steps: int, warmup: int) -> dict:
                     upd.append(st.gpu_update or 0.0)
                     tail.append(st.exposed_tail or 0.0)
                     bwd.append(st.gpu_backward or 0.0)
-        out = dict(step_ms=statistics.median(times) * 1e3)
+        out = dict(step_ms=statistics.median(times) * 1e3,
+                   peak_gib=torch.cuda.max_memory_allocated(device) / 2**30)
         if upd:
             out.update(gpu_update_ms=statistics.median(upd) * 1e3, exposed_tail_ms=statistics.median(tail) * 1e3,
                        gpu_backward_ms=statistics.median(bwd) * 1e3)
         return out
 
+    def release():
+        gc.collect()
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+
     results = {}
-    model = pipeline_model(device)
-    n = sum(p.numel() for p in model.parameters())
-
-    def floor():
-        loss_of(model).backward()
-        for p in model.parameters():
-            p.grad = None
-    results["fwd+bwd only"] = timed(floor)
-
-    opt = torch.optim.AdamW(model.parameters(), lr=c["lr"], weight_decay=c["wd"], fused=True)
-
-    def torch_step():
-        loss_of(model).backward()
-        opt.step()
-        opt.zero_grad(set_to_none=True)
-    results["torch.optim.AdamW(fused=True), bf16 state, no master"] = timed(torch_step)
-    del opt
-    torch.cuda.empty_cache()
-
-    for name, hooks, delay in (("AdamBridge bf16 step()", False, False),
-                               ("AdamBridge bf16 attach_hooks + step_sync", True, False),
-                               ("AdamBridge bf16 attach_hooks + delay_updates", True, True)):
-        model = pipeline_model(device)
-        opt = ab.AdamBridge(model.parameters(), lr=c["lr"], weight_decay=c["wd"], precision="bf16",
-                            delay_updates=delay)
-        opt._engine.timing = hooks
-        if hooks:
-            opt.attach_hooks(model)
+    runs = list(PIPELINE_RUNS) if runs is None else list(runs)
+    n = sum(p.numel() for p in pipeline_model("meta").parameters())
+    for key in runs:
+        name = PIPELINE_RUNS[key]
+        print(f"[bench] c5 run: {name}", file=sys.stderr, flush=True)
+        if key == "floor":
+            model = pipeline_model(device)
 
             def step():
                 loss_of(model).backward()
-                return opt.step_sync()
-        else:
+                for p in model.parameters():
+                    p.grad = None
+            results[name] = timed(step)
+            del model
+        elif key in ("torch", "torch-fp32"):
+            fp32 = key == "torch-fp32"
+            model = pipeline_model(device, torch.float32 if fp32 else torch.bfloat16)
+            opt = torch.optim.AdamW(model.parameters(), lr=c["lr"], weight_decay=c["wd"], fused=True)
+
             def step():
-                loss_of(model).backward()
+                with torch.autocast("cuda", dtype=torch.bfloat16, enabled=fp32):
+                    loss_of(model).backward()
                 opt.step()
                 opt.zero_grad(set_to_none=True)
-        results[name] = timed(step)
-        opt.close()
-        del opt, model
-        torch.cuda.empty_cache()
+            results[name] = timed(step)
+            del opt, model
+        else:
+            hooks, delay = key in ("hooked", "delayed"), key == "delayed"
+            model = pipeline_model(device)
+            opt = ab.AdamBridge(model.parameters(), lr=c["lr"], weight_decay=c["wd"], precision="bf16",
+                                delay_updates=delay)
+            opt._engine.timing = hooks
+            if hooks:
+                opt.attach_hooks(model)
+
+                def step():
+                    loss_of(model).backward()
+                    return opt.step_sync()
+            else:
+                def step():
+                    loss_of(model).backward()
+                    opt.step()
+                    opt.zero_grad(set_to_none=True)
+            results[name] = timed(step)
+            opt.close()
+            del opt, model
+        release()
     return dict(params=n, results=results)
 
 
@@ -552,6 +635,8 @@ def main() -> int:
                          "reports the first")
     ap.add_argument("--no-second-build", action="store_true",
                     help="skip timing a second state built while the first is alive (the placement object)")
+    ap.add_argument("--pipeline-runs", default="", metavar="RUNS",
+                    help="c5: comma-separated runs to time, of " + ",".join(PIPELINE_RUNS) + " (default: all)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="first run 3 device-to-device copies of BYTES bytes (a known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -645,16 +730,22 @@ def main() -> int:
 
 def main_pipeline(args) -> int:
     c = PIPELINE
-    print(f"[bench] c5: {c['layers']}-layer bf16 MLP {c['hidden']}->{c['inter']}->{c['hidden']}, "
-          f"{c['batch']}x{c['seq']} tokens; warmup {args.warmup}, steps {args.steps}", file=sys.stderr, flush=True)
-    r = pipeline_bench(args.steps, args.warmup)
+    runs = args.pipeline_runs.split(",") if args.pipeline_runs else list(PIPELINE_RUNS)
+    unknown = [r for r in runs if r not in PIPELINE_RUNS]
+    if unknown:
+        print(f"bench.py: unknown --pipeline-runs {unknown}; expected some of {list(PIPELINE_RUNS)}", file=sys.stderr)
+        return 2
+    print(f"[bench] c5: {c['layers']}-layer bf16 MLP LayerNorm + {c['hidden']}->{c['inter']}->{c['hidden']}, "
+          f"{c['batch']}x{c['seq']} tokens; warmup {args.warmup}, steps {args.steps}; runs {','.join(runs)}",
+          file=sys.stderr, flush=True)
+    r = pipeline_bench(args.steps, args.warmup, runs)
     for name, v in r["results"].items():
-        print(f"[bench] {name:<48} " + ", ".join(f"{k} {x:.2f}" for k, x in v.items()), file=sys.stderr, flush=True)
-    hooked = r["results"]["AdamBridge bf16 attach_hooks + step_sync"]
+        print(f"[bench] {name:<64} " + ", ".join(f"{k} {x:.2f}" for k, x in v.items()), file=sys.stderr, flush=True)
+    main = r["results"].get(PIPELINE_RUNS["hooked"]) or next(iter(r["results"].values()))
     line = {
         "metric": "training step wall time, 24-layer bf16 MLP, hooked bf16-moment AdamW (c5)",
-        "value": hooked["step_ms"], "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": hooked["step_ms"], "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "value": main["step_ms"], "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": main["step_ms"], "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16 model, f32 update", "data": "synthetic (N(0,1) tokens and targets, seed 0)",
         "config": {"workload": "c5 hooked pipeline", "params": r["params"], "tokens": c["batch"] * c["seq"],
                    "bytes_per_param": 20, "runs": r["results"]},

@@ -64,17 +64,18 @@ enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, AD
  * Lion with an FP32 master and a BF16 moment (mv_dtype DT_BF16).  p points at one 1536-byte
  * record per 256 elements, ceil(n/256) records, 16-byte aligned.  The record of elements
  * 256r .. 256r + 255 holds their 256 FP32 masters in element order (bytes 0 .. 1023), then their
- * 256 m values as BF16 bits in element order (bytes 1024 .. 1535).  Slots past n are padding,
- * written back unchanged.  p_lo is NULL (update in place) or a second buffer of the same layout
- * that receives the new state; m, v and the scales are unused.  Same arithmetic, rounding and
+ * 256 m values as BF16 bits in element order (bytes 1024 .. 1535).  p_lo is NULL (update in place)
+ * or a second buffer of the same layout that receives the new state; m, v and the scales are unused.
+ * Slots past n are padding: those up to the end of the last element's group of 4 are written back
+ * unchanged (to p_lo, when given), the rest are neither read nor written.  Same arithmetic, rounding and
  * rounding stream as the separate layout. */
 /* ADAMBRIDGE_DT_PACKED_F32 (p_dtype; no counterpart in the reference): an HBM layout for AdamW
  * with an FP32 master and FP32 moments (mv_dtype DT_F32).  p points at one 3072-byte record per
  * 256 elements, ceil(n/256) records, 16-byte aligned.  The record of elements 256r .. 256r + 255
  * holds their 256 masters (bytes 0 .. 1023), then their 256 m values (1024 .. 2047), then their
- * 256 v values (2048 .. 3071), all FP32 in element order.  Slots past n are padding, written back
- * unchanged.  p_lo is NULL (update in place) or a second buffer of the same layout that receives
- * the new state; m, v and the scales are unused.  Same arithmetic (including the scalar tail's
+ * 256 v values (2048 .. 3071), all FP32 in element order.  p_lo is NULL (update in place) or a
+ * second buffer of the same layout that receives the new state; m, v and the scales are unused.
+ * Padding past n as in DT_PACKED_LION.  Same arithmetic (including the scalar tail's
  * unfused form) as the separate layout. */
 /* ADAMBRIDGE_DT_PACKED_F24 (p_dtype; no counterpart in the reference): an HBM layout for AdamW
  * with an FP24 master and BF16 moments (mv_dtype DT_BF16).  p points at one 1792-byte record per
@@ -82,8 +83,8 @@ enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, AD
  * holds their 256 master high halves (the FP24 hi plane, BF16 bits; bytes 0 .. 511), then their
  * 256 master low bytes (the lo plane; 512 .. 767), then their 256 m values (768 .. 1279), then
  * their 256 v values (1280 .. 1791), the moments as BF16 bits, everything in element order.
- * Slots past n are padding, written back unchanged.  p_lo is NULL (update in place) or a second
- * buffer of the same layout that receives the new state; m, v and the scales are unused.  Same
+ * p_lo is NULL (update in place) or a second buffer of the same layout that receives the new state;
+ * m, v and the scales are unused.  Padding past n as in DT_PACKED_LION.  Same
  * arithmetic, rounding and rounding streams as the separate layout with an FP24 master. */
 /* ADAMBRIDGE_DT_PACKED_LION_F24 (p_dtype; no counterpart in the reference): the same for Lion with an
  * FP24 master and a BF16 moment: one 1280-byte record per 256 elements, the 256 master high halves
@@ -180,6 +181,16 @@ typedef struct adambridge_segment {
 
 /* kernels.c:1493. */
 ADAMBRIDGE_API int adambridge_abi_version(void);
+
+/* What this library adds to the reference's ABI version 5 (kept, so that the reference's binding
+ * loads it), as bits -- no counterpart in the reference, which has none of these: */
+#define ADAMBRIDGE_CAP_PACKED_LAYOUTS 0x01u   /* p_dtype DT_PACKED .. DT_PACKED_LION_F24 (5 .. 10) */
+#define ADAMBRIDGE_CAP_OUT_PREVIOUS   0x02u   /* the segment flag ADAMBRIDGE_SEG_OUT_PREVIOUS */
+#define ADAMBRIDGE_CAP_NOALLOC        0x04u   /* adambridge_multi_step_noalloc */
+#define ADAMBRIDGE_CAP_CONVERT        0x08u   /* adambridge_convert */
+#define ADAMBRIDGE_CAP_CONVERT_PLANE  0x10u   /* adambridge_convert_plane */
+#define ADAMBRIDGE_CAP_STREAM_COPY    0x20u   /* adambridge_stream_copy, adambridge_recycle_device_memory */
+ADAMBRIDGE_API uint32_t adambridge_capabilities(void);
 
 /* kernels.c:1495-1510.  The level whose results are reproduced: its vector
  * body (fused multiply-adds) covers the first n - n mod W elements of every
@@ -290,6 +301,46 @@ ADAMBRIDGE_API int adambridge_plan_launches(adambridge_segment* const* segs, int
  * scales) or _EHIP (launch failure). */
 ADAMBRIDGE_API int adambridge_convert(const void* src, const float* src_scale, int32_t src_dtype, void* dst,
                                       float* dst_scale, int32_t dst_dtype, int64_t n, int32_t role);
+
+/* One plane of values in device memory, for adambridge_convert_plane (no counterpart in the
+ * reference).  Element i of the plane is the value at
+ *     data + (i >> group_log2) * stride + (i mod 2^group_log2) * size,
+ * size being 4 bytes (ADAMBRIDGE_DT_F32) or 2 (ADAMBRIDGE_DT_BF16: BF16 bits; ADAMBRIDGE_DT_F24:
+ * the high half, with the low byte at lo + (i >> group_log2) * stride + (i mod 2^group_log2)).
+ * stride 0: contiguous (group_log2 unused).  ADAMBRIDGE_DT_PACKED_FP8: the FP32 masters of FP8
+ * block records at data (the layout above; stride and group_log2 unused).  The masters of the other
+ * interleaved layouts at a state buffer s are the planes
+ *     DT_PACKED           {s, NULL, 16, DT_F32, 1}       DT_PACKED_LION      {s, NULL, 1536, DT_F32, 8}
+ *     DT_PACKED_F32       {s, NULL, 3072, DT_F32, 8}     DT_PACKED_F24       {s, s + 512, 1792, DT_F24, 8}
+ *     DT_PACKED_LION_F24  {s, s + 512, 1280, DT_F24, 8}
+ * and a separate FP24 master is {hi, lo, 0, DT_F24, 0}.  data is aligned to its value size (16 bytes
+ * for DT_PACKED_FP8) and stride a multiple of it. */
+typedef struct adambridge_plane {
+    void* data;
+    uint8_t* lo;
+    int64_t stride;
+    int32_t dtype;
+    int32_t group_log2;
+} adambridge_plane;
+
+#define ADAMBRIDGE_CONVERT_STOCHASTIC 1
+
+/* No counterpart in the reference; the device form of the FP24 master's conversions
+ * (precision.py:421-480: rounding FP32 values into the planes, expanding them back) and of the
+ * working weight a master gives (kernels.c:108-112).  Copies n values from plane src to plane dst on
+ * the calling thread's stream (asynchronous), converting between the planes' types: a value that
+ * the destination type represents (BF16 into FP24 or FP32, FP24 into FP32, any type into itself) is
+ * copied bit for bit, NaN payloads included; otherwise it is rounded as the kernels round it --
+ * into BF16 to nearest even with a NaN quietened (sign and payload kept), into FP24 to nearest even
+ * on the top 24 bits with a NaN quietened (kernels.c:145-160) -- or, with flags
+ * ADAMBRIDGE_CONVERT_STOCHASTIC, stochastically: element i adds the low 16 (BF16) or 8 (FP24) bits
+ * of lowbias32(uint32(offset + i) ^ seed) before the cut (kernels.c:120-126, 145-150; seed is the
+ * stream's 32-bit seed itself).  src and dst must not overlap unless they are the same plane.
+ * Returns 0, ADAMBRIDGE_EBADN (n < 0, unknown flags, a negative stride or a group_log2 outside
+ * 0 .. 30), _ENULL (a NULL plane, data, or FP24 lo), _EPDTYPE (a type other than those above),
+ * _EALIGN or _EHIP (launch failure). */
+ADAMBRIDGE_API int adambridge_convert_plane(const adambridge_plane* src, const adambridge_plane* dst, int64_t n,
+                                            uint64_t offset, uint32_t seed, int32_t flags);
 
 /* No counterpart in the reference: allocates nbytes of device memory on the current device and
  * frees it at once.  For callers about to allocate a large buffer that the fused update streams

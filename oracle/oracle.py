@@ -84,6 +84,9 @@ def load_oracle() -> ctypes.CDLL:
         lib.abo_bf16_rne.argtypes = [ctypes.c_uint32]
         lib.abo_f24_round.restype = ctypes.c_uint32
         lib.abo_f24_round.argtypes = [ctypes.c_uint32, ctypes.c_int, ctypes.c_uint32]
+        lib.abo_round_values.restype = None
+        lib.abo_round_values.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_uint32, ctypes.c_uint64]
         lib.abo_fp8_decode.restype = ctypes.c_float
         lib.abo_fp8_decode.argtypes = [ctypes.c_uint32, ctypes.c_int]
         lib.abo_fp8_encode.restype = ctypes.c_uint32
@@ -301,6 +304,17 @@ def f24_planes(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
 
 def f24_value(hi: np.ndarray, lo: np.ndarray) -> np.ndarray:
     return ((hi.astype(np.uint32) << 16) | (lo.astype(np.uint32) << 8)).view(np.float32)
+
+
+def round_values(bits: np.ndarray, kind: str, seed: int | None = None, offset: int = 0) -> np.ndarray:
+    """FP32 bit patterns rounded by the C oracle's master / weight rules (abo_round_values): kind 'fp24'
+    -> the FP32 bits the FP24 master stores, 'bf16' -> BF16 codes; stochastic with stream ``seed``
+    (element i at index offset + i), nearest otherwise."""
+    src = np.ascontiguousarray(bits, dtype=np.uint32)
+    out = np.empty_like(src)
+    load_oracle().abo_round_values(src.ctypes.data, out.ctypes.data, src.size, 0 if kind == "fp24" else 1,
+                                   int(seed is not None), 0 if seed is None else seed & 0xFFFFFFFF, offset)
+    return out if kind == "fp24" else out.astype(np.uint16)
 
 
 def fp8_decode_table(role: int) -> np.ndarray:

@@ -188,6 +188,40 @@ def test_convert_argument_codes():
     assert lib.adambridge_convert(p, None, F32, p, None, FP8, 8, 1) == -7
 
 
+def test_convert_plane_argument_codes_and_capabilities():
+    """adambridge_convert_plane's checks of both planes, all made before anything is launched (an
+    empty copy of valid planes returns 0); adambridge_capabilities names what the library adds to
+    the reference's ABI version 5."""
+    lib = _hip.open_library()
+    buf = (ctypes.c_uint8 * 64)()
+    base = ctypes.addressof(buf) + (-ctypes.addressof(buf) % 16)
+    P = _hip.Plane
+    F32, BF16, F24, P8 = _hip.DT_F32, _hip.DT_BF16, _hip.DT_F24, _hip.DT_PACKED8
+
+    def rc(src, dst, n=0, flags=0):
+        return lib.adambridge_convert_plane(ctypes.byref(src), ctypes.byref(dst), n, 0, 0, flags)
+
+    ok = P(base, None, 0, F32, 0)
+    assert rc(ok, ok) == 0
+    assert rc(ok, ok, -1) == -1
+    assert rc(ok, ok, 0, 2) == -1                                   # unknown flag
+    assert lib.adambridge_convert_plane(None, ctypes.byref(ok), 0, 0, 0, 0) == -2
+    assert rc(P(None, None, 0, F32, 0), ok) == -2
+    assert rc(P(base, None, 0, F24, 0), ok) == -2                   # FP24 needs its low bytes
+    assert rc(ok, P(base, None, 0, _hip.DT_FP8, 0)) == -13
+    assert rc(ok, P(base, None, 0, _hip.DT_PACKED, 0)) == -13
+    assert rc(P(base + 2, None, 0, F32, 0), ok) == -14
+    assert rc(P(base + 1, None, 0, BF16, 0), ok) == -14
+    assert rc(P(base + 8, None, 0, P8, 0), ok) == -14               # FP8 records are 16-byte aligned
+    assert rc(P(base, None, 1536, F32, 31), ok) == -1
+    assert rc(P(base, None, -16, F32, 1), ok) == -1
+    assert rc(P(base, None, 18, F32, 1), ok) == -14
+    assert rc(P(base, base + 1, 1792, F24, 8), P(base, None, 16, F32, 1)) == 0
+    caps = lib.adambridge_capabilities()
+    assert caps == sum(_hip.CAPABILITIES.values())
+    assert lib.adambridge_abi_version() == 5
+
+
 def test_pool_threads_without_a_pool():
     """kernels.c:1484: adambridge_pool_threads(NULL) is 1."""
     lib = _hip.open_library()

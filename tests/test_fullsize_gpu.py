@@ -91,8 +91,10 @@ def _sampled_parity(name, warm, tensors, cfg, windows_of, layout) -> None:
     opt, params = bench.build(cfg, dev, layout=layout)
     windows_of = windows_of or windows
     try:
-        for _ in range(warm):
+        for t in range(1, warm + 1):   # c1: the gradient of each step regenerated from (seed, step)
+            bench.use_step_grads(cfg, params, t)
             opt.step()
+        bench.use_step_grads(cfg, params, warm + 1)
         torch.cuda.synchronize()
         if layout == "separate":
             assert all(s.state.layout == "separate" for s in opt._ordered)
@@ -185,8 +187,15 @@ def _every_element(name: str) -> None:
     dev = torch.device("cuda", 0)
     opt, params = bench.build(cfg, dev)
     try:
-        for _ in range(cfg.get("warm_steps", 2)):
+        warm = cfg.get("warm_steps", 2)
+        if cfg.get("master_init") == "fp32":   # c1 starts from an FP32 master ~ N(0, 0.02), not bf16 values
+            m = opt._ordered[0].state.master_fp32()
+            assert torch.any(m != m.to(torch.bfloat16).float()) and abs(float(m.std()) - 0.02) < 1e-3
+            del m
+        for t in range(1, warm + 1):   # c1: the gradient of each step regenerated from (seed, step)
+            bench.use_step_grads(cfg, params, t)
             opt.step()
+        bench.use_step_grads(cfg, params, warm + 1)
         torch.cuda.synchronize()
         if master == "fp24":
             assert all(s.state.layout == "f24-records" for s in opt._ordered)

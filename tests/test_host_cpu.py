@@ -684,3 +684,86 @@ def test_arena_plan_aligns_large_buffers_and_packs_small_ones(layout):
     small = [896] * 1000
     _, total = S.arena_plan(layout, small)
     assert total < 1000 * (cls.buffer_bytes(896) + S.SMALL_ALIGN)
+
+
+def test_launch_points_fire_at_the_start_of_each_hooked_modules_backward():
+    """A hooked update is launched at the next launch point of its backward pass: the hook on the
+    gradient of a hooked module's output fires before that module's parameters get their gradients,
+    so the update of a parameter is launched beside the next module's GEMMs (and not beside the
+    elementwise backward in between).  A forward pass without gradients registers nothing."""
+    from adambridge_amd.optimizer import _LaunchPoints
+
+    events = []
+
+    class Owner:
+        def launch(self):
+            events.append("point")
+
+    owner = Owner()
+    points = _LaunchPoints(owner.launch)
+    model = torch.nn.Sequential(torch.nn.Linear(4, 8), torch.nn.GELU(), torch.nn.Linear(8, 4))
+    points.add([model[0], model[2]])
+    for i, p in enumerate([model[0].weight, model[2].weight]):
+        p.register_post_accumulate_grad_hook(lambda p, i=i: events.append(f"grad{i}"))
+    with torch.no_grad():
+        model(torch.randn(3, 4))
+    assert not points.armed
+    model(torch.randn(3, 4)).sum().backward()
+    assert points.armed
+    assert events == ["point", "grad1", "point", "grad0"]
+    points.clear()
+    points.armed = False
+    events.clear()
+    model(torch.randn(3, 4)).sum().backward()
+    assert not points.armed and events == ["grad1", "grad0"]
+    del owner   # the hooks hold the owner weakly: a dropped owner is not called
+    points.add([model[2]])
+    model(torch.randn(3, 4)).sum().backward()
+    assert events == ["grad1", "grad0"] * 2
+
+
+def test_device_fp24_and_weight_conversions_take_the_plane_kernel(monkeypatch):
+    """For tensors in device memory, the FP24 master's conversions (rounding into the planes, their
+    expansion, a store's writes and reads) and the bf16 working weight of a master are one call of
+    the plane-conversion kernel each -- never the torch integer chain, whose int64 temporaries cost
+    ~33 bytes per element and ~10 dispatches per tensor.  (The device is stood in for: the calls are
+    recorded, the chain's building blocks fail the test if reached.)"""
+    from adambridge_amd import _hip
+
+    calls = []
+    monkeypatch.setattr(F, "_on_device", lambda x: True)
+    monkeypatch.setattr(F, "convert_plane", lambda src, dst, n, device, offset=0, seed=None:
+                        calls.append((src.dtype, dst.dtype, n, offset, seed)))
+
+    def forbidden(*args, **kwargs):
+        raise AssertionError("the torch FP24 / weight chain was called for a device tensor")
+
+    for name in ("_as_u32", "_from_u32", "round_bits_stochastic", "counter_hash"):
+        monkeypatch.setattr(F, name, forbidden)
+    x = torch.randn(1000)
+    hi, lo = F.fp24_encode(x, 7, 128)
+    F.fp24_join(hi, lo)
+    F.fp24_split(x)
+    F.bf16_weight(x)
+    store = P.FP24Store(1000, init=x)
+    store.read(0, 1000)
+    store.write(256, 512, x[:256], seed=5)
+    f32, bf16, f24 = _hip.DT_F32, _hip.DT_BF16, _hip.DT_F24
+    assert calls == [(f32, f24, 1000, 128, 7), (f24, f32, 1000, 0, None), (f32, f24, 1000, 0, None),
+                     (f32, bf16, 1000, 0, None), (f32, f24, 1000, 0, None), (f24, f32, 1000, 0, None),
+                     (f32, f24, 256, 256, 5)]
+
+
+def test_memory_report_keys():
+    """memory_report() has the reference's keys (optimizer.py:496-513) plus ``reserved``; every byte is
+    device memory, so ``gpu_state`` equals ``total`` (the reference reports its host bytes as
+    ``total`` and its GPU-resident state apart)."""
+    import types
+
+    opt = ab.AdamBridge.__new__(ab.AdamBridge)
+    opt._registry = types.SimpleNamespace(ordered=[])
+    opt._engine = types.SimpleNamespace(_reserved={"slot": [torch.zeros(1000, dtype=torch.uint8),
+                                                            torch.zeros(24, dtype=torch.uint8)]})
+    rep = ab.AdamBridge.memory_report(opt)
+    assert set(rep) == {"master", "moments", "staging", "reserved", "total", "gpu_state"}
+    assert rep["reserved"] == 1024 and rep["total"] == 1024 and rep["gpu_state"] == rep["total"]

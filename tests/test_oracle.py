@@ -142,6 +142,38 @@ def test_bf16_rne_matches_torch_cast():
     assert np.array_equal(mine, theirs)
 
 
+def test_round_values_follows_the_pinned_element_rules():
+    """abo_round_values (the whole-array checker of the plane conversion) against the element rules it
+    loops over: FP24 nearest = the top 24 bits to nearest even by integer arithmetic on the bits
+    (ties to an even byte 1, carries into the exponent, NaN quietened), BF16 nearest = torch's cast
+    (finite and infinite values), stochastic = the element's stream bits added before the cut, with
+    the stream index wrapping at 2^32."""
+    rng = np.random.default_rng(11)
+    bits = np.concatenate([rng.integers(0, 1 << 32, 200000, dtype=np.uint64).astype(np.uint32),
+                           np.array([0, 0x80000000, 0x7F7FFFFF, 0x7F800000, 0xFF800000, 0x7FC00001, 0x7F800001,
+                                     0x3F8000FF, 0x3F800180, 0x3F800080, 0x3F80017F, 0x007FFFFF], np.uint32)])
+    exp = (bits >> 23) & 0xFF
+    nan = (exp == 0xFF) & ((bits & 0x7FFFFF) != 0)
+    keep = bits >> 8
+    rnd = (bits & 0xFF) > 0x80
+    tie = (bits & 0xFF) == 0x80
+    up = (rnd | (tie & ((keep & 1) == 1))).astype(np.uint64)
+    near = (((keep.astype(np.uint64) + up) << 8) & 0xFFFFFFFF).astype(np.uint32)
+    near = np.where(nan, bits | 0x00400000, near)
+    assert np.array_equal(O.round_values(bits, "fp24"), near)
+    fin = ~nan
+    theirs = torch.from_numpy(bits[fin].view(np.float32)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.round_values(bits[fin], "bf16"), theirs)
+    lib = O.load_oracle()
+    seed, offset = 0x1234567, (1 << 32) - 5
+    sr24, sr16 = O.round_values(bits[:64], "fp24", seed, offset), O.round_values(bits[:64], "bf16", seed, offset)
+    for i, b in enumerate(bits[:64].tolist()):
+        r = lib.abo_hash32(((offset + i) & 0xFFFFFFFF) ^ seed)
+        if not nan[i]:
+            assert int(sr24[i]) == ((b + (r & 0xFF)) & 0xFFFFFFFF) & 0xFFFFFF00
+        assert int(sr16[i]) == ((b + (r & 0xFFFF)) & 0xFFFFFFFF) >> 16
+
+
 def test_hash_and_seed_constants():
     """lowbias32 (kernels.c:100-106) and the splitmix64 seed chain (kernels.c:774-790), restated in Python."""
     lib = O.load_oracle()

@@ -1,8 +1,8 @@
 """The hooked pipeline at its real size (BASELINE config c5) on the GPU.
 
-The 24-layer bf16 MLP of the pipeline benchmark -- 2048 -> 8192 -> 2048 with
-GELU and biases, 805,552,128 parameters, batch 8 x 512 tokens, MSE to seeded
-targets (reference benchmarks/bench_pipeline.py:22-35, 58-128) -- trained with
+The 24-layer bf16 MLP of the pipeline benchmark -- LayerNorm, 2048 -> 8192 -> 2048
+with GELU and biases, 805,650,432 parameters, batch 8 x 512 tokens, MSE to seeded
+targets (reference benchmarks/bench_pipeline.py:20-35, 58-128) -- trained with
 AdamBridge(precision='bf16').attach_hooks(), with and without delay_updates:
 
 * every element of every parameter's update is bit-exact against the oracle:
@@ -56,7 +56,7 @@ def test_c5_hooked_pipeline_matches_oracle_and_reports_overlap(delay):
     c = bench.PIPELINE
     torch.cuda.set_device(DEV)
     model = bench.pipeline_model(DEV)
-    assert sum(p.numel() for p in model.parameters()) == 805_552_128
+    assert sum(p.numel() for p in model.parameters()) == 805_650_432
     gen = torch.Generator(device=DEV).manual_seed(0)
     x = torch.randn(c["batch"] * c["seq"], c["hidden"], generator=gen, device=DEV, dtype=torch.bfloat16)
     target = torch.randn(x.shape, generator=gen, device=DEV, dtype=torch.bfloat16)
