@@ -309,10 +309,6 @@ __device__ __forceinline__ float sqrt_mid(float x)
     return __builtin_fmaf(r, h, s);
 }
 
-// The fused form of adamw for a lane's 8 elements.  The square roots take sqrt_mid when every
-// new v of the wavefront lies in its range (one uniform branch), sqrtf otherwise.  Returns
-// whether sqrt_mid was taken, i.e. whether every v, and so every sq, of the wavefront is
-// positive and finite.
 // The fused AdamW step of two elements (the pair kernel's body): the same operations as
 // adamw<true> on each, with the square roots of the new second moments taken by sqrt_mid when
 // every one of the wavefront lies in its range (2^-100 <= v < 2^100, a uniform branch), where it
@@ -336,32 +332,6 @@ __device__ __forceinline__ void adamw_pair_fused(float& p0, float& p1, float g0,
     const float d0 = __builtin_fmaf(s0, c.isbc2, c.eps), d1 = __builtin_fmaf(s1, c.isbc2, c.eps);
     p0 = __builtin_fmaf(-c.step, m0 / d0, p0 * c.decay);
     p1 = __builtin_fmaf(-c.step, m1 / d1, p1 * c.decay);
-}
-
-__device__ __forceinline__ bool adamw8_fused(float (&p)[8], const float (&g)[8], float (&m)[8], float (&v)[8],
-                                             const Coef& c, float (&sq)[8])
-{
-    uint32_t worst = 0u;   // largest offset of a v's bits from the range's start (unsigned)
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        m[k] = __builtin_fmaf(c.b1, m[k], c.omb1 * g[k]);
-        v[k] = __builtin_fmaf(c.b2, v[k], c.omb2 * (g[k] * g[k]));
-        worst = __builtin_elementwise_max(worst, fbits(v[k]) - kSqrtMidLo);
-    }
-    const bool mid = __all(worst < kSqrtMidSpan);
-    if (mid) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) sq[k] = sqrt_mid(v[k]);
-    } else {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) sq[k] = __builtin_sqrtf(v[k]);
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const float den = __builtin_fmaf(sq[k], c.isbc2, c.eps);
-        p[k] = __builtin_fmaf(-c.step, m[k] / den, p[k] * c.decay);
-    }
-    return mid;
 }
 
 __device__ __forceinline__ float adamw_sel(float p, float g, float& m, float& v, const Coef& c, bool fused,
@@ -404,6 +374,71 @@ __device__ __forceinline__ float recip_nearest(float s)
     const float y0 = __builtin_amdgcn_rcpf(s);
     const float e = __builtin_fmaf(-s, y0, 1.0f);
     return __builtin_fmaf(e, y0, y0);
+}
+
+// The AdamW step's m / den, correctly rounded, in 6 instructions instead of the general
+// division's 11, where every operand is in range: y = 1/den correctly rounded (recip_nearest),
+// q = m y, and one residual correction q + (m - q den) y (Markstein's theorem, as for the FP8 block
+// quotients).  The range: 2^-60 <= |m| <= 2^60 (quot_m_offset <= kQuotMSpan, one unsigned maximum
+// per lane), and 2^-50 <= den < 2^61, which holds when every v is in sqrt_mid's range (so sqrt(v)
+// lies in [2^-50, 2^50)) and the step's 1 <= inv_sqrt_bc2 <= 2^10 and 0 <= eps <= 2^30 (checked on
+// the host: the segment flag of adamw8_fused's caller).  Then y, q and the quotient are normal
+// (|m / den| in [2^-121, 2^110]) and m - q den, about |m| 2^-24 >= 2^-84, is exact, which the
+// theorem needs.  Zero m lies outside the range: its wavefront divides.
+constexpr uint32_t kQuotMLo = 0x21800000u, kQuotMSpan = (0x5d800000u - 0x21800000u) << 1;   // 2^-60, 2^60
+
+__device__ __forceinline__ uint32_t quot_m_offset(float m) { return (fbits(m) << 1) - (kQuotMLo << 1); }
+
+__device__ __forceinline__ float quot_fast(float m, float den)
+{
+    const float y = recip_nearest(den);
+    const float q = m * y;
+    return __builtin_fmaf(__builtin_fmaf(-q, den, m), y, q);
+}
+
+// The fused form of adamw for a lane's 8 elements.  The square roots take sqrt_mid when every new v
+// of the wavefront lies in its range (one uniform branch), sqrtf otherwise; with ``fastdiv`` (the
+// step's coefficients are in quot_fast's range) and every m of the wavefront in range as well, the
+// quotients m / den take quot_fast.  Returns whether sqrt_mid was taken, i.e. whether every v, and
+// so every sq, of the wavefront is positive and finite.
+__device__ __forceinline__ bool adamw8_fused(float (&p)[8], const float (&g)[8], float (&m)[8], float (&v)[8],
+                                             const Coef& c, float (&sq)[8], bool fastdiv)
+{
+    uint32_t worst = 0u, worst_m = 0u;   // largest offsets of the v's and m's bits from their ranges' starts
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        m[k] = __builtin_fmaf(c.b1, m[k], c.omb1 * g[k]);
+        v[k] = __builtin_fmaf(c.b2, v[k], c.omb2 * (g[k] * g[k]));
+        worst = __builtin_elementwise_max(worst, fbits(v[k]) - kSqrtMidLo);
+    }
+    const bool mid = __all(worst < kSqrtMidSpan);
+    if (mid) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) sq[k] = sqrt_mid(v[k]);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) sq[k] = __builtin_sqrtf(v[k]);
+    }
+    bool fast = false;
+    if (mid && fastdiv) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) worst_m = __builtin_elementwise_max(worst_m, quot_m_offset(m[k]));
+        fast = __all(worst_m <= kQuotMSpan);
+    }
+    if (fast) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float den = __builtin_fmaf(sq[k], c.isbc2, c.eps);
+            p[k] = __builtin_fmaf(-c.step, quot_fast(m[k], den), p[k] * c.decay);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float den = __builtin_fmaf(sq[k], c.isbc2, c.eps);
+            p[k] = __builtin_fmaf(-c.step, m[k] / den, p[k] * c.decay);
+        }
+    }
+    return mid;
 }
 
 __device__ __forceinline__ BlockDiv block_div(float s, float absmax)

@@ -75,12 +75,13 @@ struct DevSeg {
     int64_t tile_begin;  // first tile of this segment in the launch
     uint32_t idx0;       // uint32(offset): element i draws rounding bits at idx0 + i
     uint32_t flags;      // kVec: every pointer allows 16-byte access; kSR: stochastic rounding;
-                         // kPrev: out receives the weight of the master before the update
+                         // kPrev: out receives the weight of the master before the update;
+                         // kFastDiv: the coefficients allow quot_fast (adamw8_fused)
     Coef c;
     uint32_t seed_m, seed_v, seed_p, pad;
 };
 static_assert(sizeof(DevSeg) == 144, "DevSeg layout");
-constexpr uint32_t kVec = 1u, kSR = 2u, kPrev = 4u;
+constexpr uint32_t kVec = 1u, kSR = 2u, kPrev = 4u, kFastDiv = 8u;
 
 struct Launch {
     const DevSeg* table;     // device table when nsegs > kInline
@@ -238,14 +239,33 @@ template <int PT, bool SR>
 __device__ __forceinline__ void store_master8(const DevSeg& s, int64_t i, float (&x)[8], uint32_t idx)
 {
     if constexpr (PT == DT_F24) {
-        uint32_t hi[8], lo[2] = {0u, 0u};
-        const uint32_t head = SR ? hash32_head(idx ^ s.seed_p) : 0u;
+        uint32_t hi[8], lo[2] = {0u, 0u}, r[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+        if constexpr (SR) {
+            const uint32_t head = hash32_head(idx ^ s.seed_p);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) r[k] = hash32_tail(head ^ (uint32_t)k);
+        }
+        // f24_round quietens a NaN; where no lane of the wavefront holds one (a uniform test on
+        // the compares' lane masks), the rounding is the add and the cut alone
+        uint64_t nans = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) nans |= __builtin_amdgcn_ballot_w64(x[k] != x[k]);
+        uint32_t b[8];
+        if (nans == 0) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const uint32_t u = fbits(x[k]);
+                b[k] = (SR ? u + (r[k] & 0xffu) : u + 0x7fu + ((u >> 8) & 1u)) & ~0xffu;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) b[k] = f24_round<SR>(x[k], r[k]);
+        }
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            const uint32_t b = f24_round<SR>(x[k], SR ? hash32_tail(head ^ (uint32_t)k) : 0u);
-            x[k] = bitsf(b);
-            hi[k] = b >> 16;
-            lo[k >> 2] |= ((b >> 8) & 0xffu) << (8 * (k & 3));
+            x[k] = bitsf(b[k]);
+            hi[k] = b[k] >> 16;
+            lo[k >> 2] |= ((b[k] >> 8) & 0xffu) << (8 * (k & 3));
         }
         store8_u16(s.p, i, hi);
         st(reinterpret_cast<u32x2*>(s.p_lo + i), u32x2{lo[0], lo[1]});
@@ -667,7 +687,7 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     const bool lane_fused = FULL || kLion || e0 + 8 <= n_main;
     bool v_pos = false;   // every new v of the wavefront positive and finite (uniform)
     if constexpr (FULL && !kLion) {
-        v_pos = adamw8_fused(p, g, mt, vt, c, sq);
+        v_pos = adamw8_fused(p, g, mt, vt, c, sq, (s.flags & kFastDiv) != 0);
     } else {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
@@ -1757,9 +1777,12 @@ __device__ bool divisions_match(uint32_t u, uint32_t seed)
 {
     const uint32_t h1 = hash32(u ^ seed ^ 0x3c6ef372u), h2 = hash32(h1 ^ 0xa54ff53au);
     const uint32_t h3 = hash32(h2 ^ 0x510e527fu), h4 = hash32(h3 ^ 0x9b05688cu);
-    // m / den: |m| in [2^-60, 2^60], den in [2^-40, 2^40]
-    const float m = random_float(h1, h2, -60, 60, false), den = random_float(h3, h4, -40, 40, true);
+    // m / den: |m| in [2^-60, 2^61), den in [2^-50, 2^61) -- '/' everywhere, quot_fast where the
+    // AdamW kernels take it (|m| <= 2^60, den below 2^61)
+    const float m = random_float(h1, h2, -60, 60, false), den = random_float(h3, h4, -50, 60, true);
     if (!is_nearest_quotient(fbits(m), fbits(den), fbits(m / den))) return false;
+    if (quot_m_offset(m) <= kQuotMSpan && !is_nearest_quotient(fbits(m), fbits(den), fbits(quot_fast(m, den))))
+        return false;
     // block quotient: absmax in [2^-110, 2^60] (all three paths of block_div), |x| <= absmax
     const float amax = random_float(h2, h3, -110, 60, true);
     const bool e5m2 = h4 & 1u;

@@ -648,11 +648,11 @@ def main() -> int:
         return 2
     if args.steps < 1 or args.warmup < 0 or args.rebuilds < 1:
         ap.error("--steps and --rebuilds must be >= 1 and --warmup >= 0")
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy)
     if args.config == "c5":
         return main_pipeline(args)
     cfg = dict(CONFIGS[args.config], master=args.master)
-    if args.calibrate_copy:
-        calibrate_copy(args.calibrate_copy)
     print(f"[bench] config {args.config}: {cfg['desc']}; warmup {args.warmup}, steps {args.steps}",
           file=sys.stderr, flush=True)
     held: list = []

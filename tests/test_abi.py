@@ -276,9 +276,23 @@ def test_launch_plan_batches_by_variant_and_staging_slot():
     chunks = [order[:862], order[862:1600], order[1600:]]
     for (_, entries), ns in zip(sorted(by_launch.items()), chunks):
         assert len({v for v, _, _ in entries}) == 1
-        tiles = [-(-n // 1024) for n in ns]
+        tiles = [-(-n // 512) for n in ns]   # each variant moves fewer than 2^25 elements: 512-element tiles
         assert [f for _, f, _ in entries] == [sum(tiles[:j]) for j in range(len(tiles))]
         assert entries[0][2] == sum(tiles)
+
+
+def test_launch_tile_follows_the_launch_size():
+    """512-element tiles for a launch of at most 2^25 elements of a two- or four-element-per-lane
+    kernel, 1024 above; FP8 launches keep 2048 (one 128-element block per 16-lane group)."""
+    small = 1 << 24
+    for sizes, tile in (([small], 512), ([small, small], 512), ([small, small, 1], 1024), ([3 << 24], 1024)):
+        k, segs, arr = _fake_segments([(n, 0, _hip.DT_PACKED) for n in sizes])
+        rows = k.plan_launches(arr)
+        assert rows[-1][3] == sum(-(-n // tile) for n in sizes), (sizes, tile)
+    k, segs, arr = _fake_segments([(small, 0, _hip.DT_PACKED8)])
+    for s in segs:
+        s.mv_dtype, s.m_scale, s.v_scale = _hip.DT_FP8, 0x40000000, 0x50000000
+    assert k.plan_launches(arr)[0][3] == small // 2048
 
 
 def test_launch_plan_validates_first():

@@ -169,11 +169,12 @@ def _host(t: torch.Tensor) -> np.ndarray:
 CHUNK = 1 << 28   # elements per oracle call
 
 
-@pytest.mark.parametrize("name", ["c1", "c2", "c4", "c3p", "c3", "c3p-fp24"])
+@pytest.mark.parametrize("name", ["c1", "c2", "c4", "c3p", "c3", "c3p-fp24", "c3-fp24"])
 def test_full_size_every_element(name):
     """One step after the configuration's warm-up steps, every element of every tensor against the
     oracle: master (and its low plane), moments, FP8 block scales and the bf16 working weight.
-    'c3p-fp24': the 7B list with an FP24 master (FP24-master records)."""
+    'c3p-fp24': the 7B list with an FP24 master (FP24-master records); 'c3-fp24': FP8 moments with
+    an FP24 master (the reference's separate arrays)."""
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     base = torch.cuda.memory_allocated(dev)
@@ -198,7 +199,8 @@ def _every_element(name: str) -> None:
         bench.use_step_grads(cfg, params, warm + 1)
         torch.cuda.synchronize()
         if master == "fp24":
-            assert all(s.state.layout == "f24-records" for s in opt._ordered)
+            want = "f24-records" if cfg["precision"] == "bf16" else "separate"
+            assert all(s.state.layout == want for s in opt._ordered)
         before = {s.index: {k: v.clone() for k, v in s.state.window(0, s.numel).items()} for s in opt._ordered}
         opt.step()
         torch.cuda.synchronize()
