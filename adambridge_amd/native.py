@@ -26,7 +26,7 @@ from . import _hip
 from . import build as _build
 
 __all__ = ["BuildError", "Group", "Segment", "StepCoefficients", "NativeKernels", "library_path", "cache_dir",
-           "build", "load", "available", "load_error", "main"]
+           "build", "load", "available", "load_error"]
 
 Group = _hip.Group
 Segment = _hip.Segment
@@ -112,38 +112,3 @@ def available() -> bool:
 
 def load_error() -> str | None:
     return _load_error
-
-
-def main(argv: list[str]) -> int:
-    """``python -m adambridge_amd {build,info}`` (reference native.py:472-496): compile the library,
-    or show what the optimizer will use -- the library, what it runs on and which of the
-    reference's SIMD levels its results reproduce.  No host topology: there is no host state."""
-    import argparse
-
-    parser = argparse.ArgumentParser(prog="python -m adambridge_amd")
-    sub = parser.add_subparsers(dest="cmd", required=True)
-    b = sub.add_parser("build", help="compile the HIP library for gfx950")
-    b.add_argument("--force", action="store_true", help="accepted; every build recompiles")
-    b.add_argument("--verbose", action="store_true")
-    sub.add_parser("info", help="show the library, its backend and the GPUs")
-    args = parser.parse_args(argv)
-    if args.cmd == "build":
-        print(build(force=args.force, verbose=args.verbose))
-        return 0
-    kernels = load(build_if_missing=False)
-    if kernels is None:
-        print(f"HIP library unavailable: {load_error() or f'{library_path()} is not built'}")
-        return 1
-    import torch
-
-    print(f"library:  {kernels.path}")
-    print(f"backend:  {kernels.backend} (C ABI {_hip.ABI_VERSION})")
-    print(f"simd:     results of the reference's {kernels.simd_level} level (detected {kernels.detected_simd_level})")
-    count = torch.cuda.device_count()
-    if not count:
-        print("gpus:     none visible")
-    for i in range(count):
-        props = torch.cuda.get_device_properties(i)
-        print(f"gpu {i}:    {props.name} ({getattr(props, 'gcnArchName', '?')}), {props.multi_processor_count} CUs, "
-              f"{props.total_memory / 2**30:.0f} GiB")
-    return 0

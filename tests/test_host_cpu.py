@@ -628,22 +628,6 @@ def test_large_state_arenas_follow_an_allocate_free_of_their_size(monkeypatch):
     assert len(calls) == 2   # the first parameter is its own master: 3000 x 4 bytes fewer, under the minimum
 
 
-def test_command_line_info_reports_the_library():
-    """python -m adambridge_amd info (reference python -m adambridge info, native.py:472-496)."""
-    import subprocess
-    import sys
-    from pathlib import Path
-
-    root = Path(__file__).resolve().parents[1]
-    run = subprocess.run([sys.executable, "-m", "adambridge_amd", "info"], cwd=root, capture_output=True,
-                         text=True, timeout=120)
-    assert run.returncode == 0, run.stderr
-    assert "libadambridge_hip.so" in run.stdout and "backend:  hip/gfx950" in run.stdout
-    usage = subprocess.run([sys.executable, "-m", "adambridge_amd", "nonsense"], cwd=root, capture_output=True,
-                           text=True, timeout=120)
-    assert usage.returncode == 2 and "{build,info}" in usage.stderr
-
-
 def test_layout_choice_for_every_algorithm_precision_and_master():
     """Each (algorithm, moment precision) with an FP32 master of the optimizer's own gets its
     interleaved layout, and AdamW with BF16 moments and an FP24 master its FP24 records; other FP24
