@@ -6,7 +6,19 @@ state of each parameter is a :class:`~adambridge_amd.state.ParamState` in device
 memory and one launch of the fused HIP kernel updates a whole batch of
 parameters in place; what is left to the host is ordering and bookkeeping.
 
-Streams and events take the place of the reference's threads::
+Stream order takes the place of the reference's threads.  By default (``update_stream=
+"current"``) each update is launched on the stream current where it is submitted -- in a
+gradient hook, the stream autograd runs that parameter's backward on -- right after the kernels
+that produced its gradient, and before the rest of the backward pass::
+
+    current stream:  ... dW(i) | update(i) | dX(i-1), dW(i-1) | update(i-1) | ... | step_sync
+                                                          (buffered weights -> parameters, owed
+                                                           delayed weights; nothing to wait for)
+
+An update streams HBM at the rate of a copy, and so do most of the backward kernels beside it;
+run side by side the two share the bandwidth at close to 1:1, and the cross-stream events cost
+the compute stream time of their own, so the in-order launch is the faster one (c5: the step
+0.5-1 ms shorter).  ``update_stream="side"`` keeps the overlapped form::
 
     compute stream        side stream                 write-back stream
     --------------        -----------                 -----------------
@@ -149,12 +161,26 @@ class _Hyper:
 
 
 class _Lanes:
-    """A device's two streams besides the caller's: updates run on ``side``, copies into the parameters
-    (buffered weights, owed delayed updates) on ``wb`` (both at the default priority)."""
+    """A device's two streams besides the caller's, for ``update_stream="side"``: updates run on
+    ``side``, copies into the parameters (buffered weights, owed delayed updates) on ``wb`` (both at
+    the default priority, made at first use)."""
 
     def __init__(self, device: torch.device):
-        self.side = torch.cuda.Stream(device)
-        self.wb = torch.cuda.Stream(device)
+        self.device = device
+        self._side: torch.cuda.Stream | None = None
+        self._wb: torch.cuda.Stream | None = None
+
+    @property
+    def side(self) -> torch.cuda.Stream:
+        if self._side is None:
+            self._side = torch.cuda.Stream(self.device)
+        return self._side
+
+    @property
+    def wb(self) -> torch.cuda.Stream:
+        if self._wb is None:
+            self._wb = torch.cuda.Stream(self.device)
+        return self._wb
 
 
 class UpdateEngine:
@@ -162,9 +188,12 @@ class UpdateEngine:
 
     def __init__(self, *, precision: str, algorithm: str = "adamw", stochastic_rounding: bool = True, seed: int = 0,
                  overlap_writeback: bool = True, timing: bool = False, master_precision: str = "fp32",
-                 delay_capable: bool = False, state_layout: str = "auto", double_buffer: bool = False):
+                 delay_capable: bool = False, state_layout: str = "auto", double_buffer: bool = False,
+                 update_stream: str = "current"):
         if state_layout not in ("auto", "packed", "separate"):
             raise ValueError("state_layout must be 'auto', 'packed' or 'separate'")
+        if update_stream not in ("current", "side"):
+            raise ValueError("update_stream must be 'current' or 'side'")
         if algorithm not in _hip.ALGORITHMS:
             raise ValueError(f"algorithm must be one of {sorted(_hip.ALGORITHMS)}")
         if master_precision not in _hip.MASTER_CODES:
@@ -181,6 +210,7 @@ class UpdateEngine:
         self.delay_capable = delay_capable
         self.state_layout = state_layout
         self.double_buffer = double_buffer
+        self.apart = update_stream == "side"   # updates on a side stream of their own
         self._hyper = _Hyper(seed, stochastic_rounding)
         self._lock = threading.RLock()
         self._lanes: dict[torch.device, _Lanes] = {}
@@ -190,7 +220,8 @@ class UpdateEngine:
         self._num_updates = 0
         self._ready_events: list[torch.cuda.Event] = []
         self._update_events: list[tuple[torch.cuda.Event, torch.cuda.Event]] = []
-        self._used: set[torch.device] = set()
+        # every stream this engine enqueued work on, by device (what the caller's stream must wait for)
+        self._streams: dict[torch.device, dict[int, torch.cuda.Stream]] = {}
         self.launch_log: list | None = None   # a list: (start, end, elements) of every launch, read after a sync
         self.hooked_slots: list[ParamSlot] = []   # the parameters gradient hooks update (set by the optimizer)
         self._reserved: dict[ParamSlot, list[torch.Tensor]] = {}   # arena memory set aside for hooked states
@@ -388,9 +419,9 @@ class UpdateEngine:
             self._launch(device, [slots[i] for i in picks], [grads[i] for i in picks], hooked)
 
     def _launch(self, device: torch.device, slots: list[ParamSlot], grads: list[torch.Tensor], hooked: bool) -> None:
-        lanes = self.lanes(device)
         with torch.cuda.device(device):
             current = torch.cuda.current_stream(device)
+            stream = self.lanes(device).side if self.apart else current
             for slot, g in zip(slots, grads):
                 if g.numel() != slot.numel:
                     raise ValueError(f"gradient of parameter {slot.index} has {g.numel()} elements, "
@@ -398,16 +429,18 @@ class UpdateEngine:
                 if g.device != device:
                     raise ValueError(f"gradient of parameter {slot.index} is on {g.device}, parameter on {device}")
             # A strided gradient is read from a contiguous copy (logical order), made on the compute
-            # stream before `ready` is recorded, so that the update waits for it.
+            # stream before the update is ordered after it.
             grads = [g if g.is_contiguous() else g.contiguous() for g in grads]
             fresh = [s for s in slots if not s.initialized]
             if fresh:   # built on the compute stream, before `ready`; a hook does not wait for the device
                 self.initialize(fresh, place=not hooked)
-            ready = torch.cuda.Event(enable_timing=self.timing)
-            ready.record(current)
-            if self.timing:
-                self._ready_events.append(ready)
-            lanes.side.wait_event(ready)
+            if self.apart or self.timing:
+                ready = torch.cuda.Event(enable_timing=self.timing)
+                ready.record(current)
+                if self.timing:
+                    self._ready_events.append(ready)
+                if self.apart:
+                    stream.wait_event(ready)
             structs: dict[int, _hip.Group] = {}   # each group's hyperparameters, read once per launch
             for slot in slots:
                 slot.step += 1
@@ -422,24 +455,26 @@ class UpdateEngine:
                     if into_out:
                         buffered.append(slot)
                 arr = self.kernels.segment_array(ptrs)
-                self.kernels.set_stream(lanes.side)
+                self.kernels.set_stream(stream)
                 timed = self.timing or self.launch_log is not None
                 start = torch.cuda.Event(enable_timing=True) if timed else None
                 if start is not None:   # right before the launch: the pair brackets the library call only
-                    start.record(lanes.side)
+                    start.record(stream)
                 self.kernels.multi_step(None, arr)
             except BaseException:
                 for slot in slots:   # nothing was enqueued: the library validates and plans before launching
                     slot.step -= 1
                 raise
-            done = torch.cuda.Event(enable_timing=timed)
-            done.record(lanes.side)
+            done = None
+            if self.apart or timed:
+                done = torch.cuda.Event(enable_timing=timed)
+                done.record(stream)
             if self.timing:
                 self._update_events.append((start, done))
             if self.launch_log is not None:
                 self.launch_log.append((start, done, sum(s.numel for s in slots)))
-            for slot in slots:
-                slot.done_ev = done
+            for slot in slots:   # in stream order, what follows on `stream` needs no event
+                slot.done_ev = done if self.apart else None
                 slot.state.advance()
             self._deferred += buffered
             if self.delay:   # each update wrote the weight owed from the slot's last one, and owes its own
@@ -447,17 +482,43 @@ class UpdateEngine:
                     for slot in slots:
                         self._owed.pop(slot, None)
                         self._fresh[slot] = None
-            for g in grads:
-                g.record_stream(lanes.side)
-            self._used.add(device)
+            for g in grads:   # the gradient is released after this; its memory waits for the update
+                g.record_stream(stream)
             with self._lock:
+                self._note(device, stream)
                 self._num_updates += len(slots)
 
+    def _note(self, device: torch.device, stream: torch.cuda.Stream) -> None:
+        self._streams.setdefault(device, {})[stream.cuda_stream] = stream
+
+    def _join(self) -> None:
+        """The caller's current stream, on each device, waits for the work this engine enqueued on any
+        other stream, and stands for all of it from then on."""
+        with self._lock:
+            streams = {d: dict(ss) for d, ss in self._streams.items()}
+        for device, members in streams.items():
+            current = torch.cuda.current_stream(device)
+            for key, s in members.items():
+                if key != current.cuda_stream:
+                    current.wait_stream(s)
+            with self._lock:   # streams noted meanwhile (another thread) stay
+                held = self._streams[device]
+                for key in members:
+                    held.pop(key, None)
+                held[current.cuda_stream] = current
+
     def _write_back(self, device: torch.device, slots: list[ParamSlot], ready: torch.cuda.Event | None
-                    ) -> torch.cuda.Event:
-        """Copy the slots' finished updates from ``out`` into the parameters on the write-back stream,
-        after ``ready`` (the compute stream so far) and each slot's latest update; returns the event of
-        the copies."""
+                    ) -> torch.cuda.Event | None:
+        """Copy the slots' finished updates from ``out`` into the parameters: on the current stream
+        after the updates (already ordered there), or with ``update_stream="side"`` on the write-back
+        stream after ``ready`` (the compute stream so far) and each slot's latest update; returns the
+        event of the copies on the write-back stream (None on the current stream)."""
+        if not self.apart:
+            with torch.cuda.device(device), torch.no_grad():
+                torch._foreach_copy_([s.param.data for s in slots], [s.out_view for s in slots])
+                with self._lock:
+                    self._note(device, torch.cuda.current_stream(device))
+            return None
         lanes = self.lanes(device)
         if ready is None:
             ready = torch.cuda.Event()
@@ -469,6 +530,8 @@ class UpdateEngine:
             torch._foreach_copy_([s.param.data for s in slots], [s.out_view for s in slots])
         written = torch.cuda.Event()
         written.record(lanes.wb)
+        with self._lock:
+            self._note(device, lanes.wb)
         return written
 
     def _write_back_all(self, slots: list[ParamSlot]) -> None:
@@ -481,14 +544,22 @@ class UpdateEngine:
 
     def _weights_from_masters(self, slots: list[ParamSlot]) -> None:
         """Write each slot's newest weight -- its master in the parameter's dtype, as the kernels round
-        it -- into the parameter, on the write-back stream after the compute stream so far (which may
-        still read the old weights) and the slot's latest update.  For delayed updates owed to
-        parameters that their next update will not reach in time."""
+        it -- into the parameter, after the work so far on the current stream (which may still read
+        the old weights) and the slot's latest update: on the current stream itself, or with
+        ``update_stream="side"`` on the write-back stream.  For delayed updates owed to parameters
+        that their next update will not reach in time."""
         by_device: dict[torch.device, list[ParamSlot]] = {}
         for slot in slots:
             if slot.state is not None and not slot.state.master_is_param:
                 by_device.setdefault(slot.param.device, []).append(slot)
         for device, members in by_device.items():
+            if not self.apart:
+                with torch.cuda.device(device), torch.no_grad():
+                    for slot in members:   # one conversion pass each, straight into the parameter
+                        slot.state.write_weights(slot.param)
+                    with self._lock:
+                        self._note(device, torch.cuda.current_stream(device))
+                continue
             lanes = self.lanes(device)
             with torch.cuda.device(device):
                 ready = torch.cuda.Event()
@@ -499,7 +570,8 @@ class UpdateEngine:
                 with torch.cuda.stream(lanes.wb), torch.no_grad():
                     for slot in members:   # one conversion pass each, straight into the parameter
                         slot.state.write_weights(slot.param)
-            self._used.add(device)
+            with self._lock:
+                self._note(device, lanes.wb)
 
     # ---------------------------------------------------------- synchronizing
 
@@ -510,14 +582,12 @@ class UpdateEngine:
         t0 = time.perf_counter()
         with self._lock:   # owed updates whose parameters got no gradient this step: written now
             left, self._owed, self._fresh = list(self._owed), self._fresh, {}
+        if not self.apart:
+            self._join()   # updates submitted on other streams (hooks on another stream), before the copies
         self._weights_from_masters(left)
         deferred, self._deferred = self._deferred, []
         self._write_back_all(deferred)
-        for device in self._used:   # the updates write the parameters, delayed ones too
-            lanes = self.lanes(device)
-            current = torch.cuda.current_stream(device)
-            current.wait_stream(lanes.wb)
-            current.wait_stream(lanes.side)
+        self._join()   # the updates write the parameters, delayed ones too
         stats = StepStats(stall=time.perf_counter() - t0)
         with self._lock:
             stats.num_updates, self._num_updates = self._num_updates, 0
@@ -540,25 +610,23 @@ class UpdateEngine:
 
     def wait(self) -> None:
         """Block the host until every enqueued update and write-back has run."""
-        for device in list(self._used):
-            lanes = self.lanes(device)
-            lanes.side.synchronize()
-            lanes.wb.synchronize()
+        with self._lock:
+            streams = [s for ss in self._streams.values() for s in ss.values()]
+        for s in streams:
+            s.synchronize()
 
     def flush(self) -> None:
         """Write every pending delayed update into its parameter and order all of it before the caller's
         next work, which then sees the weights an exact optimizer would have produced."""
+        if not self.apart:
+            self._join()   # updates submitted on other streams, before the copies
         deferred, self._deferred = self._deferred, []
         self._write_back_all(deferred)
         with self._lock:
             pending = list({**self._owed, **self._fresh})
             self._owed, self._fresh = {}, {}
         self._weights_from_masters(pending)
-        for device in self._used:
-            lanes = self.lanes(device)
-            current = torch.cuda.current_stream(device)
-            current.wait_stream(lanes.side)
-            current.wait_stream(lanes.wb)
+        self._join()
 
     def discard_pending(self) -> None:
         """Wait for enqueued updates and forget those not yet written into the parameters."""

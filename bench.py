@@ -360,6 +360,8 @@ PIPELINE_RUNS = {
     "step": "AdamBridge bf16 step()",
     "hooked": "AdamBridge bf16 attach_hooks + step_sync",
     "delayed": "AdamBridge bf16 attach_hooks + delay_updates",
+    "step-side": "AdamBridge bf16 step(), update_stream='side'",
+    "hooked-side": "AdamBridge bf16 attach_hooks + step_sync, update_stream='side'",
 }
 
 
@@ -369,8 +371,11 @@ def pipeline_bench(steps: int, warmup: int, runs=None) -> dict:
     model under bf16 autocast (the reference's GPU baseline), AdamBridge.step() after backward,
     attach_hooks + step_sync, and attach_hooks + delay_updates; each with the peak device memory
     allocated during its steps (bench_pipeline.py:37-50), and, for the hooked runs, the GPU time of
-    the updates and the exposed tail (last gradient ready -> last update done) from the side
-    stream's events.  ``runs``: the keys of PIPELINE_RUNS to time (default: all, in that order)."""
+    the updates and the exposed tail (last gradient ready -> last update done) from the optimizer's
+    timing events, taken over 3 more steps after the timed ones (the timed steps run without those
+    events, as the optimizer does by default).  The AdamBridge runs take the default in-order
+    updates on the current stream; the "-side" runs put them on a side stream.  ``runs``: the keys
+    of PIPELINE_RUNS to time (default: all, in that order)."""
     import statistics
 
     import torch
@@ -386,23 +391,28 @@ def pipeline_bench(steps: int, warmup: int, runs=None) -> dict:
     def loss_of(model):
         return torch.nn.functional.mse_loss(model(x).float(), target.float())
 
-    def timed(step, stats_of=None):
+    def timed(step, engine=None):
         times, upd, tail, bwd = [], [], [], []
         torch.cuda.synchronize()
         torch.cuda.reset_peak_memory_stats(device)
         for i in range(warmup + steps):
             torch.cuda.synchronize()
             t0 = time.perf_counter()
-            st = step()
+            step()
             torch.cuda.synchronize()
             if i >= warmup:
                 times.append(time.perf_counter() - t0)
-                if st is not None:
-                    upd.append(st.gpu_update or 0.0)
-                    tail.append(st.exposed_tail or 0.0)
-                    bwd.append(st.gpu_backward or 0.0)
         out = dict(step_ms=statistics.median(times) * 1e3,
                    peak_gib=torch.cuda.max_memory_allocated(device) / 2**30)
+        if engine is not None:   # the update's GPU span and exposed tail, from the timing events
+            engine.timing = True
+            for _ in range(3):
+                st = step()
+                torch.cuda.synchronize()
+                upd.append(st.gpu_update or 0.0)
+                tail.append(st.exposed_tail or 0.0)
+                bwd.append(st.gpu_backward or 0.0)
+            engine.timing = False
         if upd:
             out.update(gpu_update_ms=statistics.median(upd) * 1e3, exposed_tail_ms=statistics.median(tail) * 1e3,
                        gpu_backward_ms=statistics.median(bwd) * 1e3)
@@ -441,11 +451,10 @@ def pipeline_bench(steps: int, warmup: int, runs=None) -> dict:
             results[name] = timed(step)
             del opt, model
         else:
-            hooks, delay = key in ("hooked", "delayed"), key == "delayed"
+            hooks, delay = key in ("hooked", "delayed", "hooked-side"), key == "delayed"
             model = pipeline_model(device)
             opt = ab.AdamBridge(model.parameters(), lr=c["lr"], weight_decay=c["wd"], precision="bf16",
-                                delay_updates=delay)
-            opt._engine.timing = hooks
+                                delay_updates=delay, update_stream="side" if key.endswith("-side") else "current")
             if hooks:
                 opt.attach_hooks(model)
 
@@ -457,7 +466,7 @@ def pipeline_bench(steps: int, warmup: int, runs=None) -> dict:
                     loss_of(model).backward()
                     opt.step()
                     opt.zero_grad(set_to_none=True)
-            results[name] = timed(step)
+            results[name] = timed(step, opt._engine if hooks else None)
             opt.close()
             del opt, model
         release()

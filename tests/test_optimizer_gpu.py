@@ -784,6 +784,99 @@ def test_hooks_match_step():
     opt_b.close()
 
 
+@pytest.mark.parametrize("delay", [False, True])
+@pytest.mark.parametrize("overlap", [True, False])
+def test_update_streams_give_the_same_bytes(delay, overlap):
+    """Updates in order on the current stream (the default) and on a side stream give the same bytes
+    as plain step() calls, hooked or not, with buffered write-backs (overlap_writeback=False) and
+    delayed updates, and the next forward pass reads the new weights without a host wait."""
+    torch.manual_seed(0)
+    base = TinyLM(layers=2).to(DEV).to(torch.bfloat16)
+    models = {k: copy.deepcopy(base) for k in ("ref", "current", "side", "current-step", "side-step")}
+    kw = dict(lr=3e-3, weight_decay=0.01, precision="bf16", small_param_threshold=2000, delay_updates=delay,
+              overlap_writeback=overlap)
+    opts = {k: ab.AdamBridge(m.parameters(), update_stream=k.split("-")[0] if k != "ref" else "current", **kw)
+            for k, m in models.items()}
+    for k in ("current", "side"):
+        opts[k].attach_hooks(models[k])
+    assert opts["side"]._points._handles and not opts["current"]._points._handles
+    losses = {k: [] for k in models}
+    for step in range(5):
+        for k, m in models.items():
+            loss = lm_loss(m, step)
+            losses[k].append(loss.detach())
+            loss.backward()
+            if k in ("current", "side"):
+                opts[k].step_sync()
+            else:
+                opts[k].step()
+                opts[k].zero_grad(set_to_none=True)
+    for k in models:
+        opts[k].flush()
+    torch.cuda.synchronize()
+    for k, m in models.items():
+        assert all(torch.equal(a, b) for a, b in zip(models["ref"].parameters(), m.parameters())), k
+        assert all(torch.equal(a, b) for a, b in zip(losses["ref"], losses[k])), k
+    for opt in opts.values():
+        opt.close()
+
+
+class _TwoStreamMLP(torch.nn.Module):
+    """A model whose first layer runs on a stream of its own: its backward, and so its gradient
+    hooks, run there too (autograd runs each backward op on its forward op's stream)."""
+
+    stream: torch.cuda.Stream   # set after the copies (a stream is not copyable)
+
+    def __init__(self):
+        super().__init__()
+        self.a = torch.nn.Linear(48, 256)
+        self.b = torch.nn.Linear(256, 48)
+
+    def forward(self, x):
+        self.stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(self.stream):
+            h = torch.nn.functional.gelu(self.a(x))
+        torch.cuda.current_stream().wait_stream(self.stream)
+        h.record_stream(torch.cuda.current_stream())
+        return self.b(h)
+
+
+def test_hooks_on_another_stream_are_ordered_before_step_sync():
+    """A gradient hook that fires on another stream enqueues its in-order update there; step_sync() on
+    the default stream orders it before the work that follows, and the results equal step()'s."""
+    torch.manual_seed(0)
+    other = torch.cuda.Stream()
+    base = _TwoStreamMLP().to(DEV).to(torch.bfloat16)
+    ref_model, model = copy.deepcopy(base), copy.deepcopy(base)
+    ref_model.stream = model.stream = other
+    kw = dict(lr=3e-3, precision="bf16", small_param_threshold=0)
+    ref = ab.AdamBridge(ref_model.parameters(), **kw)
+    opt = ab.AdamBridge(model.parameters(), **kw).attach_hooks(model)
+    seen = []
+    model.a.weight.register_post_accumulate_grad_hook(
+        lambda p: seen.append(torch.cuda.current_stream().cuda_stream))
+    for step in range(4):
+        x = torch.randn(64, 48, device=DEV, generator=torch.Generator(device=DEV).manual_seed(step),
+                        dtype=torch.bfloat16)
+        ref_model(x).float().pow(2).mean().backward()
+        ref.step()
+        ref.zero_grad(set_to_none=True)
+        model(x).float().pow(2).mean().backward()
+        opt.step_sync()   # on the default stream
+        snap = [p.detach().clone() for p in model.parameters()]   # read on the default stream at once
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(ref_model.parameters(), snap)), f"step {step}"
+    assert seen and all(s == other.cuda_stream for s in seen)   # the hook did fire on the other stream
+    ref.close()
+    opt.close()
+
+
+def test_update_stream_is_validated():
+    p = torch.nn.Parameter(torch.zeros(4, device=DEV))
+    with pytest.raises(ValueError, match="update_stream"):
+        ab.AdamBridge([p], update_stream="other")
+
+
 def test_errors_surface_in_step():
     """reference test_optimizer.py:217-224: a bad group fails the step with a RuntimeError."""
     model = tiny_mlp(device=DEV)

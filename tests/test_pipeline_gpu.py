@@ -3,7 +3,8 @@
 The 24-layer bf16 MLP of the pipeline benchmark -- LayerNorm, 2048 -> 8192 -> 2048
 with GELU and biases, 805,650,432 parameters, batch 8 x 512 tokens, MSE to seeded
 targets (reference benchmarks/bench_pipeline.py:20-35, 58-128) -- trained with
-AdamBridge(precision='bf16').attach_hooks(), with and without delay_updates:
+AdamBridge(precision='bf16').attach_hooks(), with and without delay_updates, with the
+updates in order on the compute stream (the default) and on a side stream:
 
 * every element of every parameter's update is bit-exact against the oracle:
   the state before the step and the gradient the hook saw go through the
@@ -51,8 +52,8 @@ def _state_arrays(slot, lo: int, hi: int) -> dict:
     return {k: _bits(v) for k, v in slot.state.window(lo, hi).items()}
 
 
-@pytest.mark.parametrize("delay", [False, True])
-def test_c5_hooked_pipeline_matches_oracle_and_reports_overlap(delay):
+@pytest.mark.parametrize("stream,delay", [("current", False), ("current", True), ("side", False)])
+def test_c5_hooked_pipeline_matches_oracle_and_reports_overlap(stream, delay):
     c = bench.PIPELINE
     torch.cuda.set_device(DEV)
     model = bench.pipeline_model(DEV)
@@ -73,7 +74,7 @@ def test_c5_hooked_pipeline_matches_oracle_and_reports_overlap(delay):
     for p in params:
         p.register_post_accumulate_grad_hook(capture)
     opt = ab.AdamBridge(params, lr=c["lr"], weight_decay=c["wd"], precision="bf16", delay_updates=delay,
-                        autotune=True)   # autotune: StepStats timing on (nothing is tuned on the GPU)
+                        autotune=True, update_stream=stream)   # autotune: StepStats timing on
     opt.attach_hooks(model)
     group = opt.param_groups[0]
     ogroup = {"lr": group["lr"], "beta1": group["betas"][0], "beta2": group["betas"][1], "eps": group["eps"],
@@ -115,7 +116,7 @@ def test_c5_hooked_pipeline_matches_oracle_and_reports_overlap(delay):
                 got = _state_arrays(slot, lo, hi)
                 for key in ("p", "m", "v"):
                     assert np.array_equal(got[key].view(np.uint8), w.arrays[key].view(np.uint8)), \
-                        f"delay={delay} step {step}: parameter {slot.index} [{lo}, {hi}) {key}"
+                        f"{stream} delay={delay} step {step}: parameter {slot.index} [{lo}, {hi}) {key}"
                 weight = _bits(slot.param.reshape(-1)[lo:hi])
                 if not delay:
                     assert np.array_equal(weight, w.arrays["out"]), f"parameter {slot.index} weights"
