@@ -400,9 +400,12 @@ __device__ __forceinline__ float quot_fast(float m, float den)
 // of the wavefront lies in its range (one uniform branch), sqrtf otherwise; with ``fastdiv`` (the
 // step's coefficients are in quot_fast's range) and every m of the wavefront in range as well, the
 // quotients m / den take quot_fast.  Returns whether sqrt_mid was taken, i.e. whether every v, and
-// so every sq, of the wavefront is positive and finite.
+// so every sq, of the wavefront is positive and finite; m_plain receives whether quot_fast was
+// taken, i.e. whether every new m of the wavefront is finite with 2^-60 <= |m| <= 2^60, and m_low
+// then the smallest quot_m_offset of the lane's new m (its smallest |m|, in an order-keeping form).
 __device__ __forceinline__ bool adamw8_fused(float (&p)[8], const float (&g)[8], float (&m)[8], float (&v)[8],
-                                             const Coef& c, float (&sq)[8], bool fastdiv)
+                                             const Coef& c, float (&sq)[8], bool fastdiv, bool& m_plain,
+                                             uint32_t& m_low)
 {
     uint32_t worst = 0u, worst_m = 0u;   // largest offsets of the v's and m's bits from their ranges' starts
 #pragma unroll
@@ -420,9 +423,14 @@ __device__ __forceinline__ bool adamw8_fused(float (&p)[8], const float (&g)[8],
         for (int k = 0; k < 8; ++k) sq[k] = __builtin_sqrtf(v[k]);
     }
     bool fast = false;
+    uint32_t low_m = 0xffffffffu;
     if (mid && fastdiv) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) worst_m = __builtin_elementwise_max(worst_m, quot_m_offset(m[k]));
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t o = quot_m_offset(m[k]);
+            worst_m = __builtin_elementwise_max(worst_m, o);
+            low_m = __builtin_elementwise_min(low_m, o);
+        }
         fast = __all(worst_m <= kQuotMSpan);
     }
     if (fast) {
@@ -438,6 +446,8 @@ __device__ __forceinline__ bool adamw8_fused(float (&p)[8], const float (&g)[8],
             p[k] = __builtin_fmaf(-c.step, m[k] / den, p[k] * c.decay);
         }
     }
+    m_plain = fast;
+    m_low = low_m;
     return mid;
 }
 
@@ -452,19 +462,21 @@ __device__ __forceinline__ BlockDiv block_div(float s, float absmax)
     return d;
 }
 
-// SCALED: the block was scaled by d.pre (absmax < 2^-40).  NONNEG: x is never -0 or NaN (the
-// sqrt-domain v), so the corrected quotient needs no care for signs: with r == 0 the correction
-// q + 0*y returns q, only turning -0 into +0, and a NaN x (only possible for m) must keep its
-// sign.  Otherwise x's sign bit is copied into the result, which is exact for every other x
-// (the quotient has x's sign) and gives -0 / NaN the sign the reference's division gives them.
-template <bool SCALED, bool NONNEG>
+// SCALED: the block was scaled by d.pre (absmax < 2^-40).  PLAIN: x is never -0, and a NaN x
+// needs no sign (the sqrt-domain v, whose NaNs the encoder replaces by 0; m wherever the AdamW
+// step took quot_fast, i.e. every m of the wavefront is finite and nonzero), so the corrected
+// quotient needs no care for signs: it is the correctly rounded quotient, with x's sign, for every
+// other x; only -0 would come out as +0 (q + 0*y), and a NaN without x's sign.  Otherwise x's sign
+// bit is copied into the result, which is exact for every other x (the quotient has x's sign) and
+// gives -0 / NaN the sign the reference's division gives them.
+template <bool SCALED, bool PLAIN>
 __device__ __forceinline__ float block_quot_fast(float x, const BlockDiv& d)
 {
     const float xs = SCALED ? x * d.pre : x;
     const float q = xs * d.y;
     const float r = __builtin_fmaf(-q, d.s2, xs);
     const float qc = __builtin_fmaf(r, d.y, q);
-    if constexpr (NONNEG) return qc;
+    if constexpr (PLAIN) return qc;
     return bitsf(fbits(qc) | (fbits(x) & 0x80000000u));
 }
 

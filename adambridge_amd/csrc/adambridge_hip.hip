@@ -151,12 +151,32 @@ __device__ __forceinline__ T ld(const T* p) { return __builtin_nontemporal_load(
 template <typename T>
 __device__ __forceinline__ void st(T* p, T v) { __builtin_nontemporal_store(v, (ABH_GLOBAL T*)p); }
 
-// 8 consecutive values as FP32, from BF16 bits or FP32, 16-byte aligned.
+// A lane's address: a uniform byte offset from a buffer plus a 32-bit per-lane offset.  The
+// uniform part stays in scalar registers and the access takes the global instructions' scalar-base
+// form (one 32-bit vector offset), with no 64-bit address arithmetic per lane.
+template <typename T>
+__device__ __forceinline__ T* lane_ptr(const void* base, int64_t ubytes, uint32_t lane)
+{
+    char* const u = static_cast<char*>(const_cast<void*>(base)) + ubytes;
+    return reinterpret_cast<T*>(u + lane);
+}
+
+// The same 32-bit lane offset as a new value: an address formed from it is formed where it is
+// used.  Instruction selection sees one basic block at a time, so an address computed before a
+// branch and used after it reaches the store as a 64-bit vector value, which loses the
+// scalar-base form.
+__device__ __forceinline__ uint32_t fresh(uint32_t x)
+{
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
+// 8 consecutive values at p as FP32, from BF16 bits or FP32, 16-byte aligned.
 template <int DT>
-__device__ __forceinline__ void load8(const void* base, int64_t i, float (&x)[8])
+__device__ __forceinline__ void load8(const void* p, float (&x)[8])
 {
     if constexpr (DT == DT_BF16) {
-        const u32x4 w = ld(reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + i));
+        const u32x4 w = ld(static_cast<const u32x4*>(p));
         const uint32_t u[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -168,24 +188,18 @@ __device__ __forceinline__ void load8(const void* base, int64_t i, float (&x)[8]
         // line it touches.  Ordinary (cached) loads let the second find the line the first brought
         // into L2; non-temporal ones fetched most lines twice (measured: 1.39x the FP8 kernel's
         // algorithmic reads, 8% slower).
-        const f32x4* q = reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + i);
+        const f32x4* q = static_cast<const f32x4*>(p);
         const f32x4 a = *(const ABH_GLOBAL f32x4*)q, b = *(const ABH_GLOBAL f32x4*)(q + 1);
         x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
         x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
     }
 }
 
-__device__ __forceinline__ void store8_f32(void* base, int64_t i, const float (&x)[8])
+__device__ __forceinline__ void store8_f32(void* p, const float (&x)[8])
 {
-    f32x4* q = reinterpret_cast<f32x4*>(static_cast<float*>(base) + i);
+    f32x4* q = static_cast<f32x4*>(p);
     st(q, f32x4{x[0], x[1], x[2], x[3]});
     st(q + 1, f32x4{x[4], x[5], x[6], x[7]});
-}
-
-__device__ __forceinline__ void store8_u16(void* base, int64_t i, const uint32_t (&h)[8])
-{
-    const u32x4 w = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
-    st(reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + i), w);
 }
 
 // Master: FP32, or FP24 = hi plane (BF16 bits) << 16 | lo plane << 8.
@@ -202,18 +216,14 @@ __device__ __forceinline__ int64_t record_master_offset(int64_t i)
     return (i >> 7) * kRecordBytes + ((i & 4) ? 256 : 0) + ((i >> 3) & 15) * 16 + (i & 3) * 4;
 }
 
-// Byte offset of the codes of elements i .. i + 7 (i % 8 == 0): m codes, then v codes 8 bytes on.
-__device__ __forceinline__ int64_t record_codes_offset(int64_t i)
-{
-    return (i >> 7) * kRecordBytes + 512 + ((i >> 3) & 15) * 16;
-}
-
+// The masters of 8 consecutive elements: the FP24 planes at p (high halves) and lo (low bytes),
+// a record's two 16-byte halves at p and p + 256 (DT_PACKED8), or FP32 at p.
 template <int PT>
-__device__ __forceinline__ void load_master8(const DevSeg& s, int64_t i, float (&x)[8])
+__device__ __forceinline__ void load_master8(const void* p, const uint8_t* lo, float (&x)[8])
 {
     if constexpr (PT == DT_F24) {
-        const u32x4 h = ld(reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(s.p) + i));
-        const u32x2 l = ld(reinterpret_cast<const u32x2*>(s.p_lo + i));
+        const u32x4 h = ld(static_cast<const u32x4*>(p));
+        const u32x2 l = ld(reinterpret_cast<const u32x2*>(lo));
         const uint32_t hu[4] = {h.x, h.y, h.z, h.w};
         const uint32_t lu[2] = {l.x, l.y};
 #pragma unroll
@@ -223,84 +233,69 @@ __device__ __forceinline__ void load_master8(const DevSeg& s, int64_t i, float (
             x[k] = bitsf((hi16 << 16) | (lo8 << 8));
         }
     } else if constexpr (PT == DT_PACKED8) {
-        const uint8_t* r = static_cast<const uint8_t*>(s.p) + record_master_offset(i);
+        const uint8_t* r = static_cast<const uint8_t*>(p);
         const f32x4 a = ld(reinterpret_cast<const f32x4*>(r)), b = ld(reinterpret_cast<const f32x4*>(r + 256));
         x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
         x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
     } else {
-        load8<DT_F32>(s.p, i, x);
+        load8<DT_F32>(p, x);
     }
 }
 
-// Rounds and stores 8 new master values; x becomes the values stored.  idx % 8 == 0 (the FP8
-// kernel's lanes start at multiples of 8 within segments that start at multiples of 128), so
-// idx + k == idx ^ k and the 8 rounding draws share one hash head.
+// Rounds and stores 8 new master values (at p and lo, as load_master8); x becomes the values
+// stored.  idx % 8 == 0 (the FP8 kernel's lanes start at multiples of 8 within segments that start
+// at multiples of 128), so idx + k == idx ^ k and the 8 rounding draws share one hash head.
 template <int PT, bool SR>
-__device__ __forceinline__ void store_master8(const DevSeg& s, int64_t i, float (&x)[8], uint32_t idx)
+__device__ __forceinline__ void store_master8(void* p, uint8_t* lo, float (&x)[8], uint32_t idx, uint32_t seed)
 {
     if constexpr (PT == DT_F24) {
-        uint32_t hi[8], lo[2] = {0u, 0u}, r[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+        uint32_t r[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
         if constexpr (SR) {
-            const uint32_t head = hash32_head(idx ^ s.seed_p);
+            const uint32_t head = hash32_head(idx ^ seed);
 #pragma unroll
             for (int k = 0; k < 8; ++k) r[k] = hash32_tail(head ^ (uint32_t)k);
         }
-        // f24_round quietens a NaN; where no lane of the wavefront holds one (a uniform test on
-        // the compares' lane masks), the rounding is the add and the cut alone
+        // f24_round: the add and the cut, and a NaN quietened instead; the NaN fix-up runs only
+        // where some lane of the wavefront holds one (a uniform test on the compares' lane masks)
         uint64_t nans = 0;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) nans |= __builtin_amdgcn_ballot_w64(x[k] != x[k]);
         uint32_t b[8];
-        if (nans == 0) {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const uint32_t u = fbits(x[k]);
-                b[k] = (SR ? u + (r[k] & 0xffu) : u + 0x7fu + ((u >> 8) & 1u)) & ~0xffu;
-            }
-        } else {
+        for (int k = 0; k < 8; ++k) {
+            nans |= __builtin_amdgcn_ballot_w64(x[k] != x[k]);
+            const uint32_t u = fbits(x[k]);
+            b[k] = (SR ? u + (r[k] & 0xffu) : u + 0x7fu + ((u >> 8) & 1u)) & ~0xffu;
+        }
+        if (nans != 0) {
 #pragma unroll
             for (int k = 0; k < 8; ++k) b[k] = f24_round<SR>(x[k], r[k]);
         }
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            x[k] = bitsf(b[k]);
-            hi[k] = b[k] >> 16;
-            lo[k >> 2] |= ((b[k] >> 8) & 0xffu) << (8 * (k & 3));
-        }
-        store8_u16(s.p, i, hi);
-        st(reinterpret_cast<u32x2*>(s.p_lo + i), u32x2{lo[0], lo[1]});
+        for (int k = 0; k < 8; ++k) x[k] = bitsf(b[k]);
+        // the planes by byte permutes: high halves two to a word, low bytes four to a word
+        const u32x4 h = {__builtin_amdgcn_perm(b[1], b[0], 0x07060302u), __builtin_amdgcn_perm(b[3], b[2], 0x07060302u),
+                         __builtin_amdgcn_perm(b[5], b[4], 0x07060302u), __builtin_amdgcn_perm(b[7], b[6], 0x07060302u)};
+        const u32x2 l = {__builtin_amdgcn_perm(b[1], b[0], 0x0c0c0501u) | __builtin_amdgcn_perm(b[3], b[2], 0x05010c0cu),
+                         __builtin_amdgcn_perm(b[5], b[4], 0x0c0c0501u) | __builtin_amdgcn_perm(b[7], b[6], 0x05010c0cu)};
+        st(static_cast<u32x4*>(p), h);
+        st(reinterpret_cast<u32x2*>(lo), l);
     } else if constexpr (PT == DT_PACKED8) {
-        uint8_t* r = static_cast<uint8_t*>(s.p) + record_master_offset(i);
+        uint8_t* r = static_cast<uint8_t*>(p);
         st(reinterpret_cast<f32x4*>(r), f32x4{x[0], x[1], x[2], x[3]});
         st(reinterpret_cast<f32x4*>(r + 256), f32x4{x[4], x[5], x[6], x[7]});
     } else {
-        store8_f32(s.p, i, x);
-    }
-}
-
-template <int MV, bool SR>
-__device__ __forceinline__ void store_moment8(void* base, int64_t i, const float (&x)[8], uint32_t idx,
-                                              uint32_t seed)
-{
-    if constexpr (MV == DT_BF16) {
-        uint32_t h[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) h[k] = bf16_store<SR>(x[k], SR ? hash32((idx + k) ^ seed) : 0u);
-        store8_u16(base, i, h);
-    } else {
-        store8_f32(base, i, x);
+        store8_f32(p, x);
     }
 }
 
 template <int OT>
-__device__ __forceinline__ void store_out8(void* base, int64_t i, const float (&x)[8])
+__device__ __forceinline__ void store_out8(void* p, const float (&x)[8])
 {
     if constexpr (OT == DT_BF16) {
         const u32x4 w = {bf16x2_rne(x[0], x[1]), bf16x2_rne(x[2], x[3]), bf16x2_rne(x[4], x[5]),
                          bf16x2_rne(x[6], x[7])};
-        st(reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + i), w);
+        st(static_cast<u32x4*>(p), w);
     } else if constexpr (OT == DT_F32) {
-        store8_f32(base, i, x);
+        store8_f32(p, x);
     }
 }
 
@@ -534,17 +529,17 @@ __device__ __forceinline__ void decode_codes(const u32x2 w, float (&x)[8])
     }
 }
 
-// x[k] / scale in place for a lane's 8 elements of one block (see block_div).  NONNEG: the
-// values are the sqrt-domain v (never -0 or NaN).
-template <bool NONNEG>
+// x[k] / scale in place for a lane's 8 elements of one block (see block_div).  PLAIN: no value is
+// -0 or NaN (block_quot_fast).
+template <bool PLAIN>
 __device__ __forceinline__ void block_quotients(float (&x)[8], const BlockDiv& d)
 {
     if (d.fast && d.pre == 1.0f) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) x[k] = block_quot_fast<false, NONNEG>(x[k], d);
+        for (int k = 0; k < 8; ++k) x[k] = block_quot_fast<false, PLAIN>(x[k], d);
     } else if (d.fast) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) x[k] = block_quot_fast<true, NONNEG>(x[k], d);
+        for (int k = 0; k < 8; ++k) x[k] = block_quot_fast<true, PLAIN>(x[k], d);
     } else {
 #pragma unroll
         for (int k = 0; k < 8; ++k) x[k] = x[k] / d.s;
@@ -573,18 +568,24 @@ __device__ __forceinline__ float group16_max(float x)
     return bitsf(u);
 }
 
-// A lane's 8 codes (two words, byte k & 3 of word k >> 2) through gfx950's conversion
-// instructions.  Returns false if some value lies outside the range where those give
-// fp8_encode's code (fp8_hw_range); the words are then to be recomputed in software.
-// idx % 8 == 0: FP8 segments start at multiples of 128 elements and a lane's group at a
-// multiple of 8, so the 8 rounding streams share one hash head.
+// Whether every one of a lane's 8 values lies in the range where gfx950's conversion instructions
+// give fp8_encode's code (fp8_hw_range): one unsigned maximum of their offsets, no branches.
 template <bool E5M2, bool SR>
-__device__ __forceinline__ bool hw_codes8(const float (&x)[8], uint32_t idx, uint32_t seed, uint32_t (&q)[2])
+__device__ __forceinline__ bool hw_range8(const float (&x)[8])
 {
-    uint32_t worst = 0u;   // largest offset from the range's start (unsigned): no branches
+    uint32_t worst = 0u;
 #pragma unroll
     for (int k = 0; k < 8; ++k) worst = __builtin_elementwise_max(worst, fp8_hw_offset<E5M2, SR>(x[k]));
-    const bool ok = worst <= fp8_hw_span<E5M2, SR>;
+    return worst <= fp8_hw_span<E5M2, SR>;
+}
+
+// A lane's 8 codes (two words, byte k & 3 of word k >> 2) through gfx950's conversion
+// instructions; they are the reference's codes where hw_range8 holds (otherwise the words are to
+// be recomputed in software).  idx % 8 == 0: FP8 segments start at multiples of 128 elements and
+// a lane's group at a multiple of 8, so the 8 rounding streams share one hash head.
+template <bool E5M2, bool SR>
+__device__ __forceinline__ void hw_codes8(const float (&x)[8], uint32_t idx, uint32_t seed, uint32_t (&q)[2])
+{
     if constexpr (SR) {
         const uint32_t head = hash32_head(idx ^ seed);
         uint32_t r[8];
@@ -602,7 +603,6 @@ __device__ __forceinline__ bool hw_codes8(const float (&x)[8], uint32_t idx, uin
         q[0] = fp8_hw_rne2<E5M2, true>(x[2], x[3], fp8_hw_rne2<E5M2, false>(x[0], x[1], 0u));
         q[1] = fp8_hw_rne2<E5M2, true>(x[6], x[7], fp8_hw_rne2<E5M2, false>(x[4], x[5], 0u));
     }
-    return ok;
 }
 
 // FP8 block scale: absmax / format max, 1 for an all-zero block (kernels.c:1049-1057), correctly
@@ -625,40 +625,61 @@ __device__ __forceinline__ float block_scale(float amax)
 // update, store master and output, block maxima by DPP within the 16 lanes, scales, codes.
 // FULL: the whole block lies inside the segment, takes the fused form and allows vector access --
 // straight-line code.  FULL is the same for the 16 lanes of a block, so the DPP maxima below always
-// run with the whole group active.
+// run with the whole group active.  base: the workgroup's first element of this pass over its tile
+// (uniform, a multiple of the FP8 quantum); off = 8 x the lane's index in the workgroup, so the
+// lane's elements start at e0 = base + off and its block at base + (off & ~127).  Vector accesses
+// address base's byte offset (scalar) plus the lane's (lane_ptr).
 template <int ALGO, int PT, int GT, int OT, bool SR, bool FULL, bool PREV>
-__device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_t b0, int lane)
+__device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_t base, uint32_t off)
 {
     constexpr bool kLion = ALGO == ALGO_LION;
+    constexpr int kGB = GT == DT_BF16 ? 2 : 4, kOB = OT == DT_BF16 ? 2 : 4, kPB = PT == DT_F24 ? 2 : 4;
     const int64_t n = s.n, n_main = s.n_main;
     const bool vec = FULL || (s.flags & kVec) != 0;
     uint8_t* const mq = static_cast<uint8_t*>(s.m);
     uint8_t* const vq = static_cast<uint8_t*>(s.v);
-    const int64_t blk = b0 / kFp8Block;
-    const int64_t e0 = b0 + lane * 8;
+    const int64_t e0 = base + off;
     const uint32_t idx = s.idx0 + (uint32_t)e0;
     const bool full = FULL || (vec && e0 + 8 <= n);
+    const uint32_t lane = (off >> 3) & 15u;         // within the block's 16
+    const uint32_t blk = off >> 7;                   // the block within this pass
+    const int64_t ublk = base / kFp8Block;           // the pass's first block
+    // DT_PACKED8: the lane's 16-byte slots in its block's record (masters, then codes at + 512)
+    const uint32_t rec = blk * (uint32_t)kRecordBytes + lane * 16u;
     // Block scales: ordinary (cached) accesses.  A wavefront reads and writes 16 bytes of each
     // scale array, four blocks' worth; through L2 the four wavefronts of a workgroup share whole
     // lines, where non-temporal accesses sent each 16-byte piece to HBM on its own (measured: the
     // launch 3-4% slower, reads and writes 1.4% above the algorithmic bytes).
-    const float sm = *(const ABH_GLOBAL float*)(s.m_scale + blk);
-    const float sv = kLion ? 0.0f : *(const ABH_GLOBAL float*)(s.v_scale + blk);
+    const float sm = *(const ABH_GLOBAL float*)lane_ptr<float>(s.m_scale, ublk * 4, blk * 4u);
+    const float sv = kLion ? 0.0f : *(const ABH_GLOBAL float*)lane_ptr<float>(s.v_scale, ublk * 4, blk * 4u);
+    // the master's (pm, pl) and the output's (po) vector addresses for the lane offset o
+    auto pm = [&](uint32_t o) -> void* {
+        if constexpr (PT == DT_PACKED8) return lane_ptr<void>(s.p, ublk * kRecordBytes, (o >> 7) * (uint32_t)kRecordBytes + ((o >> 3) & 15u) * 16u);
+        else return lane_ptr<void>(s.p, base * kPB, o * (uint32_t)kPB);
+    };
+    auto pl = [&](uint32_t o) -> uint8_t* {
+        if constexpr (PT == DT_F24) return lane_ptr<uint8_t>(s.p_lo, base, o);
+        else return nullptr;
+    };
+    auto po = [&](uint32_t o) -> void* {
+        if constexpr (OT != DT_NONE) return lane_ptr<void>(s.out, base * kOB, o * (uint32_t)kOB);
+        else return nullptr;
+    };
     // codes are stored padded to whole blocks, so all 8 of this lane's exist
     u32x2 cm, cv = {0u, 0u};
     if constexpr (PT == DT_PACKED8) {   // AdamW only
-        const u32x4 c = ld(reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(s.p) + record_codes_offset(e0)));
-        cm = u32x2{c.x, c.y};
-        cv = u32x2{c.z, c.w};
+        const u32x4 w = ld(lane_ptr<const u32x4>(s.p, ublk * kRecordBytes, rec + 512u));
+        cm = u32x2{w.x, w.y};
+        cv = u32x2{w.z, w.w};
     } else {
-        cm = vec ? ld(reinterpret_cast<const u32x2*>(mq + e0)) : load_codes8(mq + e0);
-        if constexpr (!kLion) cv = vec ? ld(reinterpret_cast<const u32x2*>(vq + e0)) : load_codes8(vq + e0);
+        cm = vec ? ld(lane_ptr<const u32x2>(mq, base, off)) : load_codes8(mq + e0);
+        if constexpr (!kLion) cv = vec ? ld(lane_ptr<const u32x2>(vq, base, off)) : load_codes8(vq + e0);
     }
     float g[8], p[8], mt[8], vt[8];
     if (full) {
-        load8<GT>(s.g, e0, g);
-        load_master8<PT>(s, e0, p);
-        if constexpr (PREV) store_out8<OT>(s.out, e0, p);   // out from the master as loaded
+        load8<GT>(lane_ptr<const void>(s.g, base * kGB, off * (uint32_t)kGB), g);
+        load_master8<PT>(pm(off), pl(off), p);
+        if constexpr (PREV) store_out8<OT>(po(off), p);   // out from the master as loaded
     } else {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
@@ -685,9 +706,11 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     // the update, FP32 moments in registers; sq = sqrt(new v), reused for the v code below
     float sq[8];
     const bool lane_fused = FULL || kLion || e0 + 8 <= n_main;
-    bool v_pos = false;   // every new v of the wavefront positive and finite (uniform)
+    bool v_pos = false;     // every new v of the wavefront positive and finite (uniform)
+    bool m_plain = false;   // every new m of the wavefront finite, 2^-60 <= |m| <= 2^60 (uniform)
+    uint32_t m_low = 0u;    // where m_plain: the lane's smallest |m| as quot_m_offset
     if constexpr (FULL && !kLion) {
-        v_pos = adamw8_fused(p, g, mt, vt, c, sq, (s.flags & kFastDiv) != 0);
+        v_pos = adamw8_fused(p, g, mt, vt, c, sq, (s.flags & kFastDiv) != 0, m_plain, m_low);
     } else {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
@@ -697,8 +720,9 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
         }
     }
     if (full) {
-        store_master8<PT, SR>(s, e0, p, idx);
-        if constexpr (!PREV) store_out8<OT>(s.out, e0, p);
+        const uint32_t o = fresh(off);
+        store_master8<PT, SR>(pm(o), pl(o), p, idx, s.seed_p);
+        if constexpr (!PREV) store_out8<OT>(po(o), p);
     } else {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
@@ -708,29 +732,35 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
             }
         }
     }
-    // block maxima (NaN skipped), elements past the end count as zero; v is stored as
-    // sqrt(max(v, 0)), which is sq wherever v > 0 (same correctly rounded root)
-    float am = 0.0f, au = 0.0f;
+    // block maxima (NaN skipped), elements past the end count as zero.  v is stored as
+    // u = sqrt(max(v, 0)) (kernels.c:893-905).  The new v is never -0 (an FMA of a product and a
+    // sum of exact zeros rounds to +0), so u is sq (the same correctly rounded root) wherever sq is
+    // not NaN, i.e. v >= 0, and 0 where it is (v < 0 or NaN).  Where v_pos holds, u = sq throughout,
+    // and the lane's smallest u serves the conversion instructions' range test below.  Otherwise sq
+    // keeps its NaNs (read here, not rewritten: a rewrite would have the branches hand sq over in
+    // different registers), v_nan marks them, and the integer encoder below codes 0 there.
+    float am = 0.0f, au = 0.0f, u_min = 0.0f;
+    uint32_t v_nan = 0u;   // bit k: sq[k] is NaN
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        if (!FULL && e0 + k >= n) { mt[k] = 0.0f; vt[k] = 0.0f; }
+        if (!FULL && e0 + k >= n) { mt[k] = 0.0f; sq[k] = 0.0f; }
         am = __builtin_fmaxf(am, fabsf(mt[k]));   // a NaN m is skipped (IEEE maxNum)
     }
     if constexpr (!kLion) {
-        if (v_pos) {   // u = sq; positive floats order as their bits
-            uint32_t ub = 0u;
+        if (v_pos) {   // positive floats order as their bits
+            uint32_t ub = 0u, lb = 0xffffffffu;
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                vt[k] = sq[k];
                 ub = __builtin_elementwise_max(ub, fbits(sq[k]));
+                lb = __builtin_elementwise_min(lb, fbits(sq[k]));
             }
             au = bitsf(ub);
+            u_min = bitsf(lb);
         } else {
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                const float u = vt[k] > 0.0f ? sq[k] : 0.0f;
-                vt[k] = u;
-                au = u > au ? u : au;
+                au = sq[k] > au ? sq[k] : au;   // a NaN is skipped
+                v_nan |= sq[k] != sq[k] ? 1u << k : 0u;
             }
         }
     }
@@ -741,16 +771,28 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
         au = group16_max(au);
         scu = block_scale<true>(au);
     }
-    block_quotients<false>(mt, block_div(scm, am));
-    if constexpr (!kLion) block_quotients<true>(vt, block_div(scu, au));
+    {
+        const BlockDiv dm = block_div(scm, am);
+        if (m_plain) block_quotients<true>(mt, dm);
+        else block_quotients<false>(mt, dm);
+    }
+    if constexpr (!kLion) block_quotients<true>(sq, block_div(scu, au));
     // codes: full blocks through the conversion instructions; a lane holding a value outside
     // their exact range (rare: zeros, values below the smallest normal after scaling, NaN) and
-    // partial blocks take the integer encoder
+    // partial blocks take the integer encoder.  Where m_plain (v_pos) holds, the lane's values
+    // are finite and nonzero, and each quotient reaches the smallest normal 2^-6 (2^-14) once the
+    // smallest |m| (u) reaches that multiple of the scale (the multiple is exact, and rounding is
+    // monotone; quot_m_offset keeps the order from 2^-60 up and wraps below, which fails the test);
+    // the per-value test is needed otherwise.
     uint32_t qm[2] = {0u, 0u}, qv[2] = {0u, 0u};
     bool soft_m = true, soft_v = !kLion;
     if constexpr (FULL) {
-        soft_m = !hw_codes8<false, SR>(mt, idx, s.seed_m, qm);
-        if constexpr (!kLion) soft_v = !hw_codes8<true, SR>(vt, idx, s.seed_v, qv);
+        hw_codes8<false, SR>(mt, idx, s.seed_m, qm);
+        soft_m = !(m_plain ? (!SR || m_low >= quot_m_offset(scm * 0x1p-6f)) : hw_range8<false, SR>(mt));
+        if constexpr (!kLion) {
+            hw_codes8<true, SR>(sq, idx, s.seed_v, qv);
+            soft_v = !(v_pos ? (!SR || u_min >= scu * 0x1p-14f) : hw_range8<true, SR>(sq));
+        }
     }
     if (soft_m) {
         qm[0] = qm[1] = 0u;
@@ -766,23 +808,25 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const bool in = FULL || e0 + k < n;
-            const uint32_t b = e5m2_encode<SR>(vt[k], SR ? hash32((idx + k) ^ s.seed_v) : 0u);
+            const float u = (v_nan >> k) & 1u ? 0.0f : sq[k];   // u / scale: 0 where sq was NaN
+            const uint32_t b = e5m2_encode<SR>(u, SR ? hash32((idx + k) ^ s.seed_v) : 0u);
             qv[k >> 2] |= (in ? b : 0u) << (8 * (k & 3));
         }
     }
+    const uint32_t o = fresh(off);
     if constexpr (PT == DT_PACKED8) {
-        st(reinterpret_cast<u32x4*>(static_cast<uint8_t*>(s.p) + record_codes_offset(e0)),
+        st(lane_ptr<u32x4>(s.p, ublk * kRecordBytes, (o >> 7) * (uint32_t)kRecordBytes + ((o >> 3) & 15u) * 16u + 512u),
            u32x4{qm[0], qm[1], qv[0], qv[1]});
     } else if (vec) {
-        st(reinterpret_cast<u32x2*>(mq + e0), u32x2{qm[0], qm[1]});
-        if constexpr (!kLion) st(reinterpret_cast<u32x2*>(vq + e0), u32x2{qv[0], qv[1]});
+        st(lane_ptr<u32x2>(mq, base, o), u32x2{qm[0], qm[1]});
+        if constexpr (!kLion) st(lane_ptr<u32x2>(vq, base, o), u32x2{qv[0], qv[1]});
     } else {
         store_codes8(mq + e0, qm);
         if constexpr (!kLion) store_codes8(vq + e0, qv);
     }
     if (lane == 0) {
-        *(ABH_GLOBAL float*)(s.m_scale + blk) = scm;
-        if constexpr (!kLion) *(ABH_GLOBAL float*)(s.v_scale + blk) = scu;
+        *(ABH_GLOBAL float*)lane_ptr<float>(s.m_scale, ublk * 4, (o >> 7) * 4u) = scm;
+        if constexpr (!kLion) *(ABH_GLOBAL float*)lane_ptr<float>(s.v_scale, ublk * 4, (o >> 7) * 4u) = scu;
     }
 }
 
@@ -791,8 +835,8 @@ __device__ __forceinline__ void update_tile_fp8(const DevSeg& s, int64_t tile, i
 {
     constexpr bool kLion = ALGO == ALGO_LION;
     const Coef c = s.c;
-    const int lane = threadIdx.x & 15;
-    const int group = threadIdx.x >> 4;
+    const uint32_t off = threadIdx.x * 8u;   // 16-lane group g holds block g of each pass
+    const int64_t goff = (int64_t)(off & ~(uint32_t)(kFp8Block - 1));
     const bool vec = (s.flags & kVec) != 0;
     // blocks wholly in the fused range (AdamW's scalar tail, if any, is the segment's last n mod W)
     const int64_t full_end = kLion ? s.n : s.n_main;
@@ -800,18 +844,20 @@ __device__ __forceinline__ void update_tile_fp8(const DevSeg& s, int64_t tile, i
     // no loop-carried addresses (measured 1.3% faster on the 7B FP8 step in a fast HBM placement,
     // equal in a slow one)
     if (T == kFp8Quantum) {
-        const int64_t b0 = (tile - s.tile_begin) * kFp8Quantum + group * kFp8Block;
+        const int64_t base = (tile - s.tile_begin) * kFp8Quantum;
+        const int64_t b0 = base + goff;
         if (b0 >= s.n) return;
-        if (vec && b0 + kFp8Block <= full_end) fp8_block<ALGO, PT, GT, OT, SR, true, PREV>(s, c, b0, lane);
-        else fp8_block<ALGO, PT, GT, OT, SR, false, PREV>(s, c, b0, lane);
+        if (vec && b0 + kFp8Block <= full_end) fp8_block<ALGO, PT, GT, OT, SR, true, PREV>(s, c, base, off);
+        else fp8_block<ALGO, PT, GT, OT, SR, false, PREV>(s, c, base, off);
         return;
     }
     const int64_t lo = (tile - s.tile_begin) * T;
     const int64_t hi = lo + T < s.n ? lo + T : s.n;
-    // larger tiles (ADAMBRIDGE_TILE_FP8): each 16-lane group walks every 16th block of the tile
-    for (int64_t b0 = lo + group * kFp8Block; b0 < hi; b0 += (kThreads / 16) * kFp8Block) {
-        if (vec && b0 + kFp8Block <= full_end) fp8_block<ALGO, PT, GT, OT, SR, true, PREV>(s, c, b0, lane);
-        else fp8_block<ALGO, PT, GT, OT, SR, false, PREV>(s, c, b0, lane);
+    // larger tiles (ADAMBRIDGE_TILE_FP8): each pass covers the next 16 blocks of the tile
+    for (int64_t base = lo; base + goff < hi; base += kFp8Quantum) {
+        const int64_t b0 = base + goff;
+        if (vec && b0 + kFp8Block <= full_end) fp8_block<ALGO, PT, GT, OT, SR, true, PREV>(s, c, base, off);
+        else fp8_block<ALGO, PT, GT, OT, SR, false, PREV>(s, c, base, off);
     }
 }
 
@@ -1791,11 +1837,11 @@ __device__ bool divisions_match(uint32_t u, uint32_t seed)
     const float r = bitsf((h1 & 0x807fffffu) | (126u << 23));   // (-1, -0.5] or [0.5, 1)
     const float x = amax * r;
     if (!(x != 0.0f)) return true;
-    const bool nonneg = x > 0.0f && (h4 & 2u);
+    const bool plain = (h4 & 2u) != 0u;   // x is nonzero and not NaN here: either variant applies
     float q;
     if (!d.fast) q = x / d.s;
-    else if (d.pre == 1.0f) q = nonneg ? block_quot_fast<false, true>(x, d) : block_quot_fast<false, false>(x, d);
-    else q = nonneg ? block_quot_fast<true, true>(x, d) : block_quot_fast<true, false>(x, d);
+    else if (d.pre == 1.0f) q = plain ? block_quot_fast<false, true>(x, d) : block_quot_fast<false, false>(x, d);
+    else q = plain ? block_quot_fast<true, true>(x, d) : block_quot_fast<true, false>(x, d);
     const float aq = fabsf(q);
     if (!(aq >= 0x1p-126f)) return true;   // quotients below the normal range are not asserted here
     return is_nearest_quotient(fbits(x), fbits(s), fbits(q));
