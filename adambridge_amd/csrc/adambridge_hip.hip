@@ -216,6 +216,17 @@ __device__ __forceinline__ int64_t record_master_offset(int64_t i)
     return (i >> 7) * kRecordBytes + ((i & 4) ? 256 : 0) + ((i >> 3) & 15) * 16 + (i & 3) * 4;
 }
 
+// FP8 records with an FP24 master (p_dtype DT_PACKED8_F24): per 128-element block one 640-byte record,
+// the block's master high halves (bytes 0 .. 255) and low bytes (256 .. 383) in element order, then
+// lane l's m codes at 384 + 16l and v codes at 392 + 16l, as in DT_PACKED8.  Lane l's three
+// accesses (16-byte high halves, 8-byte low bytes, 16-byte codes) are each one contiguous span per
+// block.
+constexpr int64_t kRecordBytesF24 = 640;
+
+// Byte offsets of element i's master high half and low byte within those records.
+__device__ __forceinline__ int64_t record_f24_hi_offset(int64_t i) { return (i >> 7) * kRecordBytesF24 + (i & 127) * 2; }
+__device__ __forceinline__ int64_t record_f24_lo_offset(int64_t i) { return (i >> 7) * kRecordBytesF24 + 256 + (i & 127); }
+
 // The masters of 8 consecutive elements: the FP24 planes at p (high halves) and lo (low bytes),
 // a record's two 16-byte halves at p and p + 256 (DT_PACKED8), or FP32 at p.
 template <int PT>
@@ -390,7 +401,11 @@ __device__ __forceinline__ float load_master1(const DevSeg& s, int64_t i)
 {
     if constexpr (PT == DT_F24)
         return bitsf(((uint32_t)ld(static_cast<const uint16_t*>(s.p) + i) << 16) | ((uint32_t)ld(s.p_lo + i) << 8));
-    else if constexpr (PT == DT_PACKED8)
+    else if constexpr (PT == DT_PACKED8_F24) {
+        const uint8_t* r = static_cast<const uint8_t*>(s.p);
+        return bitsf(((uint32_t)ld(reinterpret_cast<const uint16_t*>(r + record_f24_hi_offset(i))) << 16) |
+                     ((uint32_t)ld(r + record_f24_lo_offset(i)) << 8));
+    } else if constexpr (PT == DT_PACKED8)
         return ld(reinterpret_cast<const float*>(static_cast<const uint8_t*>(s.p) + record_master_offset(i)));
     else return ld(static_cast<const float*>(s.p) + i);
 }
@@ -402,6 +417,12 @@ __device__ __forceinline__ float store_master1(const DevSeg& s, int64_t i, float
         const uint32_t b = f24_round<SR>(x, SR ? hash32(idx ^ s.seed_p) : 0u);
         st(static_cast<uint16_t*>(s.p) + i, (uint16_t)(b >> 16));
         st(s.p_lo + i, (uint8_t)(b >> 8));
+        return bitsf(b);
+    } else if constexpr (PT == DT_PACKED8_F24) {
+        const uint32_t b = f24_round<SR>(x, SR ? hash32(idx ^ s.seed_p) : 0u);
+        uint8_t* r = static_cast<uint8_t*>(s.p);
+        st(reinterpret_cast<uint16_t*>(r + record_f24_hi_offset(i)), (uint16_t)(b >> 16));
+        st(r + record_f24_lo_offset(i), (uint8_t)(b >> 8));
         return bitsf(b);
     } else if constexpr (PT == DT_PACKED8) {
         st(reinterpret_cast<float*>(static_cast<uint8_t*>(s.p) + record_master_offset(i)), x);
@@ -634,6 +655,11 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
 {
     constexpr bool kLion = ALGO == ALGO_LION;
     constexpr int kGB = GT == DT_BF16 ? 2 : 4, kOB = OT == DT_BF16 ? 2 : 4, kPB = PT == DT_F24 ? 2 : 4;
+    // block records (AdamW only): FP32 master (DT_PACKED8) or FP24 master (DT_PACKED8_F24)
+    constexpr bool kRec = PT == DT_PACKED8 || PT == DT_PACKED8_F24;
+    constexpr uint32_t kRecB = PT == DT_PACKED8 ? (uint32_t)kRecordBytes : (uint32_t)kRecordBytesF24;
+    constexpr uint32_t kCodesAt = PT == DT_PACKED8 ? 512u : 384u;   // the codes' slots in a record
+    constexpr int kMaster = PT == DT_PACKED8_F24 ? DT_F24 : PT;     // how the 8 masters are coded
     const int64_t n = s.n, n_main = s.n_main;
     const bool vec = FULL || (s.flags & kVec) != 0;
     uint8_t* const mq = static_cast<uint8_t*>(s.m);
@@ -644,8 +670,8 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     const uint32_t lane = (off >> 3) & 15u;         // within the block's 16
     const uint32_t blk = off >> 7;                   // the block within this pass
     const int64_t ublk = base / kFp8Block;           // the pass's first block
-    // DT_PACKED8: the lane's 16-byte slots in its block's record (masters, then codes at + 512)
-    const uint32_t rec = blk * (uint32_t)kRecordBytes + lane * 16u;
+    // records: the lane's 16-byte codes slot in its block's record
+    const uint32_t rec_codes = blk * kRecB + kCodesAt + lane * 16u;
     // Block scales: ordinary (cached) accesses.  A wavefront reads and writes 16 bytes of each
     // scale array, four blocks' worth; through L2 the four wavefronts of a workgroup share whole
     // lines, where non-temporal accesses sent each 16-byte piece to HBM on its own (measured: the
@@ -654,11 +680,12 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     const float sv = kLion ? 0.0f : *(const ABH_GLOBAL float*)lane_ptr<float>(s.v_scale, ublk * 4, blk * 4u);
     // the master's (pm, pl) and the output's (po) vector addresses for the lane offset o
     auto pm = [&](uint32_t o) -> void* {
-        if constexpr (PT == DT_PACKED8) return lane_ptr<void>(s.p, ublk * kRecordBytes, (o >> 7) * (uint32_t)kRecordBytes + ((o >> 3) & 15u) * 16u);
+        if constexpr (kRec) return lane_ptr<void>(s.p, ublk * kRecB, (o >> 7) * kRecB + ((o >> 3) & 15u) * 16u);
         else return lane_ptr<void>(s.p, base * kPB, o * (uint32_t)kPB);
     };
     auto pl = [&](uint32_t o) -> uint8_t* {
         if constexpr (PT == DT_F24) return lane_ptr<uint8_t>(s.p_lo, base, o);
+        else if constexpr (PT == DT_PACKED8_F24) return lane_ptr<uint8_t>(s.p, ublk * kRecB, (o >> 7) * kRecB + 256u + ((o >> 3) & 15u) * 8u);
         else return nullptr;
     };
     auto po = [&](uint32_t o) -> void* {
@@ -667,8 +694,8 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     };
     // codes are stored padded to whole blocks, so all 8 of this lane's exist
     u32x2 cm, cv = {0u, 0u};
-    if constexpr (PT == DT_PACKED8) {   // AdamW only
-        const u32x4 w = ld(lane_ptr<const u32x4>(s.p, ublk * kRecordBytes, rec + 512u));
+    if constexpr (kRec) {   // AdamW only
+        const u32x4 w = ld(lane_ptr<const u32x4>(s.p, ublk * kRecB, rec_codes));
         cm = u32x2{w.x, w.y};
         cv = u32x2{w.z, w.w};
     } else {
@@ -678,7 +705,7 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     float g[8], p[8], mt[8], vt[8];
     if (full) {
         load8<GT>(lane_ptr<const void>(s.g, base * kGB, off * (uint32_t)kGB), g);
-        load_master8<PT>(pm(off), pl(off), p);
+        load_master8<kMaster>(pm(off), pl(off), p);
         if constexpr (PREV) store_out8<OT>(po(off), p);   // out from the master as loaded
     } else {
 #pragma unroll
@@ -721,7 +748,7 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     }
     if (full) {
         const uint32_t o = fresh(off);
-        store_master8<PT, SR>(pm(o), pl(o), p, idx, s.seed_p);
+        store_master8<kMaster, SR>(pm(o), pl(o), p, idx, s.seed_p);
         if constexpr (!PREV) store_out8<OT>(po(o), p);
     } else {
 #pragma unroll
@@ -814,8 +841,8 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
         }
     }
     const uint32_t o = fresh(off);
-    if constexpr (PT == DT_PACKED8) {
-        st(lane_ptr<u32x4>(s.p, ublk * kRecordBytes, (o >> 7) * (uint32_t)kRecordBytes + ((o >> 3) & 15u) * 16u + 512u),
+    if constexpr (kRec) {
+        st(lane_ptr<u32x4>(s.p, ublk * kRecB, (o >> 7) * kRecB + kCodesAt + ((o >> 3) & 15u) * 16u),
            u32x4{qm[0], qm[1], qv[0], qv[1]});
     } else if (vec) {
         st(lane_ptr<u32x2>(mq, base, o), u32x2{qm[0], qm[1]});
@@ -1492,11 +1519,28 @@ constexpr auto make_lion_f24rec_table(std::integer_sequence<int, I...>)
 
 static const auto kLionF24Rec = make_lion_f24rec_table(std::make_integer_sequence<int, kNumPacked>{});
 
+// FP8 records with an FP24 master (AdamW) follow: index kNumKernels + 6 * kNumPacked + gt * 3 + ot.
+template <int I>
+constexpr KernelFn packed8_f24_entry()
+{
+    constexpr int ot = I % 3, gt = I / 3;
+    return &k_update_fp8<ALGO_ADAMW, DT_PACKED8_F24, gt ? DT_BF16 : DT_F32, ot == 0 ? DT_NONE : ot == 1 ? DT_F32 : DT_BF16>;
+}
+
+template <int... I>
+constexpr auto make_packed8_f24_table(std::integer_sequence<int, I...>)
+{
+    return std::array<KernelFn, sizeof...(I)>{packed8_f24_entry<I>()...};
+}
+
+static const auto kPacked8F24 = make_packed8_f24_table(std::make_integer_sequence<int, kNumPacked>{});
+
 // Kernel family of a table index: the FP8 block kernel, or a two-element-per-lane kernel.
 inline bool kernel_is_fp8(int index)
 {
     if (index < kNumKernels) return (index / 12) % 3 == 2;
-    return index >= kNumKernels + kNumPacked && index < kNumKernels + 2 * kNumPacked;
+    return (index >= kNumKernels + kNumPacked && index < kNumKernels + 2 * kNumPacked) ||
+           index >= kNumKernels + 6 * kNumPacked;
 }
 
 inline KernelFn kernel_at(int index)
@@ -1507,7 +1551,8 @@ inline KernelFn kernel_at(int index)
     if (index < kNumKernels + 3 * kNumPacked) return kLionRec[index - kNumKernels - 2 * kNumPacked];
     if (index < kNumKernels + 4 * kNumPacked) return kF32Rec[index - kNumKernels - 3 * kNumPacked];
     if (index < kNumKernels + 5 * kNumPacked) return kF24Rec[index - kNumKernels - 4 * kNumPacked];
-    return kLionF24Rec[index - kNumKernels - 5 * kNumPacked];
+    if (index < kNumKernels + 6 * kNumPacked) return kLionF24Rec[index - kNumKernels - 5 * kNumPacked];
+    return kPacked8F24[index - kNumKernels - 6 * kNumPacked];
 }
 
 inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
@@ -1524,6 +1569,8 @@ inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
         return kNumKernels + 4 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
     if (pt == DT_PACKED_LION_F24)
         return kNumKernels + 5 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
+    if (pt == DT_PACKED8_F24)
+        return kNumKernels + 6 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
     const int mvi = mv == DT_F32 ? 0 : mv == DT_BF16 ? 1 : 2;
     const int pti = pt == DT_F24 ? 1 : 0;
     const int gti = gt == DT_BF16 ? 1 : 0;

@@ -19,6 +19,7 @@ layout          serves                                 bytes of state per elemen
 separate        anything (the reference's arrays)      master 4 (FP24: 3) + moments
 pairs           AdamW, FP32 master, BF16 moments       16 per 2 elements (x2 double-buffered)
 fp8-records     AdamW, FP32 master, FP8 moments        768 per 128 + two FP32 scales per 128
+fp8-f24-rec.    AdamW, FP24 master, FP8 moments        640 per 128 + two FP32 scales per 128
 lion-records    Lion, FP32 master, BF16 moment         1536 per 256 (x2 double-buffered)
 f32-records     AdamW, FP32 master, FP32 moments       3072 per 256 (x2 double-buffered)
 f24-records     AdamW, FP24 master, BF16 moments       1792 per 256 (x2 double-buffered)
@@ -42,9 +43,12 @@ from . import formats as F
 from .precision import BF16Store, FP8Store, FP24Store, FP32Store, MomentStore, load_master_, make_master, make_store
 
 __all__ = ["ParamState", "SeparateState", "PairState", "AdamRecordState", "LionRecordState", "F32RecordState",
-           "F24RecordState", "LionF24RecordState", "choose_layout", "new_state", "new_states", "arena_plan", "arena_memory", "LAYOUTS"]
+           "F24RecordState", "LionF24RecordState", "AdamF24RecordState", "choose_layout", "new_state", "new_states",
+           "arena_plan", "arena_memory", "LAYOUTS"]
 
-LAYOUTS = ("separate", "pairs", "fp8-records", "lion-records", "f32-records", "f24-records", "lion-f24-records")
+LAYOUTS = ("separate", "pairs", "fp8-records", "lion-records", "f32-records", "f24-records", "lion-f24-records",
+           "fp8-f24-records")
+IN_PLACE = ("fp8-records", "fp8-f24-records")   # never double-buffered
 
 # Arenas of at least this many bytes follow an allocate/free of their own size (new_states); None: never.
 RECYCLE_MIN_BYTES: int | None = 256 << 20
@@ -57,8 +61,8 @@ def choose_layout(algorithm: str, precision: str, master_precision: str, request
     if requested == "separate" or master_is_param:
         return "separate"
     if master_precision == "fp24":
-        return {("adamw", "bf16"): "f24-records", ("lion", "bf16"): "lion-f24-records"}.get((algorithm, precision),
-                                                                                          "separate")
+        return {("adamw", "bf16"): "f24-records", ("lion", "bf16"): "lion-f24-records",
+                ("adamw", "fp8"): "fp8-f24-records"}.get((algorithm, precision), "separate")
     return {("adamw", "bf16"): "pairs", ("adamw", "fp8"): "fp8-records", ("adamw", "fp32"): "f32-records",
             ("lion", "bf16"): "lion-records"}.get((algorithm, precision), "separate")
 
@@ -645,6 +649,73 @@ class AdamRecordState(_Interleaved):
         return out
 
 
+class AdamF24RecordState(AdamRecordState):
+    """AdamW, FP24 master, FP8 moments: one 640-byte record per 128-element block
+    (ADAMBRIDGE_DT_PACKED_FP8_F24) -- the block's 128 master high halves (BF16 bits) at 0 and its 128
+    low bytes at 256, both in element order, then lane l's m codes at 384 + 16l and v codes at
+    392 + 16l -- plus an FP32 block-scale array per moment.  Updated in place."""
+
+    layout = "fp8-f24-records"
+    master_precision = "fp24"
+    RECORD = 640
+
+    def __init__(self, numel, device, double_buffer: bool = False, memory: list[torch.Tensor] | None = None):
+        self.blocks = F.fp8_blocks(int(numel))
+        rec = memory[0].view(self.blocks, self.RECORD) if memory else \
+            torch.zeros(self.blocks, self.RECORD, dtype=torch.uint8, device=device)
+        _Interleaved.__init__(self, numel, device, ("m", "v"), [rec])   # updated in place: never double-buffered
+        self.scales = {r: torch.ones(self.blocks, dtype=torch.float32, device=device) for r in ("m", "v")}
+
+    @staticmethod
+    def buffer_bytes(numel: int) -> int:
+        return F.fp8_blocks(int(numel)) * AdamF24RecordState.RECORD
+
+    def bind(self, seg):
+        super().bind(seg)
+        seg.p_dtype = _hip.DT_PACKED8_F24
+
+    def _column(self, role):
+        """'p' the hi plane (BF16 bits), 'lo' the lo plane (uint8), 'm' / 'v' the codes, in element order."""
+        if role == "p":
+            return self.current[:, :256].view(torch.bfloat16)
+        if role == "lo":
+            return self.current[:, 256:384]
+        k = 0 if role == "m" else 8
+        return self.current[:, 384:].view(self.blocks, 16, 16)[:, :, k:k + 8]
+
+    def master_plane(self):
+        base = self.current.data_ptr()
+        return _hip.Plane(base, base + 256, self.RECORD, _hip.DT_F24, 7)
+
+    def _planes(self) -> FP24Store:
+        return F24RecordState._planes(self)
+
+    def master_fp32(self):
+        if self.device.type == "cuda":
+            return _Interleaved.master_fp32(self)   # one pass: the record's planes expanded to FP32
+        return self._planes().to_fp32()
+
+    def export_master(self):
+        return self._planes().state_dict()
+
+    def load(self, master=None, moments=None):
+        if master is not None and self.device.type != "cuda":
+            planes = FP24Store(self.numel, device=self.device)
+            load_master_(planes, master)   # FP24 planes as they are; other values rounded to nearest
+            self._put("p", planes.hi)
+            self._put("lo", planes.lo)
+            master = None
+        super().load(master, moments)   # on the device: FP24 planes bit for bit, other values to nearest
+
+    def footprint(self):
+        return 3 * self.numel, self.current.nbytes - 3 * self.numel + sum(s.nbytes for s in self.scales.values())
+
+    def window(self, lo, hi):
+        out = super().window(lo, hi)
+        out["p_lo"] = self._column("lo").reshape(-1)[lo:hi]
+        return out
+
+
 def _bf16_bits(store: MomentStore, device) -> torch.Tensor:
     """A moment's values as BF16 (the store's own bits when it is BF16, nearest-even otherwise)."""
     if isinstance(store, BF16Store):
@@ -655,7 +726,8 @@ def _bf16_bits(store: MomentStore, device) -> torch.Tensor:
 # -------------------------------------------------------------------- building
 
 _INTERLEAVED = {"pairs": PairState, "lion-records": LionRecordState, "fp8-records": AdamRecordState,
-                "f32-records": F32RecordState, "f24-records": F24RecordState, "lion-f24-records": LionF24RecordState}
+                "f32-records": F32RecordState, "f24-records": F24RecordState, "lion-f24-records": LionF24RecordState,
+                "fp8-f24-records": AdamF24RecordState}
 ARENA_ALIGN = 2 << 20
 SMALL_ALIGN = 256
 
@@ -666,7 +738,7 @@ def arena_plan(layout: str, sizes: list[int], double_buffer: bool = False) -> tu
     (norms, biases) are packed at 256-byte boundaries, so that a model of many small tensors does
     not pay 2 MiB for each."""
     cls = _INTERLEAVED[layout]
-    copies = 2 if double_buffer and layout != "fp8-records" else 1
+    copies = 2 if double_buffer and layout not in IN_PLACE else 1
     offsets, total = [], 0
     for n in sizes:
         nbytes = cls.buffer_bytes(n)

@@ -40,7 +40,7 @@ extern "C" {
 enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, ADAMBRIDGE_DT_FP8 = 3,
        ADAMBRIDGE_DT_F24 = 4, ADAMBRIDGE_DT_PACKED = 5, ADAMBRIDGE_DT_PACKED_FP8 = 6,
        ADAMBRIDGE_DT_PACKED_LION = 7, ADAMBRIDGE_DT_PACKED_F32 = 8, ADAMBRIDGE_DT_PACKED_F24 = 9,
-       ADAMBRIDGE_DT_PACKED_LION_F24 = 10 };
+       ADAMBRIDGE_DT_PACKED_LION_F24 = 10, ADAMBRIDGE_DT_PACKED_FP8_F24 = 11 };
 
 /* ADAMBRIDGE_DT_PACKED (p_dtype; no counterpart in the reference): an HBM layout for
  * AdamW with an FP32 master and BF16 moments (mv_dtype DT_BF16).  p points at 16-byte
@@ -89,6 +89,15 @@ enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, AD
 /* ADAMBRIDGE_DT_PACKED_LION_F24 (p_dtype; no counterpart in the reference): the same for Lion with an
  * FP24 master and a BF16 moment: one 1280-byte record per 256 elements, the 256 master high halves
  * (bytes 0 .. 511), the 256 low bytes (512 .. 767) and the 256 m values (768 .. 1279). */
+/* ADAMBRIDGE_DT_PACKED_FP8_F24 (p_dtype; no counterpart in the reference): an HBM layout for AdamW
+ * with an FP24 master and FP8 moments (mv_dtype DT_FP8).  p points at one 640-byte record per
+ * 128-element block, ceil(n/128) records, 16-byte aligned.  The record of block b holds its 128
+ * master high halves (the FP24 hi plane, BF16 bits; bytes 0 .. 255) and its 128 master low bytes
+ * (the lo plane; 256 .. 383), both in element order, then for l = 0 .. 15 the m codes (E4M3) of
+ * elements 128b + 8l + j at 384 + 16l + j and their v codes (E5M2, of sqrt v) at 392 + 16l + j.
+ * Elements past n are padding (codes written as 0, master left as it is).  m_scale and v_scale are
+ * the usual block scales; m, v and p_lo are unused (p_lo must be NULL: updated in place).  Same
+ * arithmetic, rounding and rounding streams as the separate FP8 layout with an FP24 master. */
 enum { ADAMBRIDGE_ALGO_ADAMW = 0, ADAMBRIDGE_ALGO_LION = 1 };
 
 /* Error codes (kernels.c:1537-1553, 1582-1584, 1620-1621), plus the HIP-side ones. */
@@ -145,7 +154,7 @@ typedef struct adambridge_group {
 typedef struct adambridge_segment {
     void* p;                 /* FP32 master, the FP24 hi plane (uint16) when p_dtype is DT_F24, or the
                                 packed state when p_dtype is DT_PACKED / DT_PACKED_FP8 / DT_PACKED_LION /
-                                DT_PACKED_F32 / DT_PACKED_F24 / DT_PACKED_LION_F24 */
+                                DT_PACKED_F32 / DT_PACKED_F24 / DT_PACKED_LION_F24 / DT_PACKED_FP8_F24 */
     uint8_t* p_lo;           /* FP24 lo plane (one byte per element); NULL for FP32; DT_PACKED,
                                 DT_PACKED_LION, DT_PACKED_F32, DT_PACKED_F24 and DT_PACKED_LION_F24: the
                                 destination state
@@ -165,8 +174,8 @@ typedef struct adambridge_segment {
     int32_t mv_dtype;
     int32_t out_dtype;
     int32_t algorithm;
-    int32_t p_dtype;         /* DT_F32 (or 0), DT_F24, DT_PACKED, DT_PACKED_FP8, DT_PACKED_LION, DT_PACKED_F32
-                                DT_PACKED_F24 or DT_PACKED_LION_F24 */
+    int32_t p_dtype;         /* DT_F32 (or 0), DT_F24, DT_PACKED, DT_PACKED_FP8, DT_PACKED_LION, DT_PACKED_F32,
+                                DT_PACKED_F24, DT_PACKED_LION_F24 or DT_PACKED_FP8_F24 */
     int32_t reserved;        /* 0, or ADAMBRIDGE_SEG_OUT_PREVIOUS */
 } adambridge_segment;
 
@@ -190,6 +199,7 @@ ADAMBRIDGE_API int adambridge_abi_version(void);
 #define ADAMBRIDGE_CAP_CONVERT        0x08u   /* adambridge_convert */
 #define ADAMBRIDGE_CAP_CONVERT_PLANE  0x10u   /* adambridge_convert_plane */
 #define ADAMBRIDGE_CAP_STREAM_COPY    0x20u   /* adambridge_stream_copy, adambridge_recycle_device_memory */
+#define ADAMBRIDGE_CAP_FP8_F24_RECORDS 0x40u  /* p_dtype DT_PACKED_FP8_F24 (11) */
 ADAMBRIDGE_API uint32_t adambridge_capabilities(void);
 
 /* kernels.c:1495-1510.  The level whose results are reproduced: its vector

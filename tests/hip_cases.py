@@ -245,18 +245,60 @@ def unpack_records(case: O.Case, rec: np.ndarray) -> None:
         case.arrays[key] = codes[:, :, lo:lo + 8].reshape(-1)[:size].copy()
 
 
+def pack_f8f24_records(case: O.Case) -> np.ndarray:
+    """Separate FP24 master planes + FP8 codes -> ADAMBRIDGE_DT_PACKED_FP8_F24 records (blocks x 640
+    bytes): per block, the 128 high halves (bytes 0 .. 255) and the 128 low bytes (256 .. 383) in
+    element order, then lane l's m codes at 384 + 16l and v codes at 392 + 16l.  Padding masters
+    are set to a fixed pattern so that a test can see the kernel leave them unchanged."""
+    n = case.n
+    nb = max(1, -(-n // 128))
+    hi = np.full(nb * 128, 0xA5A5, np.uint16)
+    hi[:n] = case.arrays["p"].view(np.uint16)
+    lo = np.full(nb * 128, 0x5A, np.uint8)
+    lo[:n] = case.arrays["p_lo"]
+    rec = np.zeros((nb, 640), np.uint8)
+    rec[:, :256] = hi.reshape(nb, 128).view(np.uint8)
+    rec[:, 256:384] = lo.reshape(nb, 128)
+    codes = np.zeros((nb, 16, 16), np.uint8)
+    for key, k in (("m", 0), ("v", 8)):
+        c = np.zeros(nb * 128, np.uint8)
+        src = case.arrays[key]
+        c[:min(src.size, nb * 128)] = src[:nb * 128]
+        codes[:, :, k:k + 8] = c.reshape(nb, 16, 8)
+    rec[:, 384:] = codes.reshape(nb, 256)
+    return rec
+
+
+def unpack_f8f24_records(case: O.Case, rec: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """ADAMBRIDGE_DT_PACKED_FP8_F24 records -> the case's separate master planes and codes (in place);
+    returns the padding masters' (high halves, low bytes) past n."""
+    n, nb = case.n, rec.shape[0]
+    hi = np.ascontiguousarray(rec[:, :256]).view(np.uint16).reshape(-1)
+    lo = np.ascontiguousarray(rec[:, 256:384]).reshape(-1)
+    case.arrays["p"] = hi[:n].view(case.arrays["p"].dtype).copy()
+    case.arrays["p_lo"] = lo[:n].copy()
+    codes = np.ascontiguousarray(rec[:, 384:]).reshape(nb, 16, 16)
+    for key, k in (("m", 0), ("v", 8)):
+        size = case.arrays[key].size
+        case.arrays[key] = codes[:, :, k:k + 8].reshape(-1)[:size].copy()
+    return hi[n:].copy(), lo[n:].copy()
+
+
 def run_hip_records(cases: list[O.Case], width: int = 16, misalign_g: bool = False,
-                    seg_flags: int = 0) -> list[O.Case]:
-    """Like run_hip for AdamW / FP32 master / FP8 moment cases, through the block-record layout
-    (ADAMBRIDGE_DT_PACKED_FP8): pack on the host, one call, unpack the result."""
+                    seg_flags: int = 0, padding: list | None = None) -> list[O.Case]:
+    """Like run_hip for AdamW / FP8 moment cases, through the block-record layouts: FP32 master
+    (ADAMBRIDGE_DT_PACKED_FP8) or FP24 master (ADAMBRIDGE_DT_PACKED_FP8_F24), by the case's p_dtype.
+    Pack on the host, one call, unpack the result; ``padding`` receives each FP24 case's padding
+    masters after the call."""
     kernels = _hip.load()
     work = [c.copy() for c in cases]
     keep, segs = [], []
     by_group = all(c.group is not None for c in work)
     for c in work:
-        assert c.algorithm == O.ADAMW and c.mv_dtype == O.DT_FP8 and c.p_dtype == O.DT_F32
+        assert c.algorithm == O.ADAMW and c.mv_dtype == O.DT_FP8 and c.p_dtype in (O.DT_F32, O.DT_F24)
         O.check_sizes(c)
-        rec = torch.from_numpy(pack_records(c)).cuda()
+        f24 = c.p_dtype == O.DT_F24
+        rec = torch.from_numpy(pack_f8f24_records(c) if f24 else pack_records(c)).cuda()
         g = to_device(c.arrays["g"])
         if misalign_g:
             buf = torch.empty(g.numel() + 1, dtype=g.dtype, device=g.device)
@@ -275,7 +317,8 @@ def run_hip_records(cases: list[O.Case], width: int = 16, misalign_g: bool = Fal
                                  out=out.data_ptr() if out is not None else None,
                                  group=ctypes.pointer(grp) if grp is not None else None, n=c.n, step=c.step,
                                  index=c.index, offset=c.offset, g_dtype=c.g_dtype, mv_dtype=O.DT_FP8,
-                                 out_dtype=c.out_dtype, algorithm=0, p_dtype=_hip.DT_PACKED8, reserved=seg_flags))
+                                 out_dtype=c.out_dtype, algorithm=0,
+                                 p_dtype=_hip.DT_PACKED8_F24 if f24 else _hip.DT_PACKED8, reserved=seg_flags))
     arr = kernels.segment_array([ctypes.pointer(s) for s in segs])
     kernels.set_simd_level(WIDTH_LEVEL[width])
     try:
@@ -293,7 +336,12 @@ def run_hip_records(cases: list[O.Case], width: int = 16, misalign_g: bool = Fal
         if misalign_g:
             next(it)
         rec, g, ms, vs, out, grp = (next(it) for _ in range(6))
-        unpack_records(c, rec.cpu().numpy())
+        if c.p_dtype == O.DT_F24:
+            pad = unpack_f8f24_records(c, rec.cpu().numpy())
+            if padding is not None:
+                padding.append(pad)
+        else:
+            unpack_records(c, rec.cpu().numpy())
         c.arrays["m_scale"] = from_device(ms, c.arrays["m_scale"])
         c.arrays["v_scale"] = from_device(vs, c.arrays["v_scale"])
         if out is not None:

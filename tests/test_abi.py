@@ -53,7 +53,8 @@ def test_header_codes_match_the_python_mirror():
     mirror = {"DT_NONE": _hip.DT_NONE, "DT_F32": _hip.DT_F32, "DT_BF16": _hip.DT_BF16, "DT_FP8": _hip.DT_FP8,
               "DT_F24": _hip.DT_F24, "DT_PACKED": _hip.DT_PACKED, "DT_PACKED_FP8": _hip.DT_PACKED8,
               "DT_PACKED_LION": _hip.DT_PACKED_LION, "DT_PACKED_F32": _hip.DT_PACKED_F32,
-              "DT_PACKED_F24": _hip.DT_PACKED_F24, "DT_PACKED_LION_F24": _hip.DT_PACKED_LION_F24}
+              "DT_PACKED_F24": _hip.DT_PACKED_F24, "DT_PACKED_LION_F24": _hip.DT_PACKED_LION_F24,
+              "DT_PACKED_FP8_F24": _hip.DT_PACKED8_F24}
     assert codes == mirror
     flag = re.search(r"#define ADAMBRIDGE_SEG_OUT_PREVIOUS (\d+)", text)
     assert flag and int(flag.group(1)) == _hip.SEG_OUT_PREVIOUS
@@ -97,7 +98,7 @@ def _segment_variants():
     return [
         ("negative n", m(n=-1), -1),
         ("unknown algorithm", m(algorithm=5), -12),
-        ("unknown master format", m(p_dtype=11), -13),
+        ("unknown master format", m(p_dtype=12), -13),
         ("no master", m(p=None), -2),
         ("no gradient", m(g=None), -2),
         ("no first moment", m(m=None), -2),
@@ -217,6 +218,7 @@ def test_convert_plane_argument_codes_and_capabilities():
     assert rc(P(base, None, -16, F32, 1), ok) == -1
     assert rc(P(base, None, 18, F32, 1), ok) == -14
     assert rc(P(base, base + 1, 1792, F24, 8), P(base, None, 16, F32, 1)) == 0
+    assert rc(P(base, base + 256, 640, F24, 7), P(base, None, 16, F32, 1)) == 0   # an FP8 record's FP24 planes
     caps = lib.adambridge_capabilities()
     assert caps == sum(_hip.CAPABILITIES.values())
     assert lib.adambridge_abi_version() == 5

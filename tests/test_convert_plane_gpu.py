@@ -111,6 +111,7 @@ def _values(n: int, seed: int) -> torch.Tensor:
 LAYOUTS = [("pairs", "adamw", "bf16", "fp32"), ("lion-records", "lion", "bf16", "fp32"),
            ("f32-records", "adamw", "fp32", "fp32"), ("f24-records", "adamw", "bf16", "fp24"),
            ("lion-f24-records", "lion", "bf16", "fp24"), ("fp8-records", "adamw", "fp8", "fp32"),
+           ("fp8-f24-records", "adamw", "fp8", "fp24"),
            ("separate", "adamw", "bf16", "fp24"), ("separate", "adamw", "fp8", "fp32")]
 
 
@@ -149,9 +150,10 @@ def test_master_planes_of_every_layout(layout, algorithm, precision, master, n):
         i = np.arange(n, dtype=np.int64)
         if layout == "fp8-records":
             offs = [(i >> 7) * 768 + np.where(i & 4, 256, 0) + ((i >> 3) & 15) * 16 + (i & 3) * 4 + k for k in range(4)]
-        elif master == "fp24":
-            at = (i >> 8) * plane.stride + (i & 255) * 2
-            offs = [at, at + 1, (i >> 8) * plane.stride + 512 + (i & 255)]
+        elif master == "fp24":   # hi plane at the record's start, lo plane right after it
+            g = plane.group_log2
+            at = (i >> g) * plane.stride + (i & ((1 << g) - 1)) * 2
+            offs = [at, at + 1, (i >> g) * plane.stride + (2 << g) + (i & ((1 << g) - 1))]
         else:
             at = (i >> plane.group_log2) * plane.stride + (i & ((1 << plane.group_log2) - 1)) * 4
             offs = [at + k for k in range(4)]

@@ -199,7 +199,7 @@ def _every_element(name: str) -> None:
         bench.use_step_grads(cfg, params, warm + 1)
         torch.cuda.synchronize()
         if master == "fp24":
-            want = "f24-records" if cfg["precision"] == "bf16" else "separate"
+            want = {"bf16": "f24-records", "fp8": "fp8-f24-records"}.get(cfg["precision"], "separate")
             assert all(s.state.layout == want for s in opt._ordered)
         before = {s.index: {k: v.clone() for k, v in s.state.window(0, s.numel).items()} for s in opt._ordered}
         opt.step()
