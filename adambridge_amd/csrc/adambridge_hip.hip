@@ -857,7 +857,7 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     }
 }
 
-template <int ALGO, int PT, int GT, int OT, bool SR, bool PREV>
+template <int ALGO, int PT, int GT, int OT, bool SR, bool PREV, bool WIDE>
 __device__ __forceinline__ void update_tile_fp8(const DevSeg& s, int64_t tile, int64_t T)
 {
     constexpr bool kLion = ALGO == ALGO_LION;
@@ -867,28 +867,31 @@ __device__ __forceinline__ void update_tile_fp8(const DevSeg& s, int64_t tile, i
     const bool vec = (s.flags & kVec) != 0;
     // blocks wholly in the fused range (AdamW's scalar tail, if any, is the segment's last n mod W)
     const int64_t full_end = kLion ? s.n : s.n_main;
-    // The smallest tile (the default) holds one 128-element block per 16-lane group: no loop and
-    // no loop-carried addresses (measured 1.3% faster on the 7B FP8 step in a fast HBM placement,
-    // equal in a slow one)
-    if (T == kFp8Quantum) {
+    if constexpr (!WIDE) {
+        // The smallest tile (the default) holds one 128-element block per 16-lane group: no loop and
+        // no loop-carried addresses (measured 1.3% faster on the 7B FP8 step in a fast HBM placement,
+        // equal in a slow one)
         const int64_t base = (tile - s.tile_begin) * kFp8Quantum;
         const int64_t b0 = base + goff;
         if (b0 >= s.n) return;
         if (vec && b0 + kFp8Block <= full_end) fp8_block<ALGO, PT, GT, OT, SR, true, PREV>(s, c, base, off);
         else fp8_block<ALGO, PT, GT, OT, SR, false, PREV>(s, c, base, off);
-        return;
-    }
-    const int64_t lo = (tile - s.tile_begin) * T;
-    const int64_t hi = lo + T < s.n ? lo + T : s.n;
-    // larger tiles (ADAMBRIDGE_TILE_FP8): each pass covers the next 16 blocks of the tile
-    for (int64_t base = lo; base + goff < hi; base += kFp8Quantum) {
-        const int64_t b0 = base + goff;
-        if (vec && b0 + kFp8Block <= full_end) fp8_block<ALGO, PT, GT, OT, SR, true, PREV>(s, c, base, off);
-        else fp8_block<ALGO, PT, GT, OT, SR, false, PREV>(s, c, base, off);
+    } else {
+        const int64_t lo = (tile - s.tile_begin) * T;
+        const int64_t hi = lo + T < s.n ? lo + T : s.n;
+        // larger tiles (ADAMBRIDGE_TILE_FP8): each pass covers the next 16 blocks of the tile
+        for (int64_t base = lo; base + goff < hi; base += kFp8Quantum) {
+            const int64_t b0 = base + goff;
+            if (vec && b0 + kFp8Block <= full_end) fp8_block<ALGO, PT, GT, OT, SR, true, PREV>(s, c, base, off);
+            else fp8_block<ALGO, PT, GT, OT, SR, false, PREV>(s, c, base, off);
+        }
     }
 }
 
-template <int ALGO, int PT, int GT, int OT>
+// WIDE: the launch's tiles hold more than one block per 16-lane group (ADAMBRIDGE_TILE_FP8 above
+// 2048).  The default tile takes the kernel without the loop: 58 VGPRs for the FP8-record and FP24
+// variants (8 wavefronts per SIMD) where the loop in the same kernel made it 89-102 (5).
+template <int ALGO, int PT, int GT, int OT, bool WIDE>
 __global__ __launch_bounds__(kThreads) void k_update_fp8(Launch L)
 {
     const int64_t tile = block_tile(L);
@@ -898,13 +901,13 @@ __global__ __launch_bounds__(kThreads) void k_update_fp8(Launch L)
     // code cost this VALU-heavy kernel 6% (measured on the 7B FP8 step)
     if (s.flags & kPrev) {
         if constexpr (OT != DT_NONE) {
-            if (s.flags & kSR) update_tile_fp8<ALGO, PT, GT, OT, true, true>(s, tile, L.tile);
-            else update_tile_fp8<ALGO, PT, GT, OT, false, true>(s, tile, L.tile);
+            if (s.flags & kSR) update_tile_fp8<ALGO, PT, GT, OT, true, true, WIDE>(s, tile, L.tile);
+            else update_tile_fp8<ALGO, PT, GT, OT, false, true, WIDE>(s, tile, L.tile);
         }
         return;
     }
-    if (s.flags & kSR) update_tile_fp8<ALGO, PT, GT, OT, true, false>(s, tile, L.tile);
-    else update_tile_fp8<ALGO, PT, GT, OT, false, false>(s, tile, L.tile);
+    if (s.flags & kSR) update_tile_fp8<ALGO, PT, GT, OT, true, false, WIDE>(s, tile, L.tile);
+    else update_tile_fp8<ALGO, PT, GT, OT, false, false, WIDE>(s, tile, L.tile);
 }
 
 // ------------------------------------------------- packed AdamW state kernel
@@ -1399,27 +1402,29 @@ using KernelFn = void (*)(Launch);
 // mv 0/1/2 = F32/BF16/FP8, pt 0/1 = F32/F24, gt 0/1 = F32/BF16, ot 0/1/2 = NONE/F32/BF16.
 constexpr int kNumKernels = 2 * 3 * 2 * 2 * 3;
 
-template <int ALGO, int MVI, int PTI, int GTI, int OTI>
+// WIDE: the FP8 kernels' form for tiles of more than one block per 16-lane group (the other
+// kernels have one form).
+template <int ALGO, int MVI, int PTI, int GTI, int OTI, bool WIDE>
 constexpr KernelFn pick()
 {
     constexpr int PT = PTI ? DT_F24 : DT_F32;
     constexpr int GT = GTI ? DT_BF16 : DT_F32;
     constexpr int OT = OTI == 0 ? DT_NONE : OTI == 1 ? DT_F32 : DT_BF16;
-    if constexpr (MVI == 2) return &k_update_fp8<ALGO, PT, GT, OT>;
+    if constexpr (MVI == 2) return &k_update_fp8<ALGO, PT, GT, OT, WIDE>;
     else return &k_update<ALGO, MVI ? DT_BF16 : DT_F32, PT, GT, OT>;
 }
 
-template <int I>
+template <int I, bool WIDE>
 constexpr KernelFn entry()
 {
     constexpr int ot = I % 3, gt = (I / 3) % 2, pt = (I / 6) % 2, mv = (I / 12) % 3, algo = I / 36;
-    return pick<algo, mv, pt, gt, ot>();
+    return pick<algo, mv, pt, gt, ot, WIDE>();
 }
 
-template <int... I>
+template <bool WIDE, int... I>
 constexpr auto make_table(std::integer_sequence<int, I...>)
 {
-    return std::array<KernelFn, sizeof...(I)>{entry<I>()...};
+    return std::array<KernelFn, sizeof...(I)>{entry<I, WIDE>()...};
 }
 
 // Packed-state kernels follow the table: index kNumKernels + gt * 3 + ot.
@@ -1439,17 +1444,18 @@ constexpr auto make_packed_table(std::integer_sequence<int, I...>)
 }
 
 // FP8-record kernels (AdamW) follow: index kNumKernels + kNumPacked + gt * 3 + ot.
-template <int I>
+template <int I, bool WIDE>
 constexpr KernelFn packed8_entry()
 {
     constexpr int ot = I % 3, gt = I / 3;
-    return &k_update_fp8<ALGO_ADAMW, DT_PACKED8, gt ? DT_BF16 : DT_F32, ot == 0 ? DT_NONE : ot == 1 ? DT_F32 : DT_BF16>;
+    return &k_update_fp8<ALGO_ADAMW, DT_PACKED8, gt ? DT_BF16 : DT_F32, ot == 0 ? DT_NONE : ot == 1 ? DT_F32 : DT_BF16,
+                         WIDE>;
 }
 
-template <int... I>
+template <bool WIDE, int... I>
 constexpr auto make_packed8_table(std::integer_sequence<int, I...>)
 {
-    return std::array<KernelFn, sizeof...(I)>{packed8_entry<I>()...};
+    return std::array<KernelFn, sizeof...(I)>{packed8_entry<I, WIDE>()...};
 }
 
 // Lion-record kernels follow: index kNumKernels + 2 * kNumPacked + gt * 3 + ot.
@@ -1466,9 +1472,11 @@ constexpr auto make_lion_rec_table(std::integer_sequence<int, I...>)
     return std::array<KernelFn, sizeof...(I)>{lion_rec_entry<I>()...};
 }
 
-static const auto kKernels = make_table(std::make_integer_sequence<int, kNumKernels>{});
+static const auto kKernels = make_table<false>(std::make_integer_sequence<int, kNumKernels>{});
+static const auto kKernelsWide = make_table<true>(std::make_integer_sequence<int, kNumKernels>{});
 static const auto kPacked = make_packed_table(std::make_integer_sequence<int, kNumPacked>{});
-static const auto kPacked8 = make_packed8_table(std::make_integer_sequence<int, kNumPacked>{});
+static const auto kPacked8 = make_packed8_table<false>(std::make_integer_sequence<int, kNumPacked>{});
+static const auto kPacked8Wide = make_packed8_table<true>(std::make_integer_sequence<int, kNumPacked>{});
 static const auto kLionRec = make_lion_rec_table(std::make_integer_sequence<int, kNumPacked>{});
 
 // FP32-moment record kernels (AdamW) follow: index kNumKernels + 3 * kNumPacked + gt * 3 + ot.
@@ -1520,20 +1528,22 @@ constexpr auto make_lion_f24rec_table(std::integer_sequence<int, I...>)
 static const auto kLionF24Rec = make_lion_f24rec_table(std::make_integer_sequence<int, kNumPacked>{});
 
 // FP8 records with an FP24 master (AdamW) follow: index kNumKernels + 6 * kNumPacked + gt * 3 + ot.
-template <int I>
+template <int I, bool WIDE>
 constexpr KernelFn packed8_f24_entry()
 {
     constexpr int ot = I % 3, gt = I / 3;
-    return &k_update_fp8<ALGO_ADAMW, DT_PACKED8_F24, gt ? DT_BF16 : DT_F32, ot == 0 ? DT_NONE : ot == 1 ? DT_F32 : DT_BF16>;
+    return &k_update_fp8<ALGO_ADAMW, DT_PACKED8_F24, gt ? DT_BF16 : DT_F32, ot == 0 ? DT_NONE : ot == 1 ? DT_F32 : DT_BF16,
+                         WIDE>;
 }
 
-template <int... I>
+template <bool WIDE, int... I>
 constexpr auto make_packed8_f24_table(std::integer_sequence<int, I...>)
 {
-    return std::array<KernelFn, sizeof...(I)>{packed8_f24_entry<I>()...};
+    return std::array<KernelFn, sizeof...(I)>{packed8_f24_entry<I, WIDE>()...};
 }
 
-static const auto kPacked8F24 = make_packed8_f24_table(std::make_integer_sequence<int, kNumPacked>{});
+static const auto kPacked8F24 = make_packed8_f24_table<false>(std::make_integer_sequence<int, kNumPacked>{});
+static const auto kPacked8F24Wide = make_packed8_f24_table<true>(std::make_integer_sequence<int, kNumPacked>{});
 
 // Kernel family of a table index: the FP8 block kernel, or a two-element-per-lane kernel.
 inline bool kernel_is_fp8(int index)
@@ -1541,6 +1551,31 @@ inline bool kernel_is_fp8(int index)
     if (index < kNumKernels) return (index / 12) % 3 == 2;
     return (index >= kNumKernels + kNumPacked && index < kNumKernels + 2 * kNumPacked) ||
            index >= kNumKernels + 6 * kNumPacked;
+}
+
+// Dynamic LDS (unused) per workgroup of a launch of kernel `index`: it caps the workgroups a CU holds.
+// The AdamW FP8 kernels with an FP32 master (separate arrays or block records) take 32 KiB, so at most
+// 5 workgroups (20 wavefronts) per CU: on the 7B list in FP8 records 17.57 ms per launch at 5 per
+// CU against 18.27 at 6, 18.56 at 7 and 18.73 at 8 (what their 58 VGPRs allow), 17.66 at 4 and
+// 21.64 at 3 (interleaved in one process) -- more wavefronts streaming at once cost HBM more
+// than they hide.  The FP24-master FP8 kernels, bound by their VALU, are not capped (16.66 ms at 8
+// per CU; 16.55 at 7, 16.65 at 6, 17.91 at 5), nor are the other kernels.
+inline size_t launch_lds(int index)
+{
+    constexpr size_t kCap5 = 32 * 1024;   // 160 KiB of LDS per CU: 5 workgroups
+    if (index < kNumKernels) {
+        const int pt = (index / 6) % 2, mv = (index / 12) % 3, algo = index / 36;
+        return algo == ALGO_ADAMW && mv == 2 && pt == 0 ? kCap5 : 0;
+    }
+    return index >= kNumKernels + kNumPacked && index < kNumKernels + 2 * kNumPacked ? kCap5 : 0;
+}
+
+// The FP8 kernels' form for tiles of more than one block per 16-lane group (kernel_is_fp8(index)).
+inline KernelFn wide_kernel_at(int index)
+{
+    if (index < kNumKernels) return kKernelsWide[index];
+    if (index < kNumKernels + 2 * kNumPacked) return kPacked8Wide[index - kNumKernels - kNumPacked];
+    return kPacked8F24Wide[index - kNumKernels - 6 * kNumPacked];
 }
 
 inline KernelFn kernel_at(int index)
