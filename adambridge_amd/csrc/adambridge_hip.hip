@@ -890,7 +890,10 @@ __device__ __forceinline__ void update_tile_fp8(const DevSeg& s, int64_t tile, i
 
 // WIDE: the launch's tiles hold more than one block per 16-lane group (ADAMBRIDGE_TILE_FP8 above
 // 2048).  The default tile takes the kernel without the loop: 58 VGPRs for the FP8-record and FP24
-// variants (8 wavefronts per SIMD) where the loop in the same kernel made it 89-102 (5).
+// variants, room for 8 wavefronts per SIMD, where the loop in the same kernel made it 89-102 (5).
+// The FP24-master forms, bound by their VALU, use all 8: the 7B list with an FP24 master took
+// 16.52 ms per launch against 18.5-19.0 at 5.  (launch_lds holds the FP32-master AdamW forms at 6
+// workgroups per CU.)
 template <int ALGO, int PT, int GT, int OT, bool WIDE>
 __global__ __launch_bounds__(kThreads) void k_update_fp8(Launch L)
 {
@@ -1553,21 +1556,30 @@ inline bool kernel_is_fp8(int index)
            index >= kNumKernels + 6 * kNumPacked;
 }
 
-// Dynamic LDS (unused) per workgroup of a launch of kernel `index`: it caps the workgroups a CU holds.
-// The AdamW FP8 kernels with an FP32 master (separate arrays or block records) take 32 KiB, so at most
-// 5 workgroups (20 wavefronts) per CU: on the 7B list in FP8 records 17.57 ms per launch at 5 per
-// CU against 18.27 at 6, 18.56 at 7 and 18.73 at 8 (what their 58 VGPRs allow), 17.66 at 4 and
-// 21.64 at 3 (interleaved in one process) -- more wavefronts streaming at once cost HBM more
-// than they hide.  The FP24-master FP8 kernels, bound by their VALU, are not capped (16.66 ms at 8
-// per CU; 16.55 at 7, 16.65 at 6, 17.91 at 5), nor are the other kernels.
+// Dynamic LDS (unused) per workgroup of a launch of kernel `index`: it caps the workgroups a CU holds
+// (160 KiB of LDS per CU).  These kernels need 45-58 VGPRs, which would allow 8 workgroups (32
+// wavefronts) per CU; with 6 the AdamW FP8 kernels with an FP32 master and the FP32-record kernel
+// move their bytes faster.  Measured on MI355X through bench.py's path (arena-placed state, one
+// launch per step; ms per launch, two passes each, interleaved in one process):
+//   - FP8 records, the 7B list (291 tensors): 6 workgroups per CU 17.62-17.70, 8: 17.82-17.97,
+//     5: 18.01-18.04;
+//   - FP32 records, the 7B list: 6: 29.35, 8: 29.46-29.50, 5: 29.44-29.50;
+//   - FP32 records, one 16.8M-element tensor (512-element tiles, two active wavefronts per
+//     workgroup; a lone launch, interleaved): 6: 0.078, 8: 0.085, 5: 0.087.
+// Lion records at the 1.5B list (338 tensors) run alike with 6 or 8 (4.00-4.03) and lose 13% with 5
+// (4.58-4.61): the segment search each workgroup makes first is hidden by fewer others there.  The
+// BF16 pairs lose with fewer workgroups (the 0.5B list: 1.76 against 1.67 ms with 6), and the
+// FP24-master kernels, bound by their VALU, keep 8 (FP8 with an FP24 master in records, the 7B list:
+// 8 per CU 16.66, 7: 16.55, 6: 16.65, 5: 17.91).
 inline size_t launch_lds(int index)
 {
-    constexpr size_t kCap5 = 32 * 1024;   // 160 KiB of LDS per CU: 5 workgroups
+    constexpr size_t kCap6 = 24 * 1024;   // 6 workgroups of 24 KiB in 160 KiB; 7 would need 168
     if (index < kNumKernels) {
         const int pt = (index / 6) % 2, mv = (index / 12) % 3, algo = index / 36;
-        return algo == ALGO_ADAMW && mv == 2 && pt == 0 ? kCap5 : 0;
+        return algo == ALGO_ADAMW && mv == 2 && pt == 0 ? kCap6 : 0;
     }
-    return index >= kNumKernels + kNumPacked && index < kNumKernels + 2 * kNumPacked ? kCap5 : 0;
+    const int family = (index - kNumKernels) / kNumPacked;   // 1: FP8 records, 3: FP32 records
+    return family == 1 || family == 3 ? kCap6 : 0;
 }
 
 // The FP8 kernels' form for tiles of more than one block per 16-lane group (kernel_is_fp8(index)).
