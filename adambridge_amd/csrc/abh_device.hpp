@@ -43,11 +43,58 @@ __device__ __forceinline__ uint32_t hash32(uint32_t x)
 // a % 8 == 0 the streams of a .. a + 7 are hash32_tail(hash32_head(a ^ stream) ^ k), k < 8:
 // one head per group of 8.
 __device__ __forceinline__ uint32_t hash32_head(uint32_t x) { return x ^ (x >> 16); }
-__device__ __forceinline__ uint32_t hash32_tail(uint32_t x)
+// hash32_tail after its first multiplication: hash32_tail(x) == hash32_tail_mul(x * 0x7feb352d).
+__device__ __forceinline__ uint32_t hash32_tail_mul(uint32_t x)
 {
-    x *= 0x7feb352du;
     x = (x ^ (x >> 15)) * 0x846ca68bu;
     return x ^ (x >> 16);
+}
+__device__ __forceinline__ uint32_t hash32_tail(uint32_t x) { return hash32_tail_mul(x * 0x7feb352du); }
+
+// Whether a wavefront's lanes agree in bits 16-18 of their rounding index, and those bits (see hash8).
+struct Wave8 {
+    bool uniform;
+    uint32_t hi3;
+};
+
+// The rounding bits of the 8 elements idx .. idx + 7 (idx % 8 == 0) in stream `seed`:
+// r[k] = hash32((idx + k) ^ seed).  idx + k == idx ^ k, so the 8 share one head h (hash32_head
+// commutes with xor by k < 2^16) and the tails start from (h ^ k) * 0x7feb352d.  Where the
+// wavefront's indices agree in bits 16-18 (w), h's low 3 bits are the wavefront's
+// c = (seed ^ seed >> 16 ^ bits 16-18) & 7 (the index's own low 3 bits are 0), so
+// h ^ k = (h & ~7) + (c ^ k), and the 8 products are (h & ~7) * 0x7feb352d plus the
+// wavefront-uniform (c ^ k) * 0x7feb352d: a scalar product and one vector add each, in place of a
+// vector xor and a vector multiply.
+__device__ __forceinline__ void hash8(uint32_t idx, uint32_t seed, const Wave8& w, uint32_t (&r)[8])
+{
+    constexpr uint32_t kMul = 0x7feb352du;
+    const uint32_t head = hash32_head(idx ^ seed);
+    uint32_t x[8];
+    if (w.uniform) {
+        const uint32_t c = (seed ^ (seed >> 16) ^ w.hi3) & 7u;
+        const uint32_t a = (head & ~7u) * kMul;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            // the uniform product as an opaque scalar: otherwise a + b * kMul is folded back into
+            // ((head & ~7) + b) * kMul, one vector multiply per element again
+            uint32_t b = (c ^ (uint32_t)k) * kMul;
+            asm volatile("" : "+s"(b));
+            x[k] = a + b;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[k] = (head ^ (uint32_t)k) * kMul;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) r[k] = hash32_tail_mul(x[k]);
+}
+
+// Wave8 of this lane's index (the first active lane's bits stand for the wavefront's).
+__device__ __forceinline__ Wave8 wave8_of(uint32_t idx)
+{
+    const uint32_t hi3 = (idx >> 16) & 7u;
+    const uint32_t first = __builtin_amdgcn_readfirstlane(hi3);
+    return Wave8{__builtin_amdgcn_ballot_w64(hi3 != first) == 0, first};
 }
 
 // BF16 bits of x, nearest-even, NaN quietened (kernels.c:108-112), in the low half: the rule

@@ -257,15 +257,12 @@ __device__ __forceinline__ void load_master8(const void* p, const uint8_t* lo, f
 // stored.  idx % 8 == 0 (the FP8 kernel's lanes start at multiples of 8 within segments that start
 // at multiples of 128), so idx + k == idx ^ k and the 8 rounding draws share one hash head.
 template <int PT, bool SR>
-__device__ __forceinline__ void store_master8(void* p, uint8_t* lo, float (&x)[8], uint32_t idx, uint32_t seed)
+__device__ __forceinline__ void store_master8(void* p, uint8_t* lo, float (&x)[8], uint32_t idx, uint32_t seed,
+                                              const Wave8& w)
 {
     if constexpr (PT == DT_F24) {
         uint32_t r[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
-        if constexpr (SR) {
-            const uint32_t head = hash32_head(idx ^ seed);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) r[k] = hash32_tail(head ^ (uint32_t)k);
-        }
+        if constexpr (SR) hash8(idx, seed, w, r);
         // f24_round: the add and the cut, and a NaN quietened instead; the NaN fix-up runs only
         // where some lane of the wavefront holds one (a uniform test on the compares' lane masks)
         uint64_t nans = 0;
@@ -605,13 +602,12 @@ __device__ __forceinline__ bool hw_range8(const float (&x)[8])
 // be recomputed in software).  idx % 8 == 0: FP8 segments start at multiples of 128 elements and
 // a lane's group at a multiple of 8, so the 8 rounding streams share one hash head.
 template <bool E5M2, bool SR>
-__device__ __forceinline__ void hw_codes8(const float (&x)[8], uint32_t idx, uint32_t seed, uint32_t (&q)[2])
+__device__ __forceinline__ void hw_codes8(const float (&x)[8], uint32_t idx, uint32_t seed, const Wave8& w,
+                                          uint32_t (&q)[2])
 {
     if constexpr (SR) {
-        const uint32_t head = hash32_head(idx ^ seed);
         uint32_t r[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) r[k] = hash32_tail(head ^ (uint32_t)k);
+        hash8(idx, seed, w, r);
         uint32_t w = fp8_hw_sr<E5M2, 0>(x[0], r[0], 0u);
         w = fp8_hw_sr<E5M2, 1>(x[1], r[1], w);
         w = fp8_hw_sr<E5M2, 2>(x[2], r[2], w);
@@ -666,6 +662,7 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     uint8_t* const vq = static_cast<uint8_t*>(s.v);
     const int64_t e0 = base + off;
     const uint32_t idx = s.idx0 + (uint32_t)e0;
+    const Wave8 w8 = SR ? wave8_of(idx) : Wave8{false, 0u};   // for hash8
     const bool full = FULL || (vec && e0 + 8 <= n);
     const uint32_t lane = (off >> 3) & 15u;         // within the block's 16
     const uint32_t blk = off >> 7;                   // the block within this pass
@@ -748,7 +745,7 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     }
     if (full) {
         const uint32_t o = fresh(off);
-        store_master8<kMaster, SR>(pm(o), pl(o), p, idx, s.seed_p);
+        store_master8<kMaster, SR>(pm(o), pl(o), p, idx, s.seed_p, w8);
         if constexpr (!PREV) store_out8<OT>(po(o), p);
     } else {
 #pragma unroll
@@ -814,10 +811,10 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     uint32_t qm[2] = {0u, 0u}, qv[2] = {0u, 0u};
     bool soft_m = true, soft_v = !kLion;
     if constexpr (FULL) {
-        hw_codes8<false, SR>(mt, idx, s.seed_m, qm);
+        hw_codes8<false, SR>(mt, idx, s.seed_m, w8, qm);
         soft_m = !(m_plain ? (!SR || m_low >= quot_m_offset(scm * 0x1p-6f)) : hw_range8<false, SR>(mt));
         if constexpr (!kLion) {
-            hw_codes8<true, SR>(sq, idx, s.seed_v, qv);
+            hw_codes8<true, SR>(sq, idx, s.seed_v, w8, qv);
             soft_v = !(v_pos ? (!SR || u_min >= scu * 0x1p-14f) : hw_range8<true, SR>(sq));
         }
     }
