@@ -57,19 +57,18 @@ struct Wave8 {
     uint32_t hi3;
 };
 
-// The rounding bits of the 8 elements idx .. idx + 7 (idx % 8 == 0) in stream `seed`:
-// r[k] = hash32((idx + k) ^ seed).  idx + k == idx ^ k, so the 8 share one head h (hash32_head
-// commutes with xor by k < 2^16) and the tails start from (h ^ k) * 0x7feb352d.  Where the
-// wavefront's indices agree in bits 16-18 (w), h's low 3 bits are the wavefront's
-// c = (seed ^ seed >> 16 ^ bits 16-18) & 7 (the index's own low 3 bits are 0), so
+// The rounding bits of the 8 elements idx .. idx + 7 (idx % 8 == 0) in stream `seed` are
+// hash32((idx + k) ^ seed).  idx + k == idx ^ k, so the 8 share one head h (hash32_head commutes
+// with xor by k < 2^16) and the tails start from (h ^ k) * 0x7feb352d: hash8_mul gives those 8
+// products.  Where the wavefront's indices agree in bits 16-18 (w), h's low 3 bits are the
+// wavefront's c = (seed ^ seed >> 16 ^ bits 16-18) & 7 (the index's own low 3 bits are 0), so
 // h ^ k = (h & ~7) + (c ^ k), and the 8 products are (h & ~7) * 0x7feb352d plus the
 // wavefront-uniform (c ^ k) * 0x7feb352d: a scalar product and one vector add each, in place of a
 // vector xor and a vector multiply.
-__device__ __forceinline__ void hash8(uint32_t idx, uint32_t seed, const Wave8& w, uint32_t (&r)[8])
+__device__ __forceinline__ void hash8_mul(uint32_t idx, uint32_t seed, const Wave8& w, uint32_t (&x)[8])
 {
     constexpr uint32_t kMul = 0x7feb352du;
     const uint32_t head = hash32_head(idx ^ seed);
-    uint32_t x[8];
     if (w.uniform) {
         const uint32_t c = (seed ^ (seed >> 16) ^ w.hi3) & 7u;
         const uint32_t a = (head & ~7u) * kMul;
@@ -85,8 +84,34 @@ __device__ __forceinline__ void hash8(uint32_t idx, uint32_t seed, const Wave8& 
 #pragma unroll
         for (int k = 0; k < 8; ++k) x[k] = (head ^ (uint32_t)k) * kMul;
     }
+}
+
+// r[k] = hash32((idx + k) ^ seed), k < 8.
+__device__ __forceinline__ void hash8(uint32_t idx, uint32_t seed, const Wave8& w, uint32_t (&r)[8])
+{
+    uint32_t x[8];
+    hash8_mul(idx, seed, w, x);
 #pragma unroll
     for (int k = 0; k < 8; ++k) r[k] = hash32_tail_mul(x[k]);
+}
+
+// The low byte of hash32's last step, (y ^ (y >> 16)) & 0xff, in one v_xor_b32 with sub-dword
+// operands (the upper half of y as the second source, the result's byte 0 kept and the rest zero).
+__device__ __forceinline__ uint32_t hash_low8(uint32_t y)
+{
+    uint32_t r;
+    asm("v_xor_b32_sdwa %0, %1, %1 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_1"
+        : "=v"(r) : "v"(y));
+    return r;
+}
+
+// r[k] = hash32((idx + k) ^ seed) & 0xff, k < 8: the FP24 master's rounding bits.
+__device__ __forceinline__ void hash8_low8(uint32_t idx, uint32_t seed, const Wave8& w, uint32_t (&r)[8])
+{
+    uint32_t x[8];
+    hash8_mul(idx, seed, w, x);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) r[k] = hash_low8((x[k] ^ (x[k] >> 15)) * 0x846ca68bu);
 }
 
 // Wave8 of this lane's index (the first active lane's bits stand for the wavefront's).
@@ -337,23 +362,24 @@ __device__ __forceinline__ float adamw(float p, float g, float& m, float& v, con
     return adamw<FUSED>(p, g, m, v, c, sq);
 }
 
-// Correctly rounded square root for 2^-100 <= x < 2^100 in 5 instructions (the general sqrtf
-// also scales denormals and handles 0, infinity and NaN): one Newton correction of the hardware
-// root, s + (x - s^2) * rsq(x) / 2.  v_sqrt_f32 is within one ulp of the root there, so the
-// residual x - s^2 is a float and one fused multiply-add gives it exactly; v_rsq_f32 supplies the
-// derivative.  The result is the nearest root for every x in the range, decided in exact integer
-// arithmetic by adambridge_check_conversions (check 5).  (The same correction with
-// v_rcp_f32(s) / 2 in place of rsq(x) / 2 misses the nearest root for 100 inputs of the range.)
+// Correctly rounded square root for 2^-100 <= x < 2^100 in 5 instructions, one of them a
+// transcendental (the general sqrtf also scales denormals and handles 0, infinity and NaN): from
+// y = rsq(x), the root g = x y and one Newton correction g + (x - g^2) y / 2.  g is within a few
+// ulp of the root there, so the residual x - g^2 is a float and one fused multiply-add gives it
+// exactly.  The result is the nearest root for every x in the range, decided in exact integer
+// arithmetic by adambridge_check_conversions (check 5).  (An earlier form corrected v_sqrt_f32's
+// root with the same step -- two transcendentals, also exact; the correction with v_rcp_f32(s) / 2
+// in place of rsq(x) / 2 misses the nearest root for 100 inputs of the range.)
 constexpr uint32_t kSqrtMidLo = 0x0d800000u, kSqrtMidSpan = 0x71800000u - 0x0d800000u;
 
 __device__ __forceinline__ bool sqrt_mid_range(float x) { return fbits(x) - kSqrtMidLo < kSqrtMidSpan; }
 
 __device__ __forceinline__ float sqrt_mid(float x)
 {
-    const float s = __builtin_amdgcn_sqrtf(x);
-    const float r = __builtin_fmaf(-s, s, x);
-    const float h = __builtin_amdgcn_rsqf(x) * 0.5f;
-    return __builtin_fmaf(r, h, s);
+    const float y = __builtin_amdgcn_rsqf(x);
+    const float g = x * y;
+    const float r = __builtin_fmaf(-g, g, x);
+    return __builtin_fmaf(r, y * 0.5f, g);
 }
 
 // The fused AdamW step of two elements (the pair kernel's body): the same operations as

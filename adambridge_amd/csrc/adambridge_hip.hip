@@ -262,7 +262,7 @@ __device__ __forceinline__ void store_master8(void* p, uint8_t* lo, float (&x)[8
 {
     if constexpr (PT == DT_F24) {
         uint32_t r[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
-        if constexpr (SR) hash8(idx, seed, w, r);
+        if constexpr (SR) hash8_low8(idx, seed, w, r);   // f24_round takes r & 0xff
         // f24_round: the add and the cut, and a NaN quietened instead; the NaN fix-up runs only
         // where some lane of the wavefront holds one (a uniform test on the compares' lane masks)
         uint64_t nans = 0;
@@ -271,7 +271,7 @@ __device__ __forceinline__ void store_master8(void* p, uint8_t* lo, float (&x)[8
         for (int k = 0; k < 8; ++k) {
             nans |= __builtin_amdgcn_ballot_w64(x[k] != x[k]);
             const uint32_t u = fbits(x[k]);
-            b[k] = (SR ? u + (r[k] & 0xffu) : u + 0x7fu + ((u >> 8) & 1u)) & ~0xffu;
+            b[k] = (SR ? u + r[k] : u + 0x7fu + ((u >> 8) & 1u)) & ~0xffu;   // r[k] < 256
         }
         if (nans != 0) {
 #pragma unroll
