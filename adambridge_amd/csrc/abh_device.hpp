@@ -53,7 +53,7 @@ __device__ __forceinline__ uint32_t hash32_tail(uint32_t x) { return hash32_tail
 
 // Whether a wavefront's lanes agree in bits 16-18 of their rounding index, and those bits (see hash8).
 struct Wave8 {
-    bool uniform;
+    uint32_t mixed;   // 0 where the wavefront's indices agree in bits 16-18 (a scalar)
     uint32_t hi3;
 };
 
@@ -69,7 +69,11 @@ __device__ __forceinline__ void hash8_mul(uint32_t idx, uint32_t seed, const Wav
 {
     constexpr uint32_t kMul = 0x7feb352du;
     const uint32_t head = hash32_head(idx ^ seed);
-    if (w.uniform) {
+    // the flag as an opaque scalar at each call: one test shared by the calls would be kept as a
+    // lane mask and negated through a vector register
+    uint32_t mixed = w.mixed;
+    asm volatile("" : "+s"(mixed));
+    if (mixed == 0u) {
         const uint32_t c = (seed ^ (seed >> 16) ^ w.hi3) & 7u;
         const uint32_t a = (head & ~7u) * kMul;
 #pragma unroll
@@ -119,7 +123,10 @@ __device__ __forceinline__ Wave8 wave8_of(uint32_t idx)
 {
     const uint32_t hi3 = (idx >> 16) & 7u;
     const uint32_t first = __builtin_amdgcn_readfirstlane(hi3);
-    return Wave8{__builtin_amdgcn_ballot_w64(hi3 != first) == 0, first};
+    // the lanes that differ, as an integer (the two halves of the ballot or'ed): a bool made here
+    // would be kept as a lane mask and turned into an integer through vector registers
+    const uint64_t differ = __builtin_amdgcn_ballot_w64(hi3 != first);
+    return Wave8{(uint32_t)differ | (uint32_t)(differ >> 32), first};
 }
 
 // BF16 bits of x, nearest-even, NaN quietened (kernels.c:108-112), in the low half: the rule
@@ -199,16 +206,6 @@ __device__ __forceinline__ void fp8_decode2(uint32_t word, float& x0, float& x1)
     else d = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, H);
     x0 = d.x;
     x1 = d.y;
-}
-
-// Whether one of the 8 codes in w0, w1 is a NaN code (E4M3FN: low 7 bits 0x7f; E5M2: exponent
-// 31 with a nonzero mantissa, low 7 bits 0x7d..0x7f): adding 1 (3) to each byte's low 7 bits
-// sets its bit 7 exactly for those, with no carry between bytes.
-template <bool E5M2>
-__device__ __forceinline__ bool fp8_has_nan(uint32_t w0, uint32_t w1)
-{
-    constexpr uint32_t kLift = E5M2 ? 0x03030303u : 0x01010101u;
-    return ((((w0 & 0x7f7f7f7fu) + kLift) | ((w1 & 0x7f7f7f7fu) + kLift)) & 0x80808080u) != 0u;
 }
 
 // The value of an FP8 code from the format's definition (OCP E4M3FN / E5M2), for the self-check.
@@ -452,8 +449,8 @@ __device__ __forceinline__ float recip_nearest(float s)
 // The AdamW step's m / den, correctly rounded, in 6 instructions instead of the general
 // division's 11, where every operand is in range: y = 1/den correctly rounded (recip_nearest),
 // q = m y, and one residual correction q + (m - q den) y (Markstein's theorem, as for the FP8 block
-// quotients).  The range: 2^-60 <= |m| <= 2^60 (quot_m_offset <= kQuotMSpan, one unsigned maximum
-// per lane), and 2^-50 <= den < 2^61, which holds when every v is in sqrt_mid's range (so sqrt(v)
+// quotients).  The range: 2^-60 <= |m| <= 2^60 (quot_m_offset <= kQuotMSpan, for a single value;
+// adamw8_fused tests a lane's largest and smallest |m|), and 2^-50 <= den < 2^61, which holds when every v is in sqrt_mid's range (so sqrt(v)
 // lies in [2^-50, 2^50)) and the step's 1 <= inv_sqrt_bc2 <= 2^10 and 0 <= eps <= 2^30 (checked on
 // the host: the segment flag of adamw8_fused's caller).  Then y, q and the quotient are normal
 // (|m / den| in [2^-121, 2^110]) and m - q den, about |m| 2^-24 >= 2^-84, is exact, which the
@@ -475,19 +472,24 @@ __device__ __forceinline__ float quot_fast(float m, float den)
 // quotients m / den take quot_fast.  Returns whether sqrt_mid was taken, i.e. whether every v, and
 // so every sq, of the wavefront is positive and finite; m_plain receives whether quot_fast was
 // taken, i.e. whether every new m of the wavefront is finite with 2^-60 <= |m| <= 2^60, and m_low
-// then the smallest quot_m_offset of the lane's new m (its smallest |m|, in an order-keeping form).
+// then the smallest |m| of the lane.
+//
+// The range tests take each lane's extremes: the v's as unsigned bits (a negative v, -0 and NaN
+// lie above the range's end, +0 below its start), the |m| by gfx950's three-operand maximum and
+// minimum that keep NaN (v_maximum3_f32, v_minimum3_f32: a NaN fails the test).
 __device__ __forceinline__ bool adamw8_fused(float (&p)[8], const float (&g)[8], float (&m)[8], float (&v)[8],
                                              const Coef& c, float (&sq)[8], bool fastdiv, bool& m_plain,
-                                             uint32_t& m_low)
+                                             float& m_low)
 {
-    uint32_t worst = 0u, worst_m = 0u;   // largest offsets of the v's and m's bits from their ranges' starts
+    uint32_t v_hi = 0u, v_lo = 0xffffffffu;   // the largest and smallest bits of the new v's
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         m[k] = __builtin_fmaf(c.b1, m[k], c.omb1 * g[k]);
         v[k] = __builtin_fmaf(c.b2, v[k], c.omb2 * (g[k] * g[k]));
-        worst = __builtin_elementwise_max(worst, fbits(v[k]) - kSqrtMidLo);
+        v_hi = __builtin_elementwise_max(v_hi, fbits(v[k]));
+        v_lo = __builtin_elementwise_min(v_lo, fbits(v[k]));
     }
-    const bool mid = __all(worst < kSqrtMidSpan);
+    const bool mid = __all(v_lo >= kSqrtMidLo) && __all(v_hi < kSqrtMidLo + kSqrtMidSpan);
     if (mid) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) sq[k] = sqrt_mid(v[k]);
@@ -496,15 +498,16 @@ __device__ __forceinline__ bool adamw8_fused(float (&p)[8], const float (&g)[8],
         for (int k = 0; k < 8; ++k) sq[k] = __builtin_sqrtf(v[k]);
     }
     bool fast = false;
-    uint32_t low_m = 0xffffffffu;
+    float m_min = 0.0f;
     if (mid && fastdiv) {
+        float m_max = fabsf(m[0]);
+        m_min = fabsf(m[0]);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const uint32_t o = quot_m_offset(m[k]);
-            worst_m = __builtin_elementwise_max(worst_m, o);
-            low_m = __builtin_elementwise_min(low_m, o);
+        for (int k = 1; k < 8; ++k) {
+            m_max = __builtin_elementwise_maximum(m_max, fabsf(m[k]));
+            m_min = __builtin_elementwise_minimum(m_min, fabsf(m[k]));
         }
-        fast = __all(worst_m <= kQuotMSpan);
+        fast = __all(m_max <= 0x1p60f) && __all(m_min >= 0x1p-60f);
     }
     if (fast) {
 #pragma unroll
@@ -520,7 +523,7 @@ __device__ __forceinline__ bool adamw8_fused(float (&p)[8], const float (&g)[8],
         }
     }
     m_plain = fast;
-    m_low = low_m;
+    m_low = m_min;
     return mid;
 }
 

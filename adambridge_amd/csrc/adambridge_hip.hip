@@ -171,18 +171,38 @@ __device__ __forceinline__ uint32_t fresh(uint32_t x)
     return x;
 }
 
+// 8 BF16 values, two to a word (element 2k in the low half of word k), as FP32.
+__device__ __forceinline__ void decode_bf16x8(const u32x4 w, float (&x)[8])
+{
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        x[2 * k] = bitsf(u[k] << 16);
+        x[2 * k + 1] = bitsf(u[k] & 0xffff0000u);
+    }
+}
+
+// 8 FP24 values from their planes (high halves two to a word, low bytes four to a word) as FP32:
+// value k = high half k & 1 of word k >> 1 : low byte k & 3 of word k >> 2 : a zero byte, one byte
+// permute each (selector bytes 4-7 address the first source, 0-3 the second, 0x0c gives zero).
+__device__ __forceinline__ void decode_f24x8(const u32x4 h, const u32x2 l, float (&x)[8])
+{
+    const uint32_t hu[4] = {h.x, h.y, h.z, h.w};
+    const uint32_t lu[2] = {l.x, l.y};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t hb = 4u + 2u * (uint32_t)(k & 1);
+        const uint32_t sel = 0x0cu | (uint32_t)(k & 3) << 8 | hb << 16 | (hb + 1u) << 24;
+        x[k] = bitsf(__builtin_amdgcn_perm(hu[k >> 1], lu[k >> 2], sel));
+    }
+}
+
 // 8 consecutive values at p as FP32, from BF16 bits or FP32, 16-byte aligned.
 template <int DT>
 __device__ __forceinline__ void load8(const void* p, float (&x)[8])
 {
     if constexpr (DT == DT_BF16) {
-        const u32x4 w = ld(static_cast<const u32x4*>(p));
-        const uint32_t u[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            x[2 * k] = bitsf(u[k] << 16);
-            x[2 * k + 1] = bitsf(u[k] & 0xffff0000u);
-        }
+        decode_bf16x8(ld(static_cast<const u32x4*>(p)), x);
     } else {
         // Two 16-byte loads per lane at a 32-byte lane stride: each load covers half of every cache
         // line it touches.  Ordinary (cached) loads let the second find the line the first brought
@@ -233,16 +253,7 @@ template <int PT>
 __device__ __forceinline__ void load_master8(const void* p, const uint8_t* lo, float (&x)[8])
 {
     if constexpr (PT == DT_F24) {
-        const u32x4 h = ld(static_cast<const u32x4*>(p));
-        const u32x2 l = ld(reinterpret_cast<const u32x2*>(lo));
-        const uint32_t hu[4] = {h.x, h.y, h.z, h.w};
-        const uint32_t lu[2] = {l.x, l.y};
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const uint32_t hi16 = (hu[k >> 1] >> (16 * (k & 1))) & 0xffffu;
-            const uint32_t lo8 = (lu[k >> 2] >> (8 * (k & 3))) & 0xffu;
-            x[k] = bitsf((hi16 << 16) | (lo8 << 8));
-        }
+        decode_f24x8(ld(static_cast<const u32x4*>(p)), ld(reinterpret_cast<const u32x2*>(lo)), x);
     } else if constexpr (PT == DT_PACKED8) {
         const uint8_t* r = static_cast<const uint8_t*>(p);
         const f32x4 a = ld(reinterpret_cast<const f32x4*>(r)), b = ld(reinterpret_cast<const f32x4*>(r + 256));
@@ -264,16 +275,17 @@ __device__ __forceinline__ void store_master8(void* p, uint8_t* lo, float (&x)[8
         uint32_t r[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
         if constexpr (SR) hash8_low8(idx, seed, w, r);   // f24_round takes r & 0xff
         // f24_round: the add and the cut, and a NaN quietened instead; the NaN fix-up runs only
-        // where some lane of the wavefront holds one (a uniform test on the compares' lane masks)
-        uint64_t nans = 0;
+        // where some lane of the wavefront holds one (a uniform test: the lane's 8 values through
+        // gfx950's NaN-keeping three-operand maximum, v_maximum3_f32, then one compare)
+        float any = x[0];
         uint32_t b[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            nans |= __builtin_amdgcn_ballot_w64(x[k] != x[k]);
+            if (k > 0) any = __builtin_elementwise_maximum(any, x[k]);
             const uint32_t u = fbits(x[k]);
             b[k] = (SR ? u + r[k] : u + 0x7fu + ((u >> 8) & 1u)) & ~0xffu;   // r[k] < 256
         }
-        if (nans != 0) {
+        if (__builtin_amdgcn_ballot_w64(any != any) != 0) {
 #pragma unroll
             for (int k = 0; k < 8; ++k) b[k] = f24_round<SR>(x[k], r[k]);
         }
@@ -537,7 +549,10 @@ __device__ __forceinline__ void decode_codes(const u32x2 w, float (&x)[8])
     fp8_decode2<E5M2, true>(w.x, x[2], x[3]);
     fp8_decode2<E5M2, false>(w.y, x[4], x[5]);
     fp8_decode2<E5M2, true>(w.y, x[6], x[7]);
-    if (!fp8_has_nan<E5M2>(w.x, w.y)) return;
+    // the packed conversions give NaN exactly for NaN codes: one unordered compare per pair
+    if (!(__builtin_isunordered(x[0], x[1]) | __builtin_isunordered(x[2], x[3]) |
+          __builtin_isunordered(x[4], x[5]) | __builtin_isunordered(x[6], x[7])))
+        return;
     if constexpr (E5M2) {
         x[0] = e5m2_decode<0>(w.x); x[1] = e5m2_decode<1>(w.x); x[2] = e5m2_decode<2>(w.x); x[3] = e5m2_decode<3>(w.x);
         x[4] = e5m2_decode<0>(w.y); x[5] = e5m2_decode<1>(w.y); x[6] = e5m2_decode<2>(w.y); x[7] = e5m2_decode<3>(w.y);
@@ -662,27 +677,32 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     uint8_t* const vq = static_cast<uint8_t*>(s.v);
     const int64_t e0 = base + off;
     const uint32_t idx = s.idx0 + (uint32_t)e0;
-    const Wave8 w8 = SR ? wave8_of(idx) : Wave8{false, 0u};   // for hash8
+    const Wave8 w8 = SR ? wave8_of(idx) : Wave8{1u, 0u};   // for hash8
     const bool full = FULL || (vec && e0 + 8 <= n);
     const uint32_t lane = (off >> 3) & 15u;         // within the block's 16
     const uint32_t blk = off >> 7;                   // the block within this pass
     const int64_t ublk = base / kFp8Block;           // the pass's first block
-    // records: the lane's 16-byte codes slot in its block's record
-    const uint32_t rec_codes = blk * kRecB + kCodesAt + lane * 16u;
+    // records: the lane's 16-byte slot in its block's record (FP24 master high halves, or the
+    // first half of an FP32 master with the second 256 bytes on; the codes kCodesAt bytes on) and,
+    // FP24 planes, its 8-byte slot of low bytes.  Computed once: the stores take them again
+    // through fresh(), which keeps their scalar-base form without recomputing them.
+    const uint32_t rec_lane = blk * kRecB + lane * 16u;
+    const uint32_t rec_lo = blk * kRecB + 256u + lane * 8u;
     // Block scales: ordinary (cached) accesses.  A wavefront reads and writes 16 bytes of each
     // scale array, four blocks' worth; through L2 the four wavefronts of a workgroup share whole
     // lines, where non-temporal accesses sent each 16-byte piece to HBM on its own (measured: the
     // launch 3-4% slower, reads and writes 1.4% above the algorithmic bytes).
     const float sm = *(const ABH_GLOBAL float*)lane_ptr<float>(s.m_scale, ublk * 4, blk * 4u);
     const float sv = kLion ? 0.0f : *(const ABH_GLOBAL float*)lane_ptr<float>(s.v_scale, ublk * 4, blk * 4u);
-    // the master's (pm, pl) and the output's (po) vector addresses for the lane offset o
-    auto pm = [&](uint32_t o) -> void* {
-        if constexpr (kRec) return lane_ptr<void>(s.p, ublk * kRecB, (o >> 7) * kRecB + ((o >> 3) & 15u) * 16u);
+    // the master's (pm, pl) and the output's (po) vector addresses for the lane offset o and, in
+    // records, the lane's slots ro (rec_lane) and rl (rec_lo)
+    auto pm = [&](uint32_t o, uint32_t ro) -> void* {
+        if constexpr (kRec) return lane_ptr<void>(s.p, ublk * kRecB, ro);
         else return lane_ptr<void>(s.p, base * kPB, o * (uint32_t)kPB);
     };
-    auto pl = [&](uint32_t o) -> uint8_t* {
+    auto pl = [&](uint32_t o, uint32_t rl) -> uint8_t* {
         if constexpr (PT == DT_F24) return lane_ptr<uint8_t>(s.p_lo, base, o);
-        else if constexpr (PT == DT_PACKED8_F24) return lane_ptr<uint8_t>(s.p, ublk * kRecB, (o >> 7) * kRecB + 256u + ((o >> 3) & 15u) * 8u);
+        else if constexpr (PT == DT_PACKED8_F24) return lane_ptr<uint8_t>(s.p, ublk * kRecB, rl);
         else return nullptr;
     };
     auto po = [&](uint32_t o) -> void* {
@@ -692,7 +712,7 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     // codes are stored padded to whole blocks, so all 8 of this lane's exist
     u32x2 cm, cv = {0u, 0u};
     if constexpr (kRec) {   // AdamW only
-        const u32x4 w = ld(lane_ptr<const u32x4>(s.p, ublk * kRecB, rec_codes));
+        const u32x4 w = ld(lane_ptr<const u32x4>(s.p, ublk * kRecB, rec_lane + kCodesAt));
         cm = u32x2{w.x, w.y};
         cv = u32x2{w.z, w.w};
     } else {
@@ -702,7 +722,7 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     float g[8], p[8], mt[8], vt[8];
     if (full) {
         load8<GT>(lane_ptr<const void>(s.g, base * kGB, off * (uint32_t)kGB), g);
-        load_master8<kMaster>(pm(off), pl(off), p);
+        load_master8<kMaster>(pm(off, rec_lane), pl(off, rec_lo), p);
         if constexpr (PREV) store_out8<OT>(po(off), p);   // out from the master as loaded
     } else {
 #pragma unroll
@@ -732,7 +752,7 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     const bool lane_fused = FULL || kLion || e0 + 8 <= n_main;
     bool v_pos = false;     // every new v of the wavefront positive and finite (uniform)
     bool m_plain = false;   // every new m of the wavefront finite, 2^-60 <= |m| <= 2^60 (uniform)
-    uint32_t m_low = 0u;    // where m_plain: the lane's smallest |m| as quot_m_offset
+    float m_low = 0.0f;     // where m_plain: the lane's smallest |m|
     if constexpr (FULL && !kLion) {
         v_pos = adamw8_fused(p, g, mt, vt, c, sq, (s.flags & kFastDiv) != 0, m_plain, m_low);
     } else {
@@ -745,7 +765,8 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     }
     if (full) {
         const uint32_t o = fresh(off);
-        store_master8<kMaster, SR>(pm(o), pl(o), p, idx, s.seed_p, w8);
+        const uint32_t ro = kRec ? fresh(rec_lane) : 0u, rl = PT == DT_PACKED8_F24 ? fresh(rec_lo) : 0u;
+        store_master8<kMaster, SR>(pm(o, ro), pl(o, rl), p, idx, s.seed_p, w8);
         if constexpr (!PREV) store_out8<OT>(po(o), p);
     } else {
 #pragma unroll
@@ -805,14 +826,14 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     // their exact range (rare: zeros, values below the smallest normal after scaling, NaN) and
     // partial blocks take the integer encoder.  Where m_plain (v_pos) holds, the lane's values
     // are finite and nonzero, and each quotient reaches the smallest normal 2^-6 (2^-14) once the
-    // smallest |m| (u) reaches that multiple of the scale (the multiple is exact, and rounding is
-    // monotone; quot_m_offset keeps the order from 2^-60 up and wraps below, which fails the test);
-    // the per-value test is needed otherwise.
+    // smallest |m| (u) reaches that multiple of the scale (rounding is monotone, and the multiple is
+    // exact: |m| >= 2^-60 and u >= 2^-50 there keep the scales above 2^-69 and 2^-66); the per-value
+    // test is needed otherwise.
     uint32_t qm[2] = {0u, 0u}, qv[2] = {0u, 0u};
     bool soft_m = true, soft_v = !kLion;
     if constexpr (FULL) {
         hw_codes8<false, SR>(mt, idx, s.seed_m, w8, qm);
-        soft_m = !(m_plain ? (!SR || m_low >= quot_m_offset(scm * 0x1p-6f)) : hw_range8<false, SR>(mt));
+        soft_m = !(m_plain ? (!SR || m_low >= scm * 0x1p-6f) : hw_range8<false, SR>(mt));
         if constexpr (!kLion) {
             hw_codes8<true, SR>(sq, idx, s.seed_v, w8, qv);
             soft_v = !(v_pos ? (!SR || u_min >= scu * 0x1p-14f) : hw_range8<true, SR>(sq));
@@ -839,8 +860,7 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     }
     const uint32_t o = fresh(off);
     if constexpr (kRec) {
-        st(lane_ptr<u32x4>(s.p, ublk * kRecB, (o >> 7) * kRecB + kCodesAt + ((o >> 3) & 15u) * 16u),
-           u32x4{qm[0], qm[1], qv[0], qv[1]});
+        st(lane_ptr<u32x4>(s.p, ublk * kRecB, fresh(rec_lane) + kCodesAt), u32x4{qm[0], qm[1], qv[0], qv[1]});
     } else if (vec) {
         st(lane_ptr<u32x2>(mq, base, o), u32x2{qm[0], qm[1]});
         if constexpr (!kLion) st(lane_ptr<u32x2>(vq, base, o), u32x2{qv[0], qv[1]});
@@ -888,9 +908,11 @@ __device__ __forceinline__ void update_tile_fp8(const DevSeg& s, int64_t tile, i
 // WIDE: the launch's tiles hold more than one block per 16-lane group (ADAMBRIDGE_TILE_FP8 above
 // 2048).  The default tile takes the kernel without the loop: 58 VGPRs for the FP8-record and FP24
 // variants, room for 8 wavefronts per SIMD, where the loop in the same kernel made it 89-102 (5).
-// The FP24-master forms, bound by their VALU, use all 8: the 7B list with an FP24 master took
-// 16.52 ms per launch against 18.5-19.0 at 5.  (launch_lds holds the FP32-master AdamW forms at 6
-// workgroups per CU.)
+// The FP24-master forms use all 8: the 7B list with an FP24 master took 16.52 ms per launch
+// against 18.5-19.0 at 5.  (launch_lds holds the FP32-master AdamW forms at 6 workgroups per CU.)
+// A pipelined form of the loop for block records, each pass's loads issued during the previous
+// pass's arithmetic, took 111-113 VGPRs (4 wavefronts per SIMD) and was 7-13% slower at 4096-16384
+// element tiles than this form at 2048.
 template <int ALGO, int PT, int GT, int OT, bool WIDE>
 __global__ __launch_bounds__(kThreads) void k_update_fp8(Launch L)
 {
@@ -1566,8 +1588,10 @@ inline bool kernel_is_fp8(int index)
 // Lion records at the 1.5B list (338 tensors) run alike with 6 or 8 (4.00-4.03) and lose 13% with 5
 // (4.58-4.61): the segment search each workgroup makes first is hidden by fewer others there.  The
 // BF16 pairs lose with fewer workgroups (the 0.5B list: 1.76 against 1.67 ms with 6), and the
-// FP24-master kernels, bound by their VALU, keep 8 (FP8 with an FP24 master in records, the 7B list:
-// 8 per CU 16.66, 7: 16.55, 6: 16.65, 5: 17.91).
+// FP24-master FP8 kernels keep 8 (records, the 7B list: 8 per CU 16.28-16.66, 7: 16.18-16.55, 6:
+// 16.44-16.65, 5: 17.56-17.91).  Those run at the speed of their accesses alone: a form that makes
+// the same loads and stores and no arithmetic took 16.45 ms at 8 per CU, and its time falls as the
+// CU holds fewer workgroups (15.46 at 5, 15.15 at 3) while the arithmetic needs the wavefronts.
 inline size_t launch_lds(int index)
 {
     constexpr size_t kCap6 = 24 * 1024;   // 6 workgroups of 24 KiB in 160 KiB; 7 would need 168
@@ -1940,7 +1964,7 @@ __device__ bool divisions_match(uint32_t u, uint32_t seed)
 
 // Code `code` of format E5M2 (else E4M3FN) placed in byte `pos` of a word with other bytes
 // zero: packed and per-code decoders against fp8_value_soft (NaN: a NaN of the code's sign from
-// the per-code decoder), and NaN detection.
+// the per-code decoder, which decode_codes takes where the packed conversion gives NaN).
 template <bool E5M2>
 __device__ __forceinline__ bool decode_matches_fmt(uint32_t code, uint32_t pos)
 {
@@ -1952,7 +1976,6 @@ __device__ __forceinline__ bool decode_matches_fmt(uint32_t code, uint32_t pos)
     const float want = fp8_value_soft<E5M2>(code);
     const float got = x[pos], got_hi = y[4 + pos];
     const bool nan = want != want;
-    if (fp8_has_nan<E5M2>(word, 0u) != nan) return false;
     if (nan) return got != got && got_hi != got_hi && (fbits(got) >> 31) == (code >> 7) && (fbits(got_hi) >> 31) == (code >> 7);
     return fbits(got) == fbits(want) && fbits(got_hi) == fbits(want);
 }

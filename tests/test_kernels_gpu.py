@@ -678,18 +678,20 @@ sys.exit(1 if bad else 0)
 """
 
 
-def test_fp8_larger_tile_matches_oracle():
+@pytest.mark.parametrize("tile", [4096, 8192])
+def test_fp8_larger_tile_matches_oracle(tile):
     """The FP8 kernel's loop over several blocks per 16-lane group, taken only when
     ADAMBRIDGE_TILE_FP8 asks for a tile above 2048 elements (read once per process, hence a child
-    process): separate and block-record layouts, AdamW and Lion, FP32 and FP24 masters."""
+    process): separate and block-record layouts, AdamW and Lion, FP32 and FP24 masters; 2 and 4
+    passes per tile, with partial passes and blocks at the segments' ends."""
     import os
     import subprocess
     import sys
     from pathlib import Path
 
     root = Path(__file__).resolve().parents[1]
-    env = dict(os.environ, ADAMBRIDGE_TILE_FP8="4096")
-    print("child process: ADAMBRIDGE_TILE_FP8=4096", flush=True)
+    env = dict(os.environ, ADAMBRIDGE_TILE_FP8=str(tile))
+    print(f"child process: ADAMBRIDGE_TILE_FP8={tile}", flush=True)
     run = subprocess.run([sys.executable, "-c", _LARGER_FP8_TILE, str(root), str(root / "tests")], env=env,
                          capture_output=True, text=True, timeout=110)
     print(run.stdout, flush=True)
