@@ -364,8 +364,8 @@ ADAMBRIDGE_API int adambridge_recycle_device_memory(int64_t nbytes);
 
 /* Copies nbytes (a multiple of 16; src and dst 16-byte aligned, not overlapping) on the calling
  * thread's stream with the update kernels' access type -- 16-byte non-temporal global loads and
- * stores, 4 KiB workgroup tiles handed out XCD by XCD (kernel k_stream_copy, one launch per 64 GiB)
- * -- so that hardware byte counters (rocprofv3 FETCH_SIZE / WRITE_SIZE) read for it calibrate the
+ * stores, 4 KiB workgroup tiles handed out XCD by XCD, at most 6 workgroups per CU (kernel
+ * k_stream_copy, one launch per 64 GiB) -- so that hardware byte counters (rocprofv3 FETCH_SIZE / WRITE_SIZE) read for it calibrate the
  * same counters read for the update kernels, and its time bounds what a 1:1 read/write stream of
  * the same bytes reaches.  Asynchronous.  Returns 0, ADAMBRIDGE_EBADN (negative or not a multiple of
  * 16), _ENULL, _EALIGN or _EHIP.  No counterpart in the reference: a measurement aid. */
