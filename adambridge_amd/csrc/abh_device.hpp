@@ -466,7 +466,8 @@ __device__ __forceinline__ float quot_fast(float m, float den)
     return __builtin_fmaf(__builtin_fmaf(-q, den, m), y, q);
 }
 
-// The fused form of adamw for a lane's 8 elements.  The square roots take sqrt_mid when every new v
+// The fused form of adamw for a lane's 8 elements, up to the quotients q = m / den (the master's
+// update follows in adamw8_fused).  The square roots take sqrt_mid when every new v
 // of the wavefront lies in its range (one uniform branch), sqrtf otherwise; with ``fastdiv`` (the
 // step's coefficients are in quot_fast's range) and every m of the wavefront in range as well, the
 // quotients m / den take quot_fast.  Returns whether sqrt_mid was taken, i.e. whether every v, and
@@ -477,9 +478,9 @@ __device__ __forceinline__ float quot_fast(float m, float den)
 // The range tests take each lane's extremes: the v's as unsigned bits (a negative v, -0 and NaN
 // lie above the range's end, +0 below its start), the |m| by gfx950's three-operand maximum and
 // minimum that keep NaN (v_maximum3_f32, v_minimum3_f32: a NaN fails the test).
-__device__ __forceinline__ bool adamw8_fused(float (&p)[8], const float (&g)[8], float (&m)[8], float (&v)[8],
-                                             const Coef& c, float (&sq)[8], bool fastdiv, bool& m_plain,
-                                             float& m_low)
+__device__ __forceinline__ bool adamw8_fused_q(const float (&g)[8], float (&m)[8], float (&v)[8], const Coef& c,
+                                               float (&sq)[8], bool fastdiv, bool& m_plain, float& m_low,
+                                               float (&q)[8])
 {
     uint32_t v_hi = 0u, v_lo = 0xffffffffu;   // the largest and smallest bits of the new v's
 #pragma unroll
@@ -511,19 +512,25 @@ __device__ __forceinline__ bool adamw8_fused(float (&p)[8], const float (&g)[8],
     }
     if (fast) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const float den = __builtin_fmaf(sq[k], c.isbc2, c.eps);
-            p[k] = __builtin_fmaf(-c.step, quot_fast(m[k], den), p[k] * c.decay);
-        }
+        for (int k = 0; k < 8; ++k) q[k] = quot_fast(m[k], __builtin_fmaf(sq[k], c.isbc2, c.eps));
     } else {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const float den = __builtin_fmaf(sq[k], c.isbc2, c.eps);
-            p[k] = __builtin_fmaf(-c.step, m[k] / den, p[k] * c.decay);
-        }
+        for (int k = 0; k < 8; ++k) q[k] = m[k] / __builtin_fmaf(sq[k], c.isbc2, c.eps);
     }
     m_plain = fast;
     m_low = m_min;
+    return mid;
+}
+
+// adamw8_fused_q, then the masters: p = p decay - step q (one fused multiply-add each).
+__device__ __forceinline__ bool adamw8_fused(float (&p)[8], const float (&g)[8], float (&m)[8], float (&v)[8],
+                                             const Coef& c, float (&sq)[8], bool fastdiv, bool& m_plain,
+                                             float& m_low)
+{
+    float q[8];
+    const bool mid = adamw8_fused_q(g, m, v, c, sq, fastdiv, m_plain, m_low, q);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) p[k] = __builtin_fmaf(-c.step, q[k], p[k] * c.decay);
     return mid;
 }
 
