@@ -55,6 +55,11 @@ TRAFFIC_PROFILE = {"c3p": "profiles/k_update_packed_c3p_hbm_traffic.md",
                    "c2": "profiles/k_update_f32rec_c1_packed_c2_trace_traffic.md",
                    "c3": "profiles/k_update_fp8_c3_trace_traffic_instructions.md",
                    "c4": "profiles/k_update_lion_rec_c4_trace_traffic.md"}
+# the same with an FP24 master (--master fp24), where measured
+MEASURED_TRAFFIC_FP24 = {"c3p": 60.646e9 + 60.632e9, "c3": 47.59e9 + 47.58e9, "c4": 10.806e9 + 10.804e9}
+TRAFFIC_PROFILE_FP24 = {"c3p": "profiles/k_update_f24rec_fp24_master_trace_valu.md",
+                        "c3": "profiles/k_update_fp8_c3_trace_traffic_instructions.md",
+                        "c4": "profiles/k_update_f24rec_fp24_master_trace_valu.md"}
 
 
 # ------------------------------------------------------------ parameter lists
@@ -699,8 +704,9 @@ def main() -> int:
               f"{cpu['all_cores']['ms_per_step']:.1f} ms/step on {cpu['all_cores']['threads']} ({cpu['host']})",
               file=sys.stderr, flush=True)
     ms_per_step = g["wall"] / args.steps * 1e3
-    # the traffic measured for each configuration, with its own (FP32) master
-    measured, profiled = (MEASURED_TRAFFIC, TRAFFIC_PROFILE) if args.master == "fp32" else ({}, {})
+    # the traffic measured for each configuration and master
+    measured, profiled = ((MEASURED_TRAFFIC, TRAFFIC_PROFILE) if args.master == "fp32" else
+                          (MEASURED_TRAFFIC_FP24, TRAFFIC_PROFILE_FP24))
     line = {
         "metric": METRIC if args.config == "c3p" and args.master == "fp32" else
         f"params updated/sec and achieved HBM GB/s (% roofline), {cfg['desc']} ({args.config}"
