@@ -222,18 +222,21 @@ def gpu_bench(cfg: dict, steps: int, warmup: int, layout: str = "auto", double_b
                 p.grad = g
         opts[k % len(opts)].step()
 
-    for k in range(warmup * len(opts)):
-        step(k)
-    torch.cuda.synchronize()
-    log: list = []
-    for opt in opts:
-        opt._engine.launch_log = log
     # No garbage collection inside the timed region (as timeit does): a collection pauses the host
     # for tens of milliseconds, and where a launch is shorter than the host's lead (the 0.5B list:
     # 1.6 ms) the device then idles -- between a launch's start event and the launch, inflating it.
+    # The collection runs before the warm-up, not between it and the timed steps: after the idle
+    # stretch it leaves (55-87 ms) the first launches ran slower (the 7B list 21.5 against 20.6 ms;
+    # the 0.5B list several launches of 1.6-1.8 against 1.55 ms), as traces of this script showed.
     gc.collect()
     gc.disable()
     try:
+        for k in range(warmup * len(opts)):
+            step(k)
+        torch.cuda.synchronize()
+        log: list = []
+        for opt in opts:
+            opt._engine.launch_log = log
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for k in range(steps):
