@@ -450,9 +450,10 @@ __device__ __forceinline__ float recip_nearest(float s)
 // division's 11, where every operand is in range: y = 1/den correctly rounded (recip_nearest),
 // q = m y, and one residual correction q + (m - q den) y (Markstein's theorem, as for the FP8 block
 // quotients).  The range: 2^-60 <= |m| <= 2^60 (quot_m_offset <= kQuotMSpan, for a single value;
-// adamw8_fused tests a lane's largest and smallest |m|), and 2^-50 <= den < 2^61, which holds when every v is in sqrt_mid's range (so sqrt(v)
-// lies in [2^-50, 2^50)) and the step's 1 <= inv_sqrt_bc2 <= 2^10 and 0 <= eps <= 2^30 (checked on
-// the host: the segment flag of adamw8_fused's caller).  Then y, q and the quotient are normal
+// adamw8_fused_q tests a lane's largest and smallest |m|), and 2^-50 <= den < 2^61, which holds
+// when every v is in sqrt_mid's range (so sqrt(v) lies in [2^-50, 2^50)) and the step's
+// 1 <= inv_sqrt_bc2 <= 2^10 and 0 <= eps <= 2^30 (checked on the host: the segment flag of
+// adamw8_fused_q's caller).  Then y, q and the quotient are normal
 // (|m / den| in [2^-121, 2^110]) and m - q den, about |m| 2^-24 >= 2^-84, is exact, which the
 // theorem needs.  Zero m lies outside the range: its wavefront divides.
 constexpr uint32_t kQuotMLo = 0x21800000u, kQuotMSpan = (0x5d800000u - 0x21800000u) << 1;   // 2^-60, 2^60
