@@ -1056,9 +1056,14 @@ __global__ __launch_bounds__(kThreads) void k_update_packed(Launch L)
 // lane), all timed in turn in one process.  Lion fuses every element
 // (kernels.c:1093-1106), so there is no scalar tail; a record's slots past n
 // are padding and are written back unchanged.
+//
+// With an FP32 moment (MV = DT_F32, ADAMBRIDGE_DT_PACKED_LION_F32): 2048-byte records, the 256
+// masters and then the 256 m values, both FP32 and stored exactly -- a 16-byte moment access per
+// lane, the FP32-moment AdamW records' access shape.
 
 constexpr int64_t kLionRecordElems = 256;
 constexpr int64_t kLionRecordBytes = 1536;
+constexpr int64_t kLionF32RecordBytes = 2048;
 
 // The working weights of elements i .. i + 3 below n, from FP32 bits.
 template <int OT>
@@ -1074,9 +1079,11 @@ __device__ __forceinline__ void store_quad_out(void* out, int64_t i, int64_t n, 
     }
 }
 
-template <int GT, int OT, bool SR>
+template <int GT, int OT, bool SR, int MV>
 __device__ __forceinline__ void update_tile_lion_rec(const DevSeg& s, int64_t tile, int64_t T)
 {
+    constexpr bool kF32 = MV == DT_F32;
+    constexpr int64_t kRecB = kF32 ? kLionF32RecordBytes : kLionRecordBytes;
     const int64_t n = s.n;
     const Coef c = s.c;
     const uint8_t* __restrict__ src = static_cast<const uint8_t*>(s.p);
@@ -1086,13 +1093,21 @@ __device__ __forceinline__ void update_tile_lion_rec(const DevSeg& s, int64_t ti
     const int64_t lo = (tile - s.tile_begin) * T;
     const int64_t hi = lo + T < n ? lo + T : n;
     for (int64_t i = lo + threadIdx.x * 4; i < hi; i += kThreads * 4) {
-        // i % 4 == 0: record i / 256, masters at 4 (i % 256), m values at 1024 + 2 (i % 256)
-        const int64_t rec = (i / kLionRecordElems) * kLionRecordBytes;
+        // i % 4 == 0: record i / 256, masters at 4 (i % 256), m values at 1024 + 2 (i % 256) (BF16)
+        // or 1024 + 4 (i % 256) (FP32)
+        const int64_t rec = (i / kLionRecordElems) * kRecB;
         const int64_t at = rec + (i % kLionRecordElems) * 4;
-        const int64_t at_m = rec + 1024 + (i % kLionRecordElems) * 2;
+        const int64_t at_m = rec + 1024 + (i % kLionRecordElems) * (kF32 ? 4 : 2);
         const uint32_t idx = s.idx0 + (uint32_t)i;
         const u32x4 pw = ld(reinterpret_cast<const u32x4*>(src + at));
-        const u32x2 mw = ld(reinterpret_cast<const u32x2*>(src + at_m));
+        uint32_t m_in[4];
+        if constexpr (kF32) {
+            const u32x4 mw = ld(reinterpret_cast<const u32x4*>(src + at_m));
+            m_in[0] = mw.x; m_in[1] = mw.y; m_in[2] = mw.z; m_in[3] = mw.w;
+        } else {
+            const u32x2 mw = ld(reinterpret_cast<const u32x2*>(src + at_m));
+            m_in[0] = mw.x & 0xffffu; m_in[1] = mw.x >> 16; m_in[2] = mw.y & 0xffffu; m_in[3] = mw.y >> 16;
+        }
         const bool all = i + 4 <= n;
         float g[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (vec && all) {
@@ -1104,19 +1119,20 @@ __device__ __forceinline__ void update_tile_lion_rec(const DevSeg& s, int64_t ti
                 if (i + k < n) g[k] = load1<GT>(s.g, i + k);
         }
         const uint32_t p_in[4] = {pw.x, pw.y, pw.z, pw.w};
-        const uint32_t m_in[4] = {mw.x & 0xffffu, mw.x >> 16, mw.y & 0xffffu, mw.y >> 16};
         if (prev) store_quad_out<OT>(s.out, i, n, vec && all, p_in);
         uint32_t p_out[4], m_out[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            float m = bitsf(m_in[k] << 16);
+            float m = bitsf(kF32 ? m_in[k] : m_in[k] << 16);
             const float p = lion(bitsf(p_in[k]), g[k], m, c);
             const bool in = all || i + k < n;   // padding keeps its bits
             p_out[k] = in ? fbits(p) : p_in[k];
-            m_out[k] = in ? bf16_store<SR>(m, SR ? hash32((idx + k) ^ s.seed_m) : 0u) : m_in[k];
+            if constexpr (kF32) m_out[k] = in ? fbits(m) : m_in[k];
+            else m_out[k] = in ? bf16_store<SR>(m, SR ? hash32((idx + k) ^ s.seed_m) : 0u) : m_in[k];
         }
         st(reinterpret_cast<u32x4*>(dst + at), u32x4{p_out[0], p_out[1], p_out[2], p_out[3]});
-        st(reinterpret_cast<u32x2*>(dst + at_m), u32x2{m_out[0] | (m_out[1] << 16), m_out[2] | (m_out[3] << 16)});
+        if constexpr (kF32) st(reinterpret_cast<u32x4*>(dst + at_m), u32x4{m_out[0], m_out[1], m_out[2], m_out[3]});
+        else st(reinterpret_cast<u32x2*>(dst + at_m), u32x2{m_out[0] | (m_out[1] << 16), m_out[2] | (m_out[3] << 16)});
         if (!prev) store_quad_out<OT>(s.out, i, n, vec && all, p_out);
     }
 }
@@ -1127,8 +1143,18 @@ __global__ __launch_bounds__(kThreads) void k_update_lion_rec(Launch L)
     const int64_t tile = block_tile(L);
     if (tile >= L.ntiles) return;
     const DevSeg s = find_segment(L, tile);
-    if (s.flags & kSR) update_tile_lion_rec<GT, OT, true>(s, tile, L.tile);
-    else update_tile_lion_rec<GT, OT, false>(s, tile, L.tile);
+    if (s.flags & kSR) update_tile_lion_rec<GT, OT, true, DT_BF16>(s, tile, L.tile);
+    else update_tile_lion_rec<GT, OT, false, DT_BF16>(s, tile, L.tile);
+}
+
+// The FP32 moment is stored exactly: no rounding stream, one form.
+template <int GT, int OT>
+__global__ __launch_bounds__(kThreads) void k_update_lion_f32rec(Launch L)
+{
+    const int64_t tile = block_tile(L);
+    if (tile >= L.ntiles) return;
+    const DevSeg s = find_segment(L, tile);
+    update_tile_lion_rec<GT, OT, false, DT_F32>(s, tile, L.tile);
 }
 
 // --------------------------------------------- FP32-moment AdamW record kernel
@@ -1580,12 +1606,28 @@ constexpr auto make_packed8_f24_table(std::integer_sequence<int, I...>)
 static const auto kPacked8F24 = make_packed8_f24_table<false>(std::make_integer_sequence<int, kNumPacked>{});
 static const auto kPacked8F24Wide = make_packed8_f24_table<true>(std::make_integer_sequence<int, kNumPacked>{});
 
+// Lion FP32-moment record kernels follow: index kNumKernels + 7 * kNumPacked + gt * 3 + ot.
+template <int I>
+constexpr KernelFn lion_f32rec_entry()
+{
+    constexpr int ot = I % 3, gt = I / 3;
+    return &k_update_lion_f32rec<gt ? DT_BF16 : DT_F32, ot == 0 ? DT_NONE : ot == 1 ? DT_F32 : DT_BF16>;
+}
+
+template <int... I>
+constexpr auto make_lion_f32rec_table(std::integer_sequence<int, I...>)
+{
+    return std::array<KernelFn, sizeof...(I)>{lion_f32rec_entry<I>()...};
+}
+
+static const auto kLionF32Rec = make_lion_f32rec_table(std::make_integer_sequence<int, kNumPacked>{});
+
 // Kernel family of a table index: the FP8 block kernel, or a two-element-per-lane kernel.
 inline bool kernel_is_fp8(int index)
 {
     if (index < kNumKernels) return (index / 12) % 3 == 2;
     return (index >= kNumKernels + kNumPacked && index < kNumKernels + 2 * kNumPacked) ||
-           index >= kNumKernels + 6 * kNumPacked;
+           (index >= kNumKernels + 6 * kNumPacked && index < kNumKernels + 7 * kNumPacked);
 }
 
 // Dynamic LDS (unused) per workgroup of a launch of kernel `index`: it caps the workgroups a CU holds
@@ -1599,7 +1641,9 @@ inline bool kernel_is_fp8(int index)
 //   - FP32 records, one 16.8M-element tensor (512-element tiles, two active wavefronts per
 //     workgroup; a lone launch, interleaved): 6: 0.078, 8: 0.085, 5: 0.087.
 // Lion records at the 1.5B list (338 tensors) run alike with 6 or 8 (4.00-4.03) and lose 13% with 5
-// (4.58-4.61): the segment search each workgroup makes first is hidden by fewer others there.  The
+// (4.58-4.61): the segment search each workgroup makes first is hidden by fewer others there.  Lion
+// records with an FP32 moment (family 7) gain from 6: 1.54G elements in 8 tensors 4.98 ms against
+// 5.09 at 7 and 5.15 at 8; 6.74G elements 21.02 against 21.17 and 21.38.  The
 // BF16 pairs lose with fewer workgroups (the 0.5B list: 1.76 against 1.67 ms with 6), and the
 // FP24-master FP8 kernels keep 8 (records, the 7B list: 8 per CU 16.28-16.66, 7: 16.18-16.55, 6:
 // 16.44-16.65, 5: 17.56-17.91).  Those run at the speed of their accesses alone: a form that makes
@@ -1612,8 +1656,9 @@ inline size_t launch_lds(int index)
         const int pt = (index / 6) % 2, mv = (index / 12) % 3, algo = index / 36;
         return algo == ALGO_ADAMW && mv == 2 && pt == 0 ? kCap6 : 0;
     }
-    const int family = (index - kNumKernels) / kNumPacked;   // 1: FP8 records, 3: FP32 records
-    return family == 1 || family == 3 ? kCap6 : 0;
+    // 1: FP8 records, 3: FP32 records, 7: Lion records with an FP32 moment
+    const int family = (index - kNumKernels) / kNumPacked;
+    return family == 1 || family == 3 || family == 7 ? kCap6 : 0;
 }
 
 // The FP8 kernels' form for tiles of more than one block per 16-lane group (kernel_is_fp8(index)).
@@ -1633,7 +1678,8 @@ inline KernelFn kernel_at(int index)
     if (index < kNumKernels + 4 * kNumPacked) return kF32Rec[index - kNumKernels - 3 * kNumPacked];
     if (index < kNumKernels + 5 * kNumPacked) return kF24Rec[index - kNumKernels - 4 * kNumPacked];
     if (index < kNumKernels + 6 * kNumPacked) return kLionF24Rec[index - kNumKernels - 5 * kNumPacked];
-    return kPacked8F24[index - kNumKernels - 6 * kNumPacked];
+    if (index < kNumKernels + 7 * kNumPacked) return kPacked8F24[index - kNumKernels - 6 * kNumPacked];
+    return kLionF32Rec[index - kNumKernels - 7 * kNumPacked];
 }
 
 inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
@@ -1652,6 +1698,8 @@ inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
         return kNumKernels + 5 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
     if (pt == DT_PACKED8_F24)
         return kNumKernels + 6 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
+    if (pt == DT_PACKED_LION_F32)
+        return kNumKernels + 7 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
     const int mvi = mv == DT_F32 ? 0 : mv == DT_BF16 ? 1 : 2;
     const int pti = pt == DT_F24 ? 1 : 0;
     const int gti = gt == DT_BF16 ? 1 : 0;

@@ -21,6 +21,7 @@ pairs           AdamW, FP32 master, BF16 moments       16 per 2 elements (x2 dou
 fp8-records     AdamW, FP32 master, FP8 moments        768 per 128 + two FP32 scales per 128
 fp8-f24-rec.    AdamW, FP24 master, FP8 moments        640 per 128 + two FP32 scales per 128
 lion-records    Lion, FP32 master, BF16 moment         1536 per 256 (x2 double-buffered)
+lion-f32-rec.   Lion, FP32 master, FP32 moment         2048 per 256 (x2 double-buffered)
 f32-records     AdamW, FP32 master, FP32 moments       3072 per 256 (x2 double-buffered)
 f24-records     AdamW, FP24 master, BF16 moments       1792 per 256 (x2 double-buffered)
 lion-f24-rec.   Lion, FP24 master, BF16 moment         1280 per 256 (x2 double-buffered)
@@ -43,11 +44,11 @@ from . import formats as F
 from .precision import BF16Store, FP8Store, FP24Store, FP32Store, MomentStore, load_master_, make_master, make_store
 
 __all__ = ["ParamState", "SeparateState", "PairState", "AdamRecordState", "LionRecordState", "F32RecordState",
-           "F24RecordState", "LionF24RecordState", "AdamF24RecordState", "choose_layout", "new_state", "new_states",
+           "F24RecordState", "LionF24RecordState", "AdamF24RecordState", "LionF32RecordState", "choose_layout", "new_state", "new_states",
            "arena_plan", "arena_memory", "LAYOUTS"]
 
 LAYOUTS = ("separate", "pairs", "fp8-records", "lion-records", "f32-records", "f24-records", "lion-f24-records",
-           "fp8-f24-records")
+           "fp8-f24-records", "lion-f32-records")
 IN_PLACE = ("fp8-records", "fp8-f24-records")   # never double-buffered
 
 # Arenas of at least this many bytes follow an allocate/free of their own size (new_states); None: never.
@@ -64,7 +65,8 @@ def choose_layout(algorithm: str, precision: str, master_precision: str, request
         return {("adamw", "bf16"): "f24-records", ("lion", "bf16"): "lion-f24-records",
                 ("adamw", "fp8"): "fp8-f24-records"}.get((algorithm, precision), "separate")
     return {("adamw", "bf16"): "pairs", ("adamw", "fp8"): "fp8-records", ("adamw", "fp32"): "f32-records",
-            ("lion", "bf16"): "lion-records"}.get((algorithm, precision), "separate")
+            ("lion", "bf16"): "lion-records", ("lion", "fp32"): "lion-f32-records"}.get((algorithm, precision),
+                                                                                        "separate")
 
 
 class ParamState:
@@ -472,6 +474,36 @@ class F32RecordState(_Interleaved):
         return {r: self._column(r).reshape(-1)[lo:hi] for r in ("p", "m", "v")}
 
 
+class LionF32RecordState(F32RecordState):
+    """Lion, FP32 master, FP32 moment: 2048-byte records of 256 elements, the 256 masters then the 256 m
+    values, each in element order (ADAMBRIDGE_DT_PACKED_LION_F32)."""
+
+    layout = "lion-f32-records"
+    RECORD = 2048
+    PLANE = (2048, 8)
+
+    def __init__(self, numel, device, double_buffer: bool = False, memory: list[torch.Tensor] | None = None):
+        records = max(1, -(-int(numel) // 256))
+        bufs = [m.view(records, self.RECORD) for m in memory] if memory else \
+            [torch.zeros(records, self.RECORD, dtype=torch.uint8, device=device) for _ in range(2 if double_buffer else 1)]
+        _Interleaved.__init__(self, numel, device, ("m",), bufs)
+
+    @staticmethod
+    def buffer_bytes(numel: int) -> int:
+        return max(1, -(-int(numel) // 256)) * LionF32RecordState.RECORD
+
+    def bind(self, seg):
+        super().bind(seg)
+        seg.p_dtype = _hip.DT_PACKED_LION_F32
+
+    def _column(self, role):
+        k = {"p": 0, "m": 1}[role]
+        return self.current[:, 1024 * k:1024 * (k + 1)].view(torch.float32)
+
+    def window(self, lo, hi):
+        return {r: self._column(r).reshape(-1)[lo:hi] for r in ("p", "m")}
+
+
 class F24RecordState(_Interleaved):
     """AdamW, FP24 master, BF16 moments: 1792-byte records of 256 elements, the 256 master high halves
     (BF16 bits), the 256 master low bytes, the 256 m and the 256 v values (BF16), each in element
@@ -727,7 +759,7 @@ def _bf16_bits(store: MomentStore, device) -> torch.Tensor:
 
 _INTERLEAVED = {"pairs": PairState, "lion-records": LionRecordState, "fp8-records": AdamRecordState,
                 "f32-records": F32RecordState, "f24-records": F24RecordState, "lion-f24-records": LionF24RecordState,
-                "fp8-f24-records": AdamF24RecordState}
+                "fp8-f24-records": AdamF24RecordState, "lion-f32-records": LionF32RecordState}
 ARENA_ALIGN = 2 << 20
 SMALL_ALIGN = 256
 

@@ -40,7 +40,7 @@ extern "C" {
 enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, ADAMBRIDGE_DT_FP8 = 3,
        ADAMBRIDGE_DT_F24 = 4, ADAMBRIDGE_DT_PACKED = 5, ADAMBRIDGE_DT_PACKED_FP8 = 6,
        ADAMBRIDGE_DT_PACKED_LION = 7, ADAMBRIDGE_DT_PACKED_F32 = 8, ADAMBRIDGE_DT_PACKED_F24 = 9,
-       ADAMBRIDGE_DT_PACKED_LION_F24 = 10, ADAMBRIDGE_DT_PACKED_FP8_F24 = 11 };
+       ADAMBRIDGE_DT_PACKED_LION_F24 = 10, ADAMBRIDGE_DT_PACKED_FP8_F24 = 11, ADAMBRIDGE_DT_PACKED_LION_F32 = 12 };
 
 /* ADAMBRIDGE_DT_PACKED (p_dtype; no counterpart in the reference): an HBM layout for
  * AdamW with an FP32 master and BF16 moments (mv_dtype DT_BF16).  p points at 16-byte
@@ -69,6 +69,12 @@ enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, AD
  * Slots past n are padding: those up to the end of the last element's group of 4 are written back
  * unchanged (to p_lo, when given), the rest are neither read nor written.  Same arithmetic, rounding and
  * rounding stream as the separate layout. */
+/* ADAMBRIDGE_DT_PACKED_LION_F32 (p_dtype; no counterpart in the reference): an HBM layout for
+ * Lion with an FP32 master and an FP32 moment (mv_dtype DT_F32).  p points at one 2048-byte
+ * record per 256 elements, ceil(n/256) records, 16-byte aligned: the 256 FP32 masters of elements
+ * 256r .. 256r + 255 in element order (bytes 0 .. 1023), then their 256 FP32 m values in element
+ * order (bytes 1024 .. 2047).  p_lo, padding and arithmetic as in DT_PACKED_LION; the moment is
+ * stored exactly (no rounding stream). */
 /* ADAMBRIDGE_DT_PACKED_F32 (p_dtype; no counterpart in the reference): an HBM layout for AdamW
  * with an FP32 master and FP32 moments (mv_dtype DT_F32).  p points at one 3072-byte record per
  * 256 elements, ceil(n/256) records, 16-byte aligned.  The record of elements 256r .. 256r + 255
@@ -154,10 +160,11 @@ typedef struct adambridge_group {
 typedef struct adambridge_segment {
     void* p;                 /* FP32 master, the FP24 hi plane (uint16) when p_dtype is DT_F24, or the
                                 packed state when p_dtype is DT_PACKED / DT_PACKED_FP8 / DT_PACKED_LION /
-                                DT_PACKED_F32 / DT_PACKED_F24 / DT_PACKED_LION_F24 / DT_PACKED_FP8_F24 */
+                                DT_PACKED_F32 / DT_PACKED_F24 / DT_PACKED_LION_F24 / DT_PACKED_FP8_F24 /
+                                DT_PACKED_LION_F32 */
     uint8_t* p_lo;           /* FP24 lo plane (one byte per element); NULL for FP32; DT_PACKED,
-                                DT_PACKED_LION, DT_PACKED_F32, DT_PACKED_F24 and DT_PACKED_LION_F24: the
-                                destination state
+                                DT_PACKED_LION, DT_PACKED_F32, DT_PACKED_F24, DT_PACKED_LION_F24 and
+                                DT_PACKED_LION_F32: the destination state
                                 (NULL: in place) */
     const void* g;           /* gradient, g_dtype */
     void* m;                 /* first moment, mv_dtype (FP8: E4M3 codes, padded to 128 per block) */
@@ -175,7 +182,7 @@ typedef struct adambridge_segment {
     int32_t out_dtype;
     int32_t algorithm;
     int32_t p_dtype;         /* DT_F32 (or 0), DT_F24, DT_PACKED, DT_PACKED_FP8, DT_PACKED_LION, DT_PACKED_F32,
-                                DT_PACKED_F24, DT_PACKED_LION_F24 or DT_PACKED_FP8_F24 */
+                                DT_PACKED_F24, DT_PACKED_LION_F24, DT_PACKED_FP8_F24 or DT_PACKED_LION_F32 */
     int32_t reserved;        /* 0, or ADAMBRIDGE_SEG_OUT_PREVIOUS */
 } adambridge_segment;
 
@@ -200,6 +207,7 @@ ADAMBRIDGE_API int adambridge_abi_version(void);
 #define ADAMBRIDGE_CAP_CONVERT_PLANE  0x10u   /* adambridge_convert_plane */
 #define ADAMBRIDGE_CAP_STREAM_COPY    0x20u   /* adambridge_stream_copy, adambridge_recycle_device_memory */
 #define ADAMBRIDGE_CAP_FP8_F24_RECORDS 0x40u  /* p_dtype DT_PACKED_FP8_F24 (11) */
+#define ADAMBRIDGE_CAP_LION_F32_RECORDS 0x80u /* p_dtype DT_PACKED_LION_F32 (12) */
 ADAMBRIDGE_API uint32_t adambridge_capabilities(void);
 
 /* kernels.c:1495-1510.  The level whose results are reproduced: its vector
@@ -322,7 +330,7 @@ ADAMBRIDGE_API int adambridge_convert(const void* src, const float* src_scale, i
  * interleaved layouts at a state buffer s are the planes
  *     DT_PACKED           {s, NULL, 16, DT_F32, 1}       DT_PACKED_LION      {s, NULL, 1536, DT_F32, 8}
  *     DT_PACKED_F32       {s, NULL, 3072, DT_F32, 8}     DT_PACKED_F24       {s, s + 512, 1792, DT_F24, 8}
- *     DT_PACKED_LION_F24  {s, s + 512, 1280, DT_F24, 8}
+ *     DT_PACKED_LION_F24  {s, s + 512, 1280, DT_F24, 8}   DT_PACKED_LION_F32  {s, NULL, 2048, DT_F32, 8}
  * and a separate FP24 master is {hi, lo, 0, DT_F24, 0}.  data is aligned to its value size (16 bytes
  * for DT_PACKED_FP8) and stride a multiple of it. */
 typedef struct adambridge_plane {

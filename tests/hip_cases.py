@@ -432,27 +432,34 @@ def run_hip_lion_records(cases: list[O.Case], width: int = 16, double_buffer: bo
     return work
 
 
+def _f32_record_keys(case: O.Case) -> tuple[str, ...]:
+    return ("p", "m") if case.algorithm == O.LION else ("p", "m", "v")
+
+
 def pack_f32_records(case: O.Case) -> np.ndarray:
     """Separate FP32 master, m and v -> ADAMBRIDGE_DT_PACKED_F32 records (records x 3072 bytes): per
-    256 elements, the 256 masters, the 256 m, the 256 v, each in element order.  Padding slots hold
-    a fixed NaN pattern so that a test can see the kernel leave them unchanged."""
+    256 elements, the 256 masters, the 256 m, the 256 v, each in element order; for a Lion case
+    ADAMBRIDGE_DT_PACKED_LION_F32 records (records x 2048 bytes: masters, then m).  Padding slots
+    hold a fixed NaN pattern so that a test can see the kernel leave them unchanged."""
     n = case.n
     nr = max(1, -(-n // 256))
-    rec = np.zeros((nr, 3, 256), np.uint32)
-    for k, key in enumerate(("p", "m", "v")):
+    keys = _f32_record_keys(case)
+    rec = np.zeros((nr, len(keys), 256), np.uint32)
+    for k, key in enumerate(keys):
         col = np.full(nr * 256, 0x7FA5A5A5 + k, np.uint32)
         col[:n] = case.arrays[key].view(np.uint32)
         rec[:, k, :] = col.reshape(nr, 256)
-    return rec.reshape(nr, 768).view(np.uint8).reshape(nr, 3072)
+    return rec.reshape(nr, 256 * len(keys)).view(np.uint8).reshape(nr, 1024 * len(keys))
 
 
 def unpack_f32_records(case: O.Case, rec: np.ndarray) -> list[np.ndarray]:
-    """ADAMBRIDGE_DT_PACKED_F32 records -> the case's separate master, m and v (in place); returns
-    the padding slots (bits) past n of each."""
+    """FP32 records (ADAMBRIDGE_DT_PACKED_F32, or _LION_F32 for a Lion case) -> the case's separate
+    master and moments (in place); returns the padding slots (bits) past n of each."""
     n = case.n
-    cols = np.ascontiguousarray(rec).view(np.uint32).reshape(-1, 3, 256)
+    keys = _f32_record_keys(case)
+    cols = np.ascontiguousarray(rec).view(np.uint32).reshape(-1, len(keys), 256)
     pads = []
-    for k, key in enumerate(("p", "m", "v")):
+    for k, key in enumerate(keys):
         col = cols[:, k, :].reshape(-1)
         case.arrays[key] = col[:n].view(np.float32).copy()
         pads.append(col[n:].copy())
@@ -497,7 +504,14 @@ def unpack_f24_records(case: O.Case, rec: np.ndarray) -> list[np.ndarray]:
 _RECORDS = {"f32": (_hip.DT_PACKED_F32, O.DT_F32, O.DT_F32, pack_f32_records, unpack_f32_records, O.ADAMW),
             "f24": (_hip.DT_PACKED_F24, O.DT_BF16, O.DT_F24, pack_f24_records, unpack_f24_records, O.ADAMW),
             "lion-f24": (_hip.DT_PACKED_LION_F24, O.DT_BF16, O.DT_F24, pack_f24_records, unpack_f24_records,
+                         O.LION),
+            "lion-f32": (_hip.DT_PACKED_LION_F32, O.DT_F32, O.DT_F32, pack_f32_records, unpack_f32_records,
                          O.LION)}
+
+
+def run_hip_lion_f32_records(cases: list[O.Case], width: int = 16, **kw) -> list[O.Case]:
+    """run_hip for Lion / FP32 master / FP32 moment cases through ADAMBRIDGE_DT_PACKED_LION_F32."""
+    return run_hip_f32_records(cases, width, kind="lion-f32", **kw)
 
 
 def run_hip_f24_records(cases: list[O.Case], width: int = 16, **kw) -> list[O.Case]:

@@ -558,6 +558,83 @@ def test_f32_records_reject_bad_segments():
     assert torch.count_nonzero(rec).item() == 0   # nothing ran
 
 
+# ------------------------------------------------ Lion FP32-moment records
+
+from hip_cases import run_hip_lion_f32_records  # noqa: E402
+
+
+@pytest.mark.parametrize("double_buffer", [False, True])
+def test_lion_f32_records_match_oracle(double_buffer):
+    """ADAMBRIDGE_DT_PACKED_LION_F32 (master and m FP32 in 2048-byte records) gives the separate
+    layout's bytes: sizes around the record and the lane's 4 elements, offsets, every grad/out dtype
+    (Lion fuses every element, so no tail forms); in place, the padding slots of the last record keep
+    their bits."""
+    rng = np.random.default_rng(61)
+    cases = []
+    for gt, ot, n in itertools.product([O.DT_BF16, O.DT_F32], [O.DT_NONE, O.DT_F32, O.DT_BF16],
+                                       [1, 2, 3, 4, 5, 15, 16, 17, 255, 256, 257, 1000, 2048 + 77, 5001]):
+        cases.append(O.make_case(rng, n, algorithm=O.LION, mv_dtype=O.DT_F32, g_dtype=gt, out_dtype=ot,
+                                 stochastic=bool(rng.integers(0, 2)), offset=int(rng.integers(0, 2**32)),
+                                 index=int(rng.integers(0, 999)), step=int(rng.integers(1, 30))))
+    want = O.run_many(cases, "oracle", 16)
+    pads: list = []
+    got = run_hip_lion_f32_records(cases, 16, double_buffer=double_buffer, padding=pads)
+    for w, g in zip(want, got):
+        check(w, g)
+    if not double_buffer:
+        for pad, c in zip(pads, cases):
+            for k, col in enumerate(pad):
+                assert (col == 0x7FA5A5A5 + k).all(), f"padding changed at n={c.n}"
+
+
+def test_lion_f32_records_zero_gradients_misaligned_and_specials():
+    """Exact zero gradients (sign(0) = 0), gradients shifted by one element (the element-wise path)
+    and by two, and non-finite inputs (zeros, subnormals, infinities, NaNs in every input)."""
+    rng = np.random.default_rng(62)
+    cases = [O.make_case(rng, n, algorithm=O.LION, mv_dtype=O.DT_F32, special=sp) for n, sp in
+             ((999, False), (4096, False), (4096, True), (5001, True))]
+    cases[1].arrays["g"][::3] = 0
+    want = O.run_many(cases, "oracle", 16)
+    for shift in (0, 1, 2):
+        got = run_hip_lion_f32_records(cases, 16, misalign_g=shift)
+        for w, g in zip(want, got):
+            bad = O.outputs_equal(w, g, nan_equiv=True)
+            assert not bad, (shift, bad)
+
+
+def test_lion_f32_records_multi_step_groups_and_steps():
+    """Several segments per call through the group path, then three consecutive steps of one."""
+    rng = np.random.default_rng(63)
+    cases = [O.make_case(rng, n, algorithm=O.LION, mv_dtype=O.DT_F32, explicit=False, index=i, step=2 + i)
+             for i, n in enumerate([700, 4096, 5001])]
+    for w, g in zip(O.run_many(cases, "oracle", 16), run_hip_lion_f32_records(cases, 16)):
+        check(w, g)
+    case = O.make_case(rng, 3000, algorithm=O.LION, mv_dtype=O.DT_F32, explicit=False)
+    grads = [O.make_case(rng, 3000, mv_dtype=O.DT_F32).arrays["g"] for _ in range(3)]
+    check(run_steps(case, grads, oracle_runner, 16), run_steps(case, grads, run_hip_lion_f32_records, 16))
+
+
+def test_lion_f32_records_reject_bad_segments():
+    """AdamW (-12), a BF16 moment (-4), a missing gradient (-2) and misaligned records (-14), before
+    anything runs."""
+    import ctypes
+    from adambridge_amd import _hip
+    rng = np.random.default_rng(64)
+    k = _hip.load()
+    case = O.make_case(rng, 300, algorithm=O.LION, mv_dtype=O.DT_F32)
+    rec = torch.zeros(2 * 2048 + 16, dtype=torch.uint8, device="cuda")
+    g = torch.zeros(300, dtype=torch.bfloat16, device="cuda")
+    hp = _hip.HParams(**{kk: case.hparams[kk] for kk, _ in _hip.HParams._fields_})
+    base = dict(p=rec.data_ptr(), g=g.data_ptr(), n=300, step=1, mv_dtype=O.DT_F32, g_dtype=O.DT_BF16,
+                out_dtype=0, algorithm=1, p_dtype=_hip.DT_PACKED_LION_F32)
+    for change, code in ((dict(algorithm=0), -12), (dict(mv_dtype=O.DT_BF16), -4), (dict(g=None), -2),
+                         (dict(p=rec.data_ptr() + 8), -14), (dict(p_lo=rec.data_ptr() + 4), -14)):
+        seg = _hip.Segment(**{**base, **change})
+        with pytest.raises(RuntimeError, match=rf"code {code}"):
+            k.multi_apply(None, k.segment_array([ctypes.pointer(seg)]), [hp])
+    assert torch.count_nonzero(rec).item() == 0   # nothing ran
+
+
 # ------------------------------------------------ fused_adamw, pools, streams
 
 @pytest.mark.parametrize("mv", [O.DT_F32, O.DT_BF16])
@@ -707,12 +784,13 @@ def _previous_weight(case):
 
 
 @pytest.mark.parametrize("layout", ["separate", "pairs", "fp8-records", "lion-records", "f32-records", "f24-records",
-                                    "lion-f24-records", "fp8-f24-records"])
+                                    "lion-f24-records", "fp8-f24-records", "lion-f32-records"])
 def test_out_previous_writes_the_weight_from_before_the_update(layout):
     """ADAMBRIDGE_SEG_OUT_PREVIOUS (delayed updates): out receives the weight of the master as stored
     before the update -- FP32, or bf16 by the kernels' rounding of FP32 and decoded FP24 masters,
     NaN masters included -- and the state is updated exactly as without the flag."""
-    from hip_cases import run_hip_f24_records, run_hip_f32_records, run_hip_lion_records, run_hip_packed, run_hip_records
+    from hip_cases import (run_hip_f24_records, run_hip_f32_records, run_hip_lion_f32_records, run_hip_lion_records,
+                           run_hip_packed, run_hip_records)
     from adambridge_amd import _hip
 
     rng = np.random.default_rng(31 + len(layout) + (layout == "f24-records"))
@@ -720,11 +798,12 @@ def test_out_previous_writes_the_weight_from_before_the_update(layout):
               "pairs": [(O.ADAMW, O.DT_BF16, O.DT_F32)], "fp8-records": [(O.ADAMW, O.DT_FP8, O.DT_F32)],
               "lion-records": [(O.LION, O.DT_BF16, O.DT_F32)], "f32-records": [(O.ADAMW, O.DT_F32, O.DT_F32)],
               "f24-records": [(O.ADAMW, O.DT_BF16, O.DT_F24)], "lion-f24-records": [(O.LION, O.DT_BF16, O.DT_F24)],
-              "fp8-f24-records": [(O.ADAMW, O.DT_FP8, O.DT_F24)]}[layout]
+              "fp8-f24-records": [(O.ADAMW, O.DT_FP8, O.DT_F24)],
+              "lion-f32-records": [(O.LION, O.DT_F32, O.DT_F32)]}[layout]
     runner = {"separate": run_hip, "pairs": run_hip_packed, "fp8-records": run_hip_records,
               "lion-records": run_hip_lion_records, "f32-records": run_hip_f32_records,
               "f24-records": run_hip_f24_records, "lion-f24-records": run_hip_f24_records,
-              "fp8-f24-records": run_hip_records}[layout]
+              "fp8-f24-records": run_hip_records, "lion-f32-records": run_hip_lion_f32_records}[layout]
     cases = []
     for (algo, mv, pt), gt, ot, sr, n in itertools.product(combos, [O.DT_BF16, O.DT_F32], [O.DT_F32, O.DT_BF16],
                                                              [True, False], [1, 15, 17, 129, 1000, 8192 + 77]):
