@@ -1643,7 +1643,10 @@ inline bool kernel_is_fp8(int index)
 // Lion records at the 1.5B list (338 tensors) run alike with 6 or 8 (4.00-4.03) and lose 13% with 5
 // (4.58-4.61): the segment search each workgroup makes first is hidden by fewer others there.  Lion
 // records with an FP32 moment (family 7) gain from 6: 1.54G elements in 8 tensors 4.98 ms against
-// 5.09 at 7 and 5.15 at 8; 6.74G elements 21.02 against 21.17 and 21.38.  The
+// 5.09 at 7 and 5.15 at 8; 6.74G elements 21.02 against 21.17 and 21.38.  Lion with an FP8 moment
+// in separate arrays (1.54G elements in 8 tensors) is fastest at 5 with an FP32 master (3.68-3.71 ms;
+// 4: 3.70, 3: 3.74, 6: 3.89, 8: 3.97, 2: 4.58) and at 6 with an FP24 master (3.15 ms; 5 and 4:
+// 3.18, 8: 3.21).  The
 // BF16 pairs lose with fewer workgroups (the 0.5B list: 1.76 against 1.67 ms with 6), and the
 // FP24-master FP8 kernels keep 8 (records, the 7B list: 8 per CU 16.28-16.66, 7: 16.18-16.55, 6:
 // 16.44-16.65, 5: 17.56-17.91).  Those run at the speed of their accesses alone: a form that makes
@@ -1652,9 +1655,12 @@ inline bool kernel_is_fp8(int index)
 inline size_t launch_lds(int index)
 {
     constexpr size_t kCap6 = 24 * 1024;   // 6 workgroups of 24 KiB in 160 KiB; 7 would need 168
+    constexpr size_t kCap5 = 32 * 1024;   // 5 of 32 KiB; 6 would need 192
     if (index < kNumKernels) {
         const int pt = (index / 6) % 2, mv = (index / 12) % 3, algo = index / 36;
-        return algo == ALGO_ADAMW && mv == 2 && pt == 0 ? kCap6 : 0;
+        if (mv != 2) return 0;   // FP8 moments only
+        if (algo == ALGO_ADAMW) return pt == 0 ? kCap6 : 0;
+        return pt == 0 ? kCap5 : kCap6;   // Lion: FP32 / FP24 master
     }
     // 1: FP8 records, 3: FP32 records, 7: Lion records with an FP32 moment
     const int family = (index - kNumKernels) / kNumPacked;
