@@ -21,7 +21,8 @@
 // per block (one DPP row), the two block maxima reduced by DPP row maxima, codes and
 // scales written by the same lanes (kernels.c:1034-1059).  In the block-record layout
 // (DT_PACKED8) a block's master and both code arrays are one 768-byte record, read
-// and written with three 16-byte accesses per lane.
+// and written with three 16-byte accesses per lane; Lion's (DT_PACKED8_LION) is a
+// 640-byte record of the same masters and the m codes (two 16-byte and one 8-byte access).
 //
 // Segment descriptors travel in the kernel arguments when a call has at most
 // kInline segments (the per-parameter hook path: no copy at all), otherwise in
@@ -230,10 +231,16 @@ __device__ __forceinline__ void store8_f32(void* p, const float (&x)[8])
 // the lane's three 16-byte accesses is one contiguous 256-byte span per block.
 constexpr int64_t kRecordBytes = 768;
 
-// Byte offset of element i's master value within the records.
-__device__ __forceinline__ int64_t record_master_offset(int64_t i)
+// Lion FP8 records (p_dtype DT_PACKED8_LION): the FP32 master and the m codes of a 128-element block
+// in one 640-byte record, the masters as in DT_PACKED8 (bytes 0 .. 511) and the block's 128 E4M3 codes
+// in element order at 512 (lane l's 8 at 512 + 8l).  Lane l's three accesses (two 16-byte master
+// halves, 8 bytes of codes) are each one contiguous span per block.
+constexpr int64_t kRecordBytesLion8 = 640;
+
+// Byte offset of element i's master value within records of rec bytes (768 or 640).
+__device__ __forceinline__ int64_t record_master_offset(int64_t i, int64_t rec = kRecordBytes)
 {
-    return (i >> 7) * kRecordBytes + ((i & 4) ? 256 : 0) + ((i >> 3) & 15) * 16 + (i & 3) * 4;
+    return (i >> 7) * rec + ((i & 4) ? 256 : 0) + ((i >> 3) & 15) * 16 + (i & 3) * 4;
 }
 
 // FP8 records with an FP24 master (p_dtype DT_PACKED8_F24): per 128-element block one 640-byte record,
@@ -414,8 +421,9 @@ __device__ __forceinline__ float load_master1(const DevSeg& s, int64_t i)
         const uint8_t* r = static_cast<const uint8_t*>(s.p);
         return bitsf(((uint32_t)ld(reinterpret_cast<const uint16_t*>(r + record_f24_hi_offset(i))) << 16) |
                      ((uint32_t)ld(r + record_f24_lo_offset(i)) << 8));
-    } else if constexpr (PT == DT_PACKED8)
-        return ld(reinterpret_cast<const float*>(static_cast<const uint8_t*>(s.p) + record_master_offset(i)));
+    } else if constexpr (PT == DT_PACKED8 || PT == DT_PACKED8_LION)
+        return ld(reinterpret_cast<const float*>(static_cast<const uint8_t*>(s.p) +
+                                                 record_master_offset(i, PT == DT_PACKED8 ? kRecordBytes : kRecordBytesLion8)));
     else return ld(static_cast<const float*>(s.p) + i);
 }
 
@@ -433,8 +441,9 @@ __device__ __forceinline__ float store_master1(const DevSeg& s, int64_t i, float
         st(reinterpret_cast<uint16_t*>(r + record_f24_hi_offset(i)), (uint16_t)(b >> 16));
         st(r + record_f24_lo_offset(i), (uint8_t)(b >> 8));
         return bitsf(b);
-    } else if constexpr (PT == DT_PACKED8) {
-        st(reinterpret_cast<float*>(static_cast<uint8_t*>(s.p) + record_master_offset(i)), x);
+    } else if constexpr (PT == DT_PACKED8 || PT == DT_PACKED8_LION) {
+        st(reinterpret_cast<float*>(static_cast<uint8_t*>(s.p) +
+                                    record_master_offset(i, PT == DT_PACKED8 ? kRecordBytes : kRecordBytesLion8)), x);
         return x;
     } else {
         st(static_cast<float*>(s.p) + i, x);
@@ -666,11 +675,15 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
 {
     constexpr bool kLion = ALGO == ALGO_LION;
     constexpr int kGB = GT == DT_BF16 ? 2 : 4, kOB = OT == DT_BF16 ? 2 : 4, kPB = PT == DT_F24 ? 2 : 4;
-    // block records (AdamW only): FP32 master (DT_PACKED8) or FP24 master (DT_PACKED8_F24)
-    constexpr bool kRec = PT == DT_PACKED8 || PT == DT_PACKED8_F24;
-    constexpr uint32_t kRecB = PT == DT_PACKED8 ? (uint32_t)kRecordBytes : (uint32_t)kRecordBytesF24;
-    constexpr uint32_t kCodesAt = PT == DT_PACKED8 ? 512u : 384u;   // the codes' slots in a record
-    constexpr int kMaster = PT == DT_PACKED8_F24 ? DT_F24 : PT;     // how the 8 masters are coded
+    // block records: AdamW with an FP32 master (DT_PACKED8) or an FP24 master (DT_PACKED8_F24), Lion
+    // with an FP32 master (DT_PACKED8_LION: the m codes in element order at 512)
+    constexpr bool kRec = PT == DT_PACKED8 || PT == DT_PACKED8_F24 || PT == DT_PACKED8_LION;
+    constexpr bool kRecLion = PT == DT_PACKED8_LION;
+    constexpr uint32_t kRecB = PT == DT_PACKED8 ? (uint32_t)kRecordBytes
+                             : kRecLion ? (uint32_t)kRecordBytesLion8 : (uint32_t)kRecordBytesF24;
+    constexpr uint32_t kCodesAt = PT == DT_PACKED8 ? 512u : 384u;   // the AdamW records' code slots
+    constexpr uint32_t kLoAt = kRecLion ? 512u : 256u;              // the 8-byte slots: low bytes, Lion codes
+    constexpr int kMaster = PT == DT_PACKED8_F24 ? DT_F24 : kRecLion ? DT_PACKED8 : PT;   // how the 8 masters are coded
     const int64_t n = s.n, n_main = s.n_main;
     const bool vec = FULL || (s.flags & kVec) != 0;
     uint8_t* const mq = static_cast<uint8_t*>(s.m);
@@ -683,11 +696,11 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     const uint32_t blk = off >> 7;                   // the block within this pass
     const int64_t ublk = base / kFp8Block;           // the pass's first block
     // records: the lane's 16-byte slot in its block's record (FP24 master high halves, or the
-    // first half of an FP32 master with the second 256 bytes on; the codes kCodesAt bytes on) and,
-    // FP24 planes, its 8-byte slot of low bytes.  Computed once: the stores take them again
+    // first half of an FP32 master with the second 256 bytes on; AdamW's codes kCodesAt bytes on) and
+    // its 8-byte slot (FP24 low bytes; Lion's codes).  Computed once: the stores take them again
     // through fresh(), which keeps their scalar-base form without recomputing them.
     const uint32_t rec_lane = blk * kRecB + lane * 16u;
-    const uint32_t rec_lo = blk * kRecB + 256u + lane * 8u;
+    const uint32_t rec_lo = blk * kRecB + kLoAt + lane * 8u;
     // Block scales: ordinary (cached) accesses.  A wavefront reads and writes 16 bytes of each
     // scale array, four blocks' worth; through L2 the four wavefronts of a workgroup share whole
     // lines, where non-temporal accesses sent each 16-byte piece to HBM on its own (measured: the
@@ -711,7 +724,9 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     };
     // codes are stored padded to whole blocks, so all 8 of this lane's exist
     u32x2 cm, cv = {0u, 0u};
-    if constexpr (kRec) {   // AdamW only
+    if constexpr (kRecLion) {
+        cm = ld(lane_ptr<const u32x2>(s.p, ublk * kRecB, rec_lo));
+    } else if constexpr (kRec) {
         const u32x4 w = ld(lane_ptr<const u32x4>(s.p, ublk * kRecB, rec_lane + kCodesAt));
         cm = u32x2{w.x, w.y};
         cv = u32x2{w.z, w.w};
@@ -872,7 +887,9 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
         }
     }
     const uint32_t o = fresh(off);
-    if constexpr (kRec) {
+    if constexpr (kRecLion) {
+        st(lane_ptr<u32x2>(s.p, ublk * kRecB, fresh(rec_lo)), u32x2{qm[0], qm[1]});
+    } else if constexpr (kRec) {
         st(lane_ptr<u32x4>(s.p, ublk * kRecB, fresh(rec_lane) + kCodesAt), u32x4{qm[0], qm[1], qv[0], qv[1]});
     } else if (vec) {
         st(lane_ptr<u32x2>(mq, base, o), u32x2{qm[0], qm[1]});
@@ -1622,12 +1639,31 @@ constexpr auto make_lion_f32rec_table(std::integer_sequence<int, I...>)
 
 static const auto kLionF32Rec = make_lion_f32rec_table(std::make_integer_sequence<int, kNumPacked>{});
 
+// Lion FP8 records follow: index kNumKernels + 8 * kNumPacked + gt * 3 + ot.
+template <int I, bool WIDE>
+constexpr KernelFn packed8_lion_entry()
+{
+    constexpr int ot = I % 3, gt = I / 3;
+    return &k_update_fp8<ALGO_LION, DT_PACKED8_LION, gt ? DT_BF16 : DT_F32, ot == 0 ? DT_NONE : ot == 1 ? DT_F32 : DT_BF16,
+                         WIDE>;
+}
+
+template <bool WIDE, int... I>
+constexpr auto make_packed8_lion_table(std::integer_sequence<int, I...>)
+{
+    return std::array<KernelFn, sizeof...(I)>{packed8_lion_entry<I, WIDE>()...};
+}
+
+static const auto kPacked8Lion = make_packed8_lion_table<false>(std::make_integer_sequence<int, kNumPacked>{});
+static const auto kPacked8LionWide = make_packed8_lion_table<true>(std::make_integer_sequence<int, kNumPacked>{});
+
 // Kernel family of a table index: the FP8 block kernel, or a two-element-per-lane kernel.
 inline bool kernel_is_fp8(int index)
 {
     if (index < kNumKernels) return (index / 12) % 3 == 2;
     return (index >= kNumKernels + kNumPacked && index < kNumKernels + 2 * kNumPacked) ||
-           (index >= kNumKernels + 6 * kNumPacked && index < kNumKernels + 7 * kNumPacked);
+           (index >= kNumKernels + 6 * kNumPacked && index < kNumKernels + 7 * kNumPacked) ||
+           index >= kNumKernels + 8 * kNumPacked;
 }
 
 // Dynamic LDS (unused) per workgroup of a launch of kernel `index`: it caps the workgroups a CU holds
@@ -1662,8 +1698,9 @@ inline size_t launch_lds(int index)
         if (algo == ALGO_ADAMW) return pt == 0 ? kCap6 : 0;
         return pt == 0 ? kCap5 : kCap6;   // Lion: FP32 / FP24 master
     }
-    // 1: FP8 records, 3: FP32 records, 7: Lion records with an FP32 moment
+    // 1: FP8 records, 3: FP32 records, 7: Lion records with an FP32 moment, 8: Lion FP8 records
     const int family = (index - kNumKernels) / kNumPacked;
+    if (family == 8) return kCap5;
     return family == 1 || family == 3 || family == 7 ? kCap6 : 0;
 }
 
@@ -1672,7 +1709,8 @@ inline KernelFn wide_kernel_at(int index)
 {
     if (index < kNumKernels) return kKernelsWide[index];
     if (index < kNumKernels + 2 * kNumPacked) return kPacked8Wide[index - kNumKernels - kNumPacked];
-    return kPacked8F24Wide[index - kNumKernels - 6 * kNumPacked];
+    if (index < kNumKernels + 7 * kNumPacked) return kPacked8F24Wide[index - kNumKernels - 6 * kNumPacked];
+    return kPacked8LionWide[index - kNumKernels - 8 * kNumPacked];
 }
 
 inline KernelFn kernel_at(int index)
@@ -1685,7 +1723,8 @@ inline KernelFn kernel_at(int index)
     if (index < kNumKernels + 5 * kNumPacked) return kF24Rec[index - kNumKernels - 4 * kNumPacked];
     if (index < kNumKernels + 6 * kNumPacked) return kLionF24Rec[index - kNumKernels - 5 * kNumPacked];
     if (index < kNumKernels + 7 * kNumPacked) return kPacked8F24[index - kNumKernels - 6 * kNumPacked];
-    return kLionF32Rec[index - kNumKernels - 7 * kNumPacked];
+    if (index < kNumKernels + 8 * kNumPacked) return kLionF32Rec[index - kNumKernels - 7 * kNumPacked];
+    return kPacked8Lion[index - kNumKernels - 8 * kNumPacked];
 }
 
 inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
@@ -1706,6 +1745,8 @@ inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
         return kNumKernels + 6 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
     if (pt == DT_PACKED_LION_F32)
         return kNumKernels + 7 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
+    if (pt == DT_PACKED8_LION)
+        return kNumKernels + 8 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
     const int mvi = mv == DT_F32 ? 0 : mv == DT_BF16 ? 1 : 2;
     const int pti = pt == DT_F24 ? 1 : 0;
     const int gti = gt == DT_BF16 ? 1 : 0;
@@ -1818,7 +1859,7 @@ inline ConvertFn convert_kernel(int src, int dst, bool v)
 // is a base address and a group structure: element i lives at data + (i >> shift) * stride +
 // (i & (2^shift - 1)) * size (stride 0: contiguous), which describes the separate arrays and the
 // master columns of the interleaved layouts alike; DT_PACKED8 names the masters of FP8 block
-// records (record_master_offset).  One element per lane, grid-stride.
+// records (record_master_offset), the stride then the record size.  One element per lane, grid-stride.
 
 struct DevPlane {
     uint8_t* data;
@@ -1840,7 +1881,7 @@ template <int DT>
 __device__ __forceinline__ uint32_t plane_load(const DevPlane& q, int64_t i)
 {
     if constexpr (DT == DT_F32) return ld(reinterpret_cast<const uint32_t*>(q.data + plane_at(q, i, 4)));
-    else if constexpr (DT == DT_PACKED8) return ld(reinterpret_cast<const uint32_t*>(q.data + record_master_offset(i)));
+    else if constexpr (DT == DT_PACKED8) return ld(reinterpret_cast<const uint32_t*>(q.data + record_master_offset(i, q.stride)));
     else if constexpr (DT == DT_BF16) return (uint32_t)ld(reinterpret_cast<const uint16_t*>(q.data + plane_at(q, i, 2))) << 16;
     else
         return ((uint32_t)ld(reinterpret_cast<const uint16_t*>(q.data + plane_at(q, i, 2))) << 16) |
@@ -1853,7 +1894,7 @@ template <int DT, bool SR>
 __device__ __forceinline__ void plane_store(const DevPlane& q, int64_t i, uint32_t b, bool exact, uint32_t r)
 {
     if constexpr (DT == DT_F32) st(reinterpret_cast<uint32_t*>(q.data + plane_at(q, i, 4)), b);
-    else if constexpr (DT == DT_PACKED8) st(reinterpret_cast<uint32_t*>(q.data + record_master_offset(i)), b);
+    else if constexpr (DT == DT_PACKED8) st(reinterpret_cast<uint32_t*>(q.data + record_master_offset(i, q.stride)), b);
     else if constexpr (DT == DT_BF16) {
         const uint32_t h = exact ? b >> 16 : bf16_store<SR>(bitsf(b), r);   // nearest: the working weight's rule
         st(reinterpret_cast<uint16_t*>(q.data + plane_at(q, i, 2)), (uint16_t)h);

@@ -22,6 +22,7 @@ fp8-records     AdamW, FP32 master, FP8 moments        768 per 128 + two FP32 sc
 fp8-f24-rec.    AdamW, FP24 master, FP8 moments        640 per 128 + two FP32 scales per 128
 lion-records    Lion, FP32 master, BF16 moment         1536 per 256 (x2 double-buffered)
 lion-f32-rec.   Lion, FP32 master, FP32 moment         2048 per 256 (x2 double-buffered)
+lion-fp8-rec.   Lion, FP32 master, FP8 moment          640 per 128 + one FP32 scale per 128
 f32-records     AdamW, FP32 master, FP32 moments       3072 per 256 (x2 double-buffered)
 f24-records     AdamW, FP24 master, BF16 moments       1792 per 256 (x2 double-buffered)
 lion-f24-rec.   Lion, FP24 master, BF16 moment         1280 per 256 (x2 double-buffered)
@@ -44,12 +45,12 @@ from . import formats as F
 from .precision import BF16Store, FP8Store, FP24Store, FP32Store, MomentStore, load_master_, make_master, make_store
 
 __all__ = ["ParamState", "SeparateState", "PairState", "AdamRecordState", "LionRecordState", "F32RecordState",
-           "F24RecordState", "LionF24RecordState", "AdamF24RecordState", "LionF32RecordState", "choose_layout", "new_state", "new_states",
+           "F24RecordState", "LionF24RecordState", "AdamF24RecordState", "LionF32RecordState", "LionFP8RecordState", "choose_layout", "new_state", "new_states",
            "arena_plan", "arena_memory", "LAYOUTS"]
 
 LAYOUTS = ("separate", "pairs", "fp8-records", "lion-records", "f32-records", "f24-records", "lion-f24-records",
-           "fp8-f24-records", "lion-f32-records")
-IN_PLACE = ("fp8-records", "fp8-f24-records")   # never double-buffered
+           "fp8-f24-records", "lion-f32-records", "lion-fp8-records")
+IN_PLACE = ("fp8-records", "fp8-f24-records", "lion-fp8-records")   # never double-buffered
 
 # Arenas of at least this many bytes follow an allocate/free of their own size (new_states); None: never.
 RECYCLE_MIN_BYTES: int | None = 256 << 20
@@ -65,7 +66,8 @@ def choose_layout(algorithm: str, precision: str, master_precision: str, request
         return {("adamw", "bf16"): "f24-records", ("lion", "bf16"): "lion-f24-records",
                 ("adamw", "fp8"): "fp8-f24-records"}.get((algorithm, precision), "separate")
     return {("adamw", "bf16"): "pairs", ("adamw", "fp8"): "fp8-records", ("adamw", "fp32"): "f32-records",
-            ("lion", "bf16"): "lion-records", ("lion", "fp32"): "lion-f32-records"}.get((algorithm, precision),
+            ("lion", "bf16"): "lion-records", ("lion", "fp32"): "lion-f32-records",
+            ("lion", "fp8"): "lion-fp8-records"}.get((algorithm, precision),
                                                                                         "separate")
 
 
@@ -748,6 +750,45 @@ class AdamF24RecordState(AdamRecordState):
         return out
 
 
+class LionFP8RecordState(AdamRecordState):
+    """Lion, FP32 master, FP8 moment: one 640-byte record per 128-element block
+    (ADAMBRIDGE_DT_PACKED_LION_FP8) -- the masters as in the AdamW FP8 records (lane l's elements
+    8l .. 8l + 7 at 16l and 256 + 16l), then the block's 128 m codes in element order at 512 -- plus
+    the FP32 m block scales.  Updated in place."""
+
+    layout = "lion-fp8-records"
+    RECORD = 640   # master_plane's record stride too
+
+    def __init__(self, numel, device, double_buffer: bool = False, memory: list[torch.Tensor] | None = None):
+        self.blocks = F.fp8_blocks(int(numel))
+        rec = memory[0].view(self.blocks, self.RECORD) if memory else \
+            torch.zeros(self.blocks, self.RECORD, dtype=torch.uint8, device=device)
+        _Interleaved.__init__(self, numel, device, ("m",), [rec])   # updated in place: never double-buffered
+        self.scales = {"m": torch.ones(self.blocks, dtype=torch.float32, device=device)}
+
+    @staticmethod
+    def buffer_bytes(numel: int) -> int:
+        return F.fp8_blocks(int(numel)) * LionFP8RecordState.RECORD
+
+    def bind(self, seg):
+        seg.p, seg.p_lo, seg.m, seg.v = self.current.data_ptr(), None, None, None
+        seg.m_scale, seg.v_scale = self.scales["m"].data_ptr(), None
+        seg.p_dtype, seg.mv_dtype = _hip.DT_PACKED8_LION, _hip.DT_FP8
+
+    def _column(self, role):
+        if role == "p":
+            return super()._column("p")
+        return self.current[:, 512:].view(self.blocks, 16, 8)   # 'm': element order
+
+    def master_plane(self):
+        return _hip.Plane(self.current.data_ptr(), None, self.RECORD, _hip.DT_PACKED8, 0)
+
+    def window(self, lo, hi):
+        b0, b1 = lo // 128, -(-hi // 128)
+        return {"p": self._column("p").reshape(-1)[lo:hi], "m": self._column("m")[b0:b1].reshape(-1),
+                "m_scale": self.scales["m"][b0:b1]}
+
+
 def _bf16_bits(store: MomentStore, device) -> torch.Tensor:
     """A moment's values as BF16 (the store's own bits when it is BF16, nearest-even otherwise)."""
     if isinstance(store, BF16Store):
@@ -759,7 +800,8 @@ def _bf16_bits(store: MomentStore, device) -> torch.Tensor:
 
 _INTERLEAVED = {"pairs": PairState, "lion-records": LionRecordState, "fp8-records": AdamRecordState,
                 "f32-records": F32RecordState, "f24-records": F24RecordState, "lion-f24-records": LionF24RecordState,
-                "fp8-f24-records": AdamF24RecordState, "lion-f32-records": LionF32RecordState}
+                "fp8-f24-records": AdamF24RecordState, "lion-f32-records": LionF32RecordState,
+                "lion-fp8-records": LionFP8RecordState}
 ARENA_ALIGN = 2 << 20
 SMALL_ALIGN = 256
 

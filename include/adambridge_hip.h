@@ -40,7 +40,8 @@ extern "C" {
 enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, ADAMBRIDGE_DT_FP8 = 3,
        ADAMBRIDGE_DT_F24 = 4, ADAMBRIDGE_DT_PACKED = 5, ADAMBRIDGE_DT_PACKED_FP8 = 6,
        ADAMBRIDGE_DT_PACKED_LION = 7, ADAMBRIDGE_DT_PACKED_F32 = 8, ADAMBRIDGE_DT_PACKED_F24 = 9,
-       ADAMBRIDGE_DT_PACKED_LION_F24 = 10, ADAMBRIDGE_DT_PACKED_FP8_F24 = 11, ADAMBRIDGE_DT_PACKED_LION_F32 = 12 };
+       ADAMBRIDGE_DT_PACKED_LION_F24 = 10, ADAMBRIDGE_DT_PACKED_FP8_F24 = 11, ADAMBRIDGE_DT_PACKED_LION_F32 = 12,
+       ADAMBRIDGE_DT_PACKED_LION_FP8 = 13 };
 
 /* ADAMBRIDGE_DT_PACKED (p_dtype; no counterpart in the reference): an HBM layout for
  * AdamW with an FP32 master and BF16 moments (mv_dtype DT_BF16).  p points at 16-byte
@@ -104,6 +105,14 @@ enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, AD
  * Elements past n are padding (codes written as 0, master left as it is).  m_scale and v_scale are
  * the usual block scales; m, v and p_lo are unused (p_lo must be NULL: updated in place).  Same
  * arithmetic, rounding and rounding streams as the separate FP8 layout with an FP24 master. */
+/* ADAMBRIDGE_DT_PACKED_LION_FP8 (p_dtype; no counterpart in the reference): an HBM layout for Lion
+ * with an FP32 master and an FP8 moment (mv_dtype DT_FP8).  p points at one 640-byte record per
+ * 128-element block, ceil(n/128) records, 16-byte aligned.  The record of block b holds the masters
+ * as in DT_PACKED_FP8 (element 128b + 8l + j at byte 16l + 4j for j < 4, 256 + 16l + 4(j - 4) for
+ * j >= 4), then the block's 128 m codes (E4M3) in element order (bytes 512 .. 639).  Elements past n
+ * are padding (codes written as 0, master left as it is).  m_scale holds the usual block scales;
+ * m, v, v_scale and p_lo are unused (p_lo must be NULL: updated in place).  Same arithmetic,
+ * rounding and rounding streams as the separate FP8 layout. */
 enum { ADAMBRIDGE_ALGO_ADAMW = 0, ADAMBRIDGE_ALGO_LION = 1 };
 
 /* Error codes (kernels.c:1537-1553, 1582-1584, 1620-1621), plus the HIP-side ones. */
@@ -161,7 +170,7 @@ typedef struct adambridge_segment {
     void* p;                 /* FP32 master, the FP24 hi plane (uint16) when p_dtype is DT_F24, or the
                                 packed state when p_dtype is DT_PACKED / DT_PACKED_FP8 / DT_PACKED_LION /
                                 DT_PACKED_F32 / DT_PACKED_F24 / DT_PACKED_LION_F24 / DT_PACKED_FP8_F24 /
-                                DT_PACKED_LION_F32 */
+                                DT_PACKED_LION_F32 / DT_PACKED_LION_FP8 */
     uint8_t* p_lo;           /* FP24 lo plane (one byte per element); NULL for FP32; DT_PACKED,
                                 DT_PACKED_LION, DT_PACKED_F32, DT_PACKED_F24, DT_PACKED_LION_F24 and
                                 DT_PACKED_LION_F32: the destination state
@@ -182,7 +191,8 @@ typedef struct adambridge_segment {
     int32_t out_dtype;
     int32_t algorithm;
     int32_t p_dtype;         /* DT_F32 (or 0), DT_F24, DT_PACKED, DT_PACKED_FP8, DT_PACKED_LION, DT_PACKED_F32,
-                                DT_PACKED_F24, DT_PACKED_LION_F24, DT_PACKED_FP8_F24 or DT_PACKED_LION_F32 */
+                                DT_PACKED_F24, DT_PACKED_LION_F24, DT_PACKED_FP8_F24, DT_PACKED_LION_F32 or
+                                DT_PACKED_LION_FP8 */
     int32_t reserved;        /* 0, or ADAMBRIDGE_SEG_OUT_PREVIOUS */
 } adambridge_segment;
 
@@ -208,6 +218,8 @@ ADAMBRIDGE_API int adambridge_abi_version(void);
 #define ADAMBRIDGE_CAP_STREAM_COPY    0x20u   /* adambridge_stream_copy, adambridge_recycle_device_memory */
 #define ADAMBRIDGE_CAP_FP8_F24_RECORDS 0x40u  /* p_dtype DT_PACKED_FP8_F24 (11) */
 #define ADAMBRIDGE_CAP_LION_F32_RECORDS 0x80u /* p_dtype DT_PACKED_LION_F32 (12) */
+#define ADAMBRIDGE_CAP_LION_FP8_RECORDS 0x100u /* p_dtype DT_PACKED_LION_FP8 (13); record size in a
+                                                 DT_PACKED_FP8 plane's stride */
 ADAMBRIDGE_API uint32_t adambridge_capabilities(void);
 
 /* kernels.c:1495-1510.  The level whose results are reproduced: its vector
@@ -326,7 +338,8 @@ ADAMBRIDGE_API int adambridge_convert(const void* src, const float* src_scale, i
  * size being 4 bytes (ADAMBRIDGE_DT_F32) or 2 (ADAMBRIDGE_DT_BF16: BF16 bits; ADAMBRIDGE_DT_F24:
  * the high half, with the low byte at lo + (i >> group_log2) * stride + (i mod 2^group_log2)).
  * stride 0: contiguous (group_log2 unused).  ADAMBRIDGE_DT_PACKED_FP8: the FP32 masters of FP8
- * block records at data (the layout above; stride and group_log2 unused).  The masters of the other
+ * block records at data (the layout above), stride the record size: 768 (or 0) for DT_PACKED_FP8
+ * records, 640 for DT_PACKED_LION_FP8 (group_log2 unused).  The masters of the other
  * interleaved layouts at a state buffer s are the planes
  *     DT_PACKED           {s, NULL, 16, DT_F32, 1}       DT_PACKED_LION      {s, NULL, 1536, DT_F32, 8}
  *     DT_PACKED_F32       {s, NULL, 3072, DT_F32, 8}     DT_PACKED_F24       {s, s + 512, 1792, DT_F24, 8}

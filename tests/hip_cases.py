@@ -284,28 +284,60 @@ def unpack_f8f24_records(case: O.Case, rec: np.ndarray) -> tuple[np.ndarray, np.
     return hi[n:].copy(), lo[n:].copy()
 
 
+def pack_lion8_records(case: O.Case) -> np.ndarray:
+    """Separate FP32 master + FP8 m codes -> ADAMBRIDGE_DT_PACKED_LION_FP8 records (blocks x 640
+    bytes): per block the masters as in pack_records (bytes 0 .. 511), then the 128 m codes in
+    element order.  Padding masters are set to a fixed pattern so that a test can see the kernel
+    leave them unchanged."""
+    n = case.n
+    nb = max(1, -(-n // 128))
+    p = np.full(nb * 128, 0x7F8A5A5A, np.uint32)   # a NaN pattern: any arithmetic on it would show
+    p[:n] = case.arrays["p"].view(np.uint32)
+    rec = np.zeros((nb, 640), np.uint8)
+    rec[:, :512] = p.reshape(nb, 16, 2, 4).transpose(0, 2, 1, 3).reshape(nb, 128).view(np.uint8)
+    c = np.zeros(nb * 128, np.uint8)
+    src = case.arrays["m"]
+    c[:min(src.size, nb * 128)] = src[:nb * 128]
+    rec[:, 512:] = c.reshape(nb, 128)
+    return rec
+
+
+def unpack_lion8_records(case: O.Case, rec: np.ndarray) -> np.ndarray:
+    """ADAMBRIDGE_DT_PACKED_LION_FP8 records -> the case's separate master and m codes (in place);
+    returns the padding masters' bits past n."""
+    n, nb = case.n, rec.shape[0]
+    p = np.ascontiguousarray(rec[:, :512]).view(np.uint32).reshape(nb, 2, 16, 4).transpose(0, 2, 1, 3).reshape(-1)
+    case.arrays["p"] = p[:n].view(np.float32).copy()
+    size = case.arrays["m"].size
+    case.arrays["m"] = np.ascontiguousarray(rec[:, 512:]).reshape(-1)[:size].copy()
+    return p[n:].copy()
+
+
 def run_hip_records(cases: list[O.Case], width: int = 16, misalign_g: bool = False,
                     seg_flags: int = 0, padding: list | None = None) -> list[O.Case]:
-    """Like run_hip for AdamW / FP8 moment cases, through the block-record layouts: FP32 master
-    (ADAMBRIDGE_DT_PACKED_FP8) or FP24 master (ADAMBRIDGE_DT_PACKED_FP8_F24), by the case's p_dtype.
-    Pack on the host, one call, unpack the result; ``padding`` receives each FP24 case's padding
-    masters after the call."""
+    """Like run_hip for FP8 moment cases, through the block-record layouts: AdamW with an FP32 master
+    (ADAMBRIDGE_DT_PACKED_FP8) or an FP24 master (ADAMBRIDGE_DT_PACKED_FP8_F24), by the case's
+    p_dtype, and Lion with an FP32 master (ADAMBRIDGE_DT_PACKED_LION_FP8).  Pack on the host, one
+    call, unpack the result; ``padding`` receives each FP24 or Lion case's padding masters after the
+    call."""
     kernels = _hip.load()
     work = [c.copy() for c in cases]
     keep, segs = [], []
     by_group = all(c.group is not None for c in work)
     for c in work:
-        assert c.algorithm == O.ADAMW and c.mv_dtype == O.DT_FP8 and c.p_dtype in (O.DT_F32, O.DT_F24)
+        lion = c.algorithm == O.LION
+        assert c.mv_dtype == O.DT_FP8 and c.p_dtype in ((O.DT_F32,) if lion else (O.DT_F32, O.DT_F24))
         O.check_sizes(c)
         f24 = c.p_dtype == O.DT_F24
-        rec = torch.from_numpy(pack_f8f24_records(c) if f24 else pack_records(c)).cuda()
+        rec = torch.from_numpy(pack_lion8_records(c) if lion else pack_f8f24_records(c) if f24 else pack_records(c)).cuda()
         g = to_device(c.arrays["g"])
         if misalign_g:
             buf = torch.empty(g.numel() + 1, dtype=g.dtype, device=g.device)
             buf[1:].copy_(g)
             keep.append(buf)
             g = buf[1:]
-        ms, vs = to_device(c.arrays["m_scale"]), to_device(c.arrays["v_scale"])
+        ms = to_device(c.arrays["m_scale"])
+        vs = None if lion else to_device(c.arrays["v_scale"])
         out = to_device(c.arrays["out"]) if "out" in c.arrays else None
         grp = None
         if by_group:
@@ -313,12 +345,13 @@ def run_hip_records(cases: list[O.Case], width: int = 16, misalign_g: bool = Fal
                              seed=c.group["seed"] & (2**64 - 1), stochastic=int(c.group["stochastic"]))
         keep += [rec, g, ms, vs, out, grp]
         segs.append(_hip.Segment(p=rec.data_ptr(), p_lo=None, g=g.data_ptr(), m=None, v=None,
-                                 m_scale=ms.data_ptr(), v_scale=vs.data_ptr(),
+                                 m_scale=ms.data_ptr(), v_scale=vs.data_ptr() if vs is not None else None,
                                  out=out.data_ptr() if out is not None else None,
                                  group=ctypes.pointer(grp) if grp is not None else None, n=c.n, step=c.step,
                                  index=c.index, offset=c.offset, g_dtype=c.g_dtype, mv_dtype=O.DT_FP8,
-                                 out_dtype=c.out_dtype, algorithm=0,
-                                 p_dtype=_hip.DT_PACKED8_F24 if f24 else _hip.DT_PACKED8, reserved=seg_flags))
+                                 out_dtype=c.out_dtype, algorithm=c.algorithm,
+                                 p_dtype=_hip.DT_PACKED8_LION if lion else _hip.DT_PACKED8_F24 if f24 else _hip.DT_PACKED8,
+                                 reserved=seg_flags))
     arr = kernels.segment_array([ctypes.pointer(s) for s in segs])
     kernels.set_simd_level(WIDTH_LEVEL[width])
     try:
@@ -336,14 +369,19 @@ def run_hip_records(cases: list[O.Case], width: int = 16, misalign_g: bool = Fal
         if misalign_g:
             next(it)
         rec, g, ms, vs, out, grp = (next(it) for _ in range(6))
-        if c.p_dtype == O.DT_F24:
+        if c.algorithm == O.LION:
+            pad = unpack_lion8_records(c, rec.cpu().numpy())
+            if padding is not None:
+                padding.append(pad)
+        elif c.p_dtype == O.DT_F24:
             pad = unpack_f8f24_records(c, rec.cpu().numpy())
             if padding is not None:
                 padding.append(pad)
         else:
             unpack_records(c, rec.cpu().numpy())
         c.arrays["m_scale"] = from_device(ms, c.arrays["m_scale"])
-        c.arrays["v_scale"] = from_device(vs, c.arrays["v_scale"])
+        if vs is not None:
+            c.arrays["v_scale"] = from_device(vs, c.arrays["v_scale"])
         if out is not None:
             c.arrays["out"] = from_device(out, c.arrays["out"])
     return work

@@ -54,7 +54,8 @@ def test_header_codes_match_the_python_mirror():
               "DT_F24": _hip.DT_F24, "DT_PACKED": _hip.DT_PACKED, "DT_PACKED_FP8": _hip.DT_PACKED8,
               "DT_PACKED_LION": _hip.DT_PACKED_LION, "DT_PACKED_F32": _hip.DT_PACKED_F32,
               "DT_PACKED_F24": _hip.DT_PACKED_F24, "DT_PACKED_LION_F24": _hip.DT_PACKED_LION_F24,
-              "DT_PACKED_FP8_F24": _hip.DT_PACKED8_F24, "DT_PACKED_LION_F32": _hip.DT_PACKED_LION_F32}
+              "DT_PACKED_FP8_F24": _hip.DT_PACKED8_F24, "DT_PACKED_LION_F32": _hip.DT_PACKED_LION_F32,
+              "DT_PACKED_LION_FP8": _hip.DT_PACKED8_LION}
     assert codes == mirror
     flag = re.search(r"#define ADAMBRIDGE_SEG_OUT_PREVIOUS (\d+)", text)
     assert flag and int(flag.group(1)) == _hip.SEG_OUT_PREVIOUS
@@ -98,7 +99,7 @@ def _segment_variants():
     return [
         ("negative n", m(n=-1), -1),
         ("unknown algorithm", m(algorithm=5), -12),
-        ("unknown master format", m(p_dtype=13), -13),
+        ("unknown master format", m(p_dtype=14), -13),
         ("no master", m(p=None), -2),
         ("no gradient", m(g=None), -2),
         ("no first moment", m(m=None), -2),
@@ -214,6 +215,10 @@ def test_convert_plane_argument_codes_and_capabilities():
     assert rc(P(base + 2, None, 0, F32, 0), ok) == -14
     assert rc(P(base + 1, None, 0, BF16, 0), ok) == -14
     assert rc(P(base + 8, None, 0, P8, 0), ok) == -14               # FP8 records are 16-byte aligned
+    assert rc(P(base, None, 640, P8, 0), ok) == 0                    # Lion FP8 records: 640-byte stride
+    assert rc(P(base, None, 640, P8, 31), ok) == 0                   # group_log2 unused there
+    assert rc(P(base, None, 496, P8, 0), ok) == -1                   # shorter than a record's masters
+    assert rc(P(base, None, 648, P8, 0), ok) == -14                  # records stay 16-byte aligned
     assert rc(P(base, None, 1536, F32, 31), ok) == -1
     assert rc(P(base, None, -16, F32, 1), ok) == -1
     assert rc(P(base, None, 18, F32, 1), ok) == -14

@@ -112,6 +112,7 @@ LAYOUTS = [("pairs", "adamw", "bf16", "fp32"), ("lion-records", "lion", "bf16", 
            ("f32-records", "adamw", "fp32", "fp32"), ("f24-records", "adamw", "bf16", "fp24"),
            ("lion-f24-records", "lion", "bf16", "fp24"), ("fp8-records", "adamw", "fp8", "fp32"),
            ("fp8-f24-records", "adamw", "fp8", "fp24"), ("lion-f32-records", "lion", "fp32", "fp32"),
+           ("lion-fp8-records", "lion", "fp8", "fp32"),
            ("separate", "adamw", "bf16", "fp24"), ("separate", "adamw", "fp8", "fp32")]
 
 
@@ -148,8 +149,10 @@ def test_master_planes_of_every_layout(layout, algorithm, precision, master, n):
         written = np.zeros(st.current.nbytes, bool)
         plane = st.master_plane()
         i = np.arange(n, dtype=np.int64)
-        if layout == "fp8-records":
-            offs = [(i >> 7) * 768 + np.where(i & 4, 256, 0) + ((i >> 3) & 15) * 16 + (i & 3) * 4 + k for k in range(4)]
+        if layout in ("fp8-records", "lion-fp8-records"):   # the plane's stride is the record size
+            rec = 768 if layout == "fp8-records" else 640
+            assert plane.stride in (0, rec) and (plane.stride == rec or layout == "fp8-records")
+            offs = [(i >> 7) * rec + np.where(i & 4, 256, 0) + ((i >> 3) & 15) * 16 + (i & 3) * 4 + k for k in range(4)]
         elif master == "fp24":   # hi plane at the record's start, lo plane right after it
             g = plane.group_log2
             at = (i >> g) * plane.stride + (i & ((1 << g) - 1)) * 2

@@ -268,20 +268,24 @@ def run_hip_packed_unchecked(case):
 from hip_cases import run_hip_records  # noqa: E402
 
 
-RECORD_MASTERS = [O.DT_F32, O.DT_F24]   # ADAMBRIDGE_DT_PACKED_FP8, ADAMBRIDGE_DT_PACKED_FP8_F24
+# (algorithm, master): ADAMBRIDGE_DT_PACKED_FP8, ADAMBRIDGE_DT_PACKED_FP8_F24, ADAMBRIDGE_DT_PACKED_LION_FP8
+RECORD_KINDS = [(O.ADAMW, O.DT_F32), (O.ADAMW, O.DT_F24), (O.LION, O.DT_F32)]
+RECORD_IDS = ["adamw-f32", "adamw-f24", "lion-f32"]
 
 
-@pytest.mark.parametrize("pt", RECORD_MASTERS)
-def test_fp8_records_match_oracle(pt):
-    """ADAMBRIDGE_DT_PACKED_FP8 (FP32 master and both FP8 moments in 768-byte block records) and
-    ADAMBRIDGE_DT_PACKED_FP8_F24 (FP24 master planes and codes in 640-byte records) give the separate
-    layout's bytes: ragged and block-aligned sizes, tails of every reproduced ISA, 128-aligned
-    offsets, SR on/off, every grad/out dtype; an FP24 record's padding masters stay as they were."""
-    rng = np.random.default_rng(31 + pt)
+@pytest.mark.parametrize("algo,pt", RECORD_KINDS, ids=RECORD_IDS)
+def test_fp8_records_match_oracle(algo, pt):
+    """ADAMBRIDGE_DT_PACKED_FP8 (FP32 master and both FP8 moments in 768-byte block records),
+    ADAMBRIDGE_DT_PACKED_FP8_F24 (FP24 master planes and codes in 640-byte records) and
+    ADAMBRIDGE_DT_PACKED_LION_FP8 (Lion: FP32 master and m codes in 640-byte records) give the
+    separate layout's bytes: ragged and block-aligned sizes, tails of every reproduced ISA,
+    128-aligned offsets, SR on/off, every grad/out dtype; an FP24 or Lion record's padding masters
+    stay as they were."""
+    rng = np.random.default_rng(31 + pt + 7 * algo)
     cases = []
     for gt, ot, sr, n in itertools.product([O.DT_BF16, O.DT_F32], [O.DT_NONE, O.DT_F32, O.DT_BF16], [True, False],
                                            [1, 15, 127, 128, 129, 1000, 2048 + 77, 16384 + 300]):
-        cases.append(O.make_case(rng, n, mv_dtype=O.DT_FP8, p_dtype=pt, g_dtype=gt, out_dtype=ot,
+        cases.append(O.make_case(rng, n, algorithm=algo, mv_dtype=O.DT_FP8, p_dtype=pt, g_dtype=gt, out_dtype=ot,
                                  stochastic=sr, offset=128 * int(rng.integers(0, 2**24)),
                                  index=int(rng.integers(0, 999)), step=int(rng.integers(1, 30))))
     for width in (16, 8, 0):
@@ -290,14 +294,19 @@ def test_fp8_records_match_oracle(pt):
         got = run_hip_records(cases, width, padding=padding)
         for w, g in zip(want, got):
             check(w, g)
-        for hi, lo in padding:
-            assert np.all(hi == 0xA5A5) and np.all(lo == 0x5A), "an FP24 record's padding master was written"
+        for pad in padding:
+            if algo == O.LION:
+                assert np.all(pad == 0x7F8A5A5A), "a Lion record's padding master was written"
+            else:
+                hi, lo = pad
+                assert np.all(hi == 0xA5A5) and np.all(lo == 0x5A), "an FP24 record's padding master was written"
 
 
-@pytest.mark.parametrize("pt", RECORD_MASTERS)
-def test_fp8_records_misaligned_gradient_and_specials(pt):
-    rng = np.random.default_rng(32 + pt)
-    cases = [O.make_case(rng, n, mv_dtype=O.DT_FP8, p_dtype=pt, special=sp) for n in (999, 4096) for sp in (False, True)]
+@pytest.mark.parametrize("algo,pt", RECORD_KINDS, ids=RECORD_IDS)
+def test_fp8_records_misaligned_gradient_and_specials(algo, pt):
+    rng = np.random.default_rng(32 + pt + 7 * algo)
+    cases = [O.make_case(rng, n, algorithm=algo, mv_dtype=O.DT_FP8, p_dtype=pt, special=sp)
+             for n in (999, 4096) for sp in (False, True)]
     want = O.run_many(cases, "oracle", 16)
     got = run_hip_records(cases, 16, misalign_g=True)
     for w, g in zip(want, got):
@@ -305,24 +314,25 @@ def test_fp8_records_misaligned_gradient_and_specials(pt):
         assert not bad, bad
 
 
-@pytest.mark.parametrize("pt", RECORD_MASTERS)
-def test_fp8_records_multi_step_groups_and_steps(pt):
+@pytest.mark.parametrize("algo,pt", RECORD_KINDS, ids=RECORD_IDS)
+def test_fp8_records_multi_step_groups_and_steps(algo, pt):
     """Several segments per call through the group path, then three consecutive steps of one."""
-    rng = np.random.default_rng(33 + pt)
-    cases = [O.make_case(rng, 3000 + 128 * k + 7, mv_dtype=O.DT_FP8, p_dtype=pt, explicit=False, index=k, step=k + 2,
-                         seed=3) for k in range(12)]
+    rng = np.random.default_rng(33 + pt + 7 * algo)
+    cases = [O.make_case(rng, 3000 + 128 * k + 7, algorithm=algo, mv_dtype=O.DT_FP8, p_dtype=pt, explicit=False,
+                         index=k, step=k + 2, seed=3) for k in range(12)]
     want = O.run_many(cases, "oracle", 16)
     got = run_hip_records(cases, 16)
     for w, g in zip(want, got):
         check(w, g)
-    case = O.make_case(rng, 5000, mv_dtype=O.DT_FP8, p_dtype=pt)
+    case = O.make_case(rng, 5000, algorithm=algo, mv_dtype=O.DT_FP8, p_dtype=pt)
     grads = [O.make_case(rng, 5000, mv_dtype=O.DT_FP8).arrays["g"] for _ in range(3)]
     check(run_steps(case, grads, oracle_runner, 16), run_steps(case, grads, run_hip_records, 16))
 
 
-@pytest.mark.parametrize("layout", ["fp8-records", "fp8-f24-records"])
+@pytest.mark.parametrize("layout", ["fp8-records", "fp8-f24-records", "lion-fp8-records"])
 def test_fp8_records_reject_bad_segments(layout):
-    """Lion (-12), a second state buffer (-13), BF16 moments (-4) and a misaligned record (-14)."""
+    """The other algorithm (-12), a second state buffer (-13), BF16 moments (-4) and a misaligned
+    record (-14)."""
     import ctypes
     from adambridge_amd import _hip
     rng = np.random.default_rng(34)
@@ -332,10 +342,12 @@ def test_fp8_records_reject_bad_segments(layout):
     g = torch.zeros(300, dtype=torch.bfloat16, device="cuda")
     sc = torch.ones(3, dtype=torch.float32, device="cuda")
     hp = _hip.HParams(**{kk: case.hparams[kk] for kk, _ in _hip.HParams._fields_})
-    pt = _hip.DT_PACKED8 if layout == "fp8-records" else _hip.DT_PACKED8_F24
+    pt = {"fp8-records": _hip.DT_PACKED8, "fp8-f24-records": _hip.DT_PACKED8_F24,
+          "lion-fp8-records": _hip.DT_PACKED8_LION}[layout]
+    algo = 1 if layout == "lion-fp8-records" else 0
     base = dict(p=rec.data_ptr(), g=g.data_ptr(), m_scale=sc.data_ptr(), v_scale=sc.data_ptr(), n=300, step=1,
-                mv_dtype=O.DT_FP8, g_dtype=O.DT_BF16, out_dtype=0, algorithm=0, p_dtype=pt)
-    for change, code in ((dict(algorithm=1), -12), (dict(p_lo=rec.data_ptr()), -13),
+                mv_dtype=O.DT_FP8, g_dtype=O.DT_BF16, out_dtype=0, algorithm=algo, p_dtype=pt)
+    for change, code in ((dict(algorithm=1 - algo), -12), (dict(p_lo=rec.data_ptr()), -13),
                          (dict(mv_dtype=O.DT_BF16), -4), (dict(p=rec.data_ptr() + 8), -14)):
         seg = _hip.Segment(**{**base, **change})
         with pytest.raises(RuntimeError, match=rf"code {code}"):
@@ -742,7 +754,7 @@ cases = [O.make_case(rng, n, algorithm=algo, mv_dtype=O.DT_FP8, p_dtype=pt, stoc
                      offset=128 * int(rng.integers(0, 2**20)), index=int(rng.integers(0, 999)), step=3)
          for algo, pt, sr, n in itertools.product([O.ADAMW, O.LION], [O.DT_F32, O.DT_F24], [True, False],
                                                   [129, 4096 + 77, 3 * 4096, 20000 + 5])]
-records = [c for c in cases if c.algorithm == O.ADAMW]   # FP32- and FP24-master block records
+records = [c for c in cases if c.algorithm == O.ADAMW or c.p_dtype == O.DT_F32]   # the block-record layouts
 bad = 0
 for runner, subset in ((run_hip, cases), (run_hip_records, records)):
     for w, g in zip(O.run_many(subset, "oracle", 16), runner(subset, 16)):
@@ -784,7 +796,7 @@ def _previous_weight(case):
 
 
 @pytest.mark.parametrize("layout", ["separate", "pairs", "fp8-records", "lion-records", "f32-records", "f24-records",
-                                    "lion-f24-records", "fp8-f24-records", "lion-f32-records"])
+                                    "lion-f24-records", "fp8-f24-records", "lion-f32-records", "lion-fp8-records"])
 def test_out_previous_writes_the_weight_from_before_the_update(layout):
     """ADAMBRIDGE_SEG_OUT_PREVIOUS (delayed updates): out receives the weight of the master as stored
     before the update -- FP32, or bf16 by the kernels' rounding of FP32 and decoded FP24 masters,
@@ -799,11 +811,12 @@ def test_out_previous_writes_the_weight_from_before_the_update(layout):
               "lion-records": [(O.LION, O.DT_BF16, O.DT_F32)], "f32-records": [(O.ADAMW, O.DT_F32, O.DT_F32)],
               "f24-records": [(O.ADAMW, O.DT_BF16, O.DT_F24)], "lion-f24-records": [(O.LION, O.DT_BF16, O.DT_F24)],
               "fp8-f24-records": [(O.ADAMW, O.DT_FP8, O.DT_F24)],
-              "lion-f32-records": [(O.LION, O.DT_F32, O.DT_F32)]}[layout]
+              "lion-f32-records": [(O.LION, O.DT_F32, O.DT_F32)], "lion-fp8-records": [(O.LION, O.DT_FP8, O.DT_F32)]}[layout]
     runner = {"separate": run_hip, "pairs": run_hip_packed, "fp8-records": run_hip_records,
               "lion-records": run_hip_lion_records, "f32-records": run_hip_f32_records,
               "f24-records": run_hip_f24_records, "lion-f24-records": run_hip_f24_records,
-              "fp8-f24-records": run_hip_records, "lion-f32-records": run_hip_lion_f32_records}[layout]
+              "fp8-f24-records": run_hip_records, "lion-f32-records": run_hip_lion_f32_records,
+              "lion-fp8-records": run_hip_records}[layout]
     cases = []
     for (algo, mv, pt), gt, ot, sr, n in itertools.product(combos, [O.DT_BF16, O.DT_F32], [O.DT_F32, O.DT_BF16],
                                                              [True, False], [1, 15, 17, 129, 1000, 8192 + 77]):

@@ -398,17 +398,19 @@ def test_lion_no_eps():
         ab.LionBridge(tiny_mlp(device=DEV).parameters(), eps=1e-8)
 
 
-@pytest.mark.parametrize("layout,precision", [("auto", "bf16"), ("auto", "fp32"), ("separate", "bf16"),
+@pytest.mark.parametrize("layout,precision", [("auto", "bf16"), ("auto", "fp32"), ("auto", "fp8"), ("separate", "bf16"),
                                               ("separate", "fp32"), ("separate", "fp8")])
 def test_lion_state_dict_resume_is_exact(layout, precision):
     """reference test_lion.py:102-124: a Lion checkpoint resumed into a fresh optimizer continues bit
-    for bit (bf16 parameters, so the master is a buffer of its own; 'auto' keeps a BF16 or FP32 moment
-    in Lion records, whose checkpoint holds the reference's separate arrays); AdamBridge refuses it."""
+    for bit (bf16 parameters, so the master is a buffer of its own; 'auto' keeps a BF16, FP32 or FP8
+    moment in Lion records, whose checkpoint holds the reference's separate arrays); AdamBridge
+    refuses it."""
     kw = dict(lr=1e-3, precision=precision, state_layout=layout, seed=3)
     model = tiny_mlp(device=DEV, dtype=torch.bfloat16)
     opt = ab.LionBridge(model.parameters(), **kw)
     train(model, opt, 3)
-    want = {"bf16": "lion-records", "fp32": "lion-f32-records"}[precision] if layout == "auto" else "separate"
+    want = {"bf16": "lion-records", "fp32": "lion-f32-records", "fp8": "lion-fp8-records"}[precision] \
+        if layout == "auto" else "separate"
     assert {s.state.layout for s in opt._ordered} == {want}
     buf = io.BytesIO()
     torch.save({"model": model.state_dict(), "opt": opt.state_dict()}, buf)
