@@ -1270,13 +1270,21 @@ __global__ __launch_bounds__(kThreads) void k_update_f32rec(Launch L)
 // place of the separate layout's six arrays (two of them read 2 bytes a lane).
 // Arithmetic as the FP32-moment records; the master is rounded to FP24 and the
 // moments to BF16 with the separate layout's roundings and rounding streams.
+//
+// With FP32 moments (MV = DT_F32, ADAMBRIDGE_DT_PACKED_F24_F32): 2816-byte records, the same high
+// halves and low bytes, then the 256 m and the 256 v as FP32 (16-byte accesses a lane), stored
+// exactly.
 
 constexpr int64_t kF24RecordElems = 256;
 constexpr int64_t kF24RecordBytes = 1792;
+constexpr int64_t kF24F32RecordBytes = 2816;
 
-template <int GT, int OT, bool SR>
+template <int GT, int OT, bool SR, int MV = DT_BF16>
 __device__ __forceinline__ void update_tile_f24rec(const DevSeg& s, int64_t tile, int64_t T)
 {
+    constexpr bool kF32 = MV == DT_F32;
+    constexpr int64_t kRecB = kF32 ? kF24F32RecordBytes : kF24RecordBytes;
+    constexpr int64_t kMB = kF32 ? 4 : 2;   // bytes per moment value
     const int64_t n = s.n, n_main = s.n_main;
     const Coef c = s.c;
     const uint8_t* __restrict__ src = static_cast<const uint8_t*>(s.p);
@@ -1286,16 +1294,27 @@ __device__ __forceinline__ void update_tile_f24rec(const DevSeg& s, int64_t tile
     const int64_t lo = (tile - s.tile_begin) * T;
     const int64_t hi = lo + T < n ? lo + T : n;
     for (int64_t i = lo + threadIdx.x * 4; i < hi; i += kThreads * 4) {
-        // i % 4 == 0: record i / 256; high halves at 2j, low bytes at 512 + j, m at 768 + 2j,
-        // v at 1280 + 2j, for j = i % 256
-        const int64_t rec = (i / kF24RecordElems) * kF24RecordBytes;
+        // i % 4 == 0: record i / 256; high halves at 2j, low bytes at 512 + j, m at 768 + 2j and
+        // v at 1280 + 2j (BF16), or m at 768 + 4j and v at 1792 + 4j (FP32), for j = i % 256
+        const int64_t rec = (i / kF24RecordElems) * kRecB;
         const int64_t j = i % kF24RecordElems;
-        const int64_t at_h = rec + 2 * j, at_l = rec + 512 + j, at_m = rec + 768 + 2 * j, at_v = rec + 1280 + 2 * j;
+        const int64_t at_h = rec + 2 * j, at_l = rec + 512 + j, at_m = rec + 768 + kMB * j,
+                      at_v = rec + 768 + 256 * kMB + kMB * j;
         const uint32_t idx = s.idx0 + (uint32_t)i;
         const u32x2 hw = ld(reinterpret_cast<const u32x2*>(src + at_h));
         const uint32_t lw = ld(reinterpret_cast<const uint32_t*>(src + at_l));
-        const u32x2 mw = ld(reinterpret_cast<const u32x2*>(src + at_m));
-        const u32x2 vw = ld(reinterpret_cast<const u32x2*>(src + at_v));
+        uint32_t m_in[4], v_in[4];
+        if constexpr (kF32) {
+            const u32x4 mw = ld(reinterpret_cast<const u32x4*>(src + at_m));
+            const u32x4 vw = ld(reinterpret_cast<const u32x4*>(src + at_v));
+            m_in[0] = mw.x; m_in[1] = mw.y; m_in[2] = mw.z; m_in[3] = mw.w;
+            v_in[0] = vw.x; v_in[1] = vw.y; v_in[2] = vw.z; v_in[3] = vw.w;
+        } else {
+            const u32x2 mw = ld(reinterpret_cast<const u32x2*>(src + at_m));
+            const u32x2 vw = ld(reinterpret_cast<const u32x2*>(src + at_v));
+            m_in[0] = mw.x & 0xffffu; m_in[1] = mw.x >> 16; m_in[2] = mw.y & 0xffffu; m_in[3] = mw.y >> 16;
+            v_in[0] = vw.x & 0xffffu; v_in[1] = vw.x >> 16; v_in[2] = vw.y & 0xffffu; v_in[3] = vw.y >> 16;
+        }
         const bool all = i + 4 <= n;
         float g[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (vec && all) {
@@ -1307,8 +1326,6 @@ __device__ __forceinline__ void update_tile_f24rec(const DevSeg& s, int64_t tile
                 if (i + k < n) g[k] = load1<GT>(s.g, i + k);
         }
         const uint32_t h_in[4] = {hw.x & 0xffffu, hw.x >> 16, hw.y & 0xffffu, hw.y >> 16};
-        const uint32_t m_in[4] = {mw.x & 0xffffu, mw.x >> 16, mw.y & 0xffffu, mw.y >> 16};
-        const uint32_t v_in[4] = {vw.x & 0xffffu, vw.x >> 16, vw.y & 0xffffu, vw.y >> 16};
         uint32_t p_in[4];   // the stored masters as FP32 bits: hi << 16 | lo << 8
 #pragma unroll
         for (int k = 0; k < 4; ++k) p_in[k] = (h_in[k] << 16) | (((lw >> (8 * k)) & 0xffu) << 8);
@@ -1317,8 +1334,8 @@ __device__ __forceinline__ void update_tile_f24rec(const DevSeg& s, int64_t tile
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             p[k] = bitsf(p_in[k]);
-            m[k] = bitsf(m_in[k] << 16);
-            v[k] = bitsf(v_in[k] << 16);
+            m[k] = bitsf(kF32 ? m_in[k] : m_in[k] << 16);
+            v[k] = bitsf(kF32 ? v_in[k] : v_in[k] << 16);
         }
         if (i + 4 <= n_main) {
             adamw_pair_fused(p[0], p[1], g[0], g[1], m[0], m[1], v[0], v[1], c);
@@ -1333,15 +1350,25 @@ __device__ __forceinline__ void update_tile_f24rec(const DevSeg& s, int64_t tile
         for (int k = 0; k < 4; ++k) {
             const bool in = all || i + k < n;   // padding keeps its bits
             p_out[k] = in ? f24_round<SR>(p[k], SR ? hash32((idx + k) ^ s.seed_p) : 0u) : p_in[k];
-            m_out[k] = in ? bf16_store<SR>(m[k], SR ? hash32((idx + k) ^ s.seed_m) : 0u) : m_in[k];
-            v_out[k] = in ? bf16_store<SR>(v[k], SR ? hash32((idx + k) ^ s.seed_v) : 0u) : v_in[k];
+            if constexpr (kF32) {
+                m_out[k] = in ? fbits(m[k]) : m_in[k];
+                v_out[k] = in ? fbits(v[k]) : v_in[k];
+            } else {
+                m_out[k] = in ? bf16_store<SR>(m[k], SR ? hash32((idx + k) ^ s.seed_m) : 0u) : m_in[k];
+                v_out[k] = in ? bf16_store<SR>(v[k], SR ? hash32((idx + k) ^ s.seed_v) : 0u) : v_in[k];
+            }
             l_out |= ((p_out[k] >> 8) & 0xffu) << (8 * k);
         }
         st(reinterpret_cast<u32x2*>(dst + at_h),
            u32x2{(p_out[0] >> 16) | (p_out[1] & 0xffff0000u), (p_out[2] >> 16) | (p_out[3] & 0xffff0000u)});
         st(reinterpret_cast<uint32_t*>(dst + at_l), l_out);
-        st(reinterpret_cast<u32x2*>(dst + at_m), u32x2{m_out[0] | (m_out[1] << 16), m_out[2] | (m_out[3] << 16)});
-        st(reinterpret_cast<u32x2*>(dst + at_v), u32x2{v_out[0] | (v_out[1] << 16), v_out[2] | (v_out[3] << 16)});
+        if constexpr (kF32) {
+            st(reinterpret_cast<u32x4*>(dst + at_m), u32x4{m_out[0], m_out[1], m_out[2], m_out[3]});
+            st(reinterpret_cast<u32x4*>(dst + at_v), u32x4{v_out[0], v_out[1], v_out[2], v_out[3]});
+        } else {
+            st(reinterpret_cast<u32x2*>(dst + at_m), u32x2{m_out[0] | (m_out[1] << 16), m_out[2] | (m_out[3] << 16)});
+            st(reinterpret_cast<u32x2*>(dst + at_v), u32x2{v_out[0] | (v_out[1] << 16), v_out[2] | (v_out[3] << 16)});
+        }
         if (!prev) store_quad_out<OT>(s.out, i, n, vec && all, p_out);
     }
 }
@@ -1354,6 +1381,17 @@ __global__ __launch_bounds__(kThreads) void k_update_f24rec(Launch L)
     const DevSeg s = find_segment(L, tile);
     if (s.flags & kSR) update_tile_f24rec<GT, OT, true>(s, tile, L.tile);
     else update_tile_f24rec<GT, OT, false>(s, tile, L.tile);
+}
+
+// FP32 moments: only the master rounds (stochastically under kSR).
+template <int GT, int OT>
+__global__ __launch_bounds__(kThreads) void k_update_f24f32rec(Launch L)
+{
+    const int64_t tile = block_tile(L);
+    if (tile >= L.ntiles) return;
+    const DevSeg s = find_segment(L, tile);
+    if (s.flags & kSR) update_tile_f24rec<GT, OT, true, DT_F32>(s, tile, L.tile);
+    else update_tile_f24rec<GT, OT, false, DT_F32>(s, tile, L.tile);
 }
 
 // Lion with an FP24 master and a BF16 moment in one 1280-byte record per 256 elements: the
@@ -1657,13 +1695,29 @@ constexpr auto make_packed8_lion_table(std::integer_sequence<int, I...>)
 static const auto kPacked8Lion = make_packed8_lion_table<false>(std::make_integer_sequence<int, kNumPacked>{});
 static const auto kPacked8LionWide = make_packed8_lion_table<true>(std::make_integer_sequence<int, kNumPacked>{});
 
+// FP24-master FP32-moment records (AdamW) follow: index kNumKernels + 9 * kNumPacked + gt * 3 + ot.
+template <int I>
+constexpr KernelFn f24f32rec_entry()
+{
+    constexpr int ot = I % 3, gt = I / 3;
+    return &k_update_f24f32rec<gt ? DT_BF16 : DT_F32, ot == 0 ? DT_NONE : ot == 1 ? DT_F32 : DT_BF16>;
+}
+
+template <int... I>
+constexpr auto make_f24f32rec_table(std::integer_sequence<int, I...>)
+{
+    return std::array<KernelFn, sizeof...(I)>{f24f32rec_entry<I>()...};
+}
+
+static const auto kF24F32Rec = make_f24f32rec_table(std::make_integer_sequence<int, kNumPacked>{});
+
 // Kernel family of a table index: the FP8 block kernel, or a two-element-per-lane kernel.
 inline bool kernel_is_fp8(int index)
 {
     if (index < kNumKernels) return (index / 12) % 3 == 2;
     return (index >= kNumKernels + kNumPacked && index < kNumKernels + 2 * kNumPacked) ||
            (index >= kNumKernels + 6 * kNumPacked && index < kNumKernels + 7 * kNumPacked) ||
-           index >= kNumKernels + 8 * kNumPacked;
+           (index >= kNumKernels + 8 * kNumPacked && index < kNumKernels + 9 * kNumPacked);
 }
 
 // Dynamic LDS (unused) per workgroup of a launch of kernel `index`: it caps the workgroups a CU holds
@@ -1682,7 +1736,9 @@ inline bool kernel_is_fp8(int index)
 // 5.09 at 7 and 5.15 at 8; 6.74G elements 21.02 against 21.17 and 21.38.  Lion with an FP8 moment
 // in separate arrays (1.54G elements in 8 tensors) is fastest at 5 with an FP32 master (3.68-3.71 ms;
 // 4: 3.70, 3: 3.74, 6: 3.89, 8: 3.97, 2: 4.58) and at 6 with an FP24 master (3.15 ms; 5 and 4:
-// 3.18, 8: 3.21).  The
+// 3.18, 8: 3.21).  Lion FP8 records: 5 per CU 3.51 ms, 4: 3.50, 6: 3.69, 8: 3.75.  FP24-master
+// FP32-moment records (6.74G elements in 8 tensors): 5 per CU 27.12 ms (the copy of their bytes:
+// 27.14), 6: 27.73, 8: 27.93.  The
 // BF16 pairs lose with fewer workgroups (the 0.5B list: 1.76 against 1.67 ms with 6), and the
 // FP24-master FP8 kernels keep 8 (records, the 7B list: 8 per CU 16.28-16.66, 7: 16.18-16.55, 6:
 // 16.44-16.65, 5: 17.56-17.91).  Those run at the speed of their accesses alone: a form that makes
@@ -1698,9 +1754,10 @@ inline size_t launch_lds(int index)
         if (algo == ALGO_ADAMW) return pt == 0 ? kCap6 : 0;
         return pt == 0 ? kCap5 : kCap6;   // Lion: FP32 / FP24 master
     }
-    // 1: FP8 records, 3: FP32 records, 7: Lion records with an FP32 moment, 8: Lion FP8 records
+    // 1: FP8 records, 3: FP32 records, 7: Lion records with an FP32 moment, 8: Lion FP8 records,
+    // 9: FP24-master FP32-moment records
     const int family = (index - kNumKernels) / kNumPacked;
-    if (family == 8) return kCap5;
+    if (family == 8 || family == 9) return kCap5;
     return family == 1 || family == 3 || family == 7 ? kCap6 : 0;
 }
 
@@ -1724,7 +1781,8 @@ inline KernelFn kernel_at(int index)
     if (index < kNumKernels + 6 * kNumPacked) return kLionF24Rec[index - kNumKernels - 5 * kNumPacked];
     if (index < kNumKernels + 7 * kNumPacked) return kPacked8F24[index - kNumKernels - 6 * kNumPacked];
     if (index < kNumKernels + 8 * kNumPacked) return kLionF32Rec[index - kNumKernels - 7 * kNumPacked];
-    return kPacked8Lion[index - kNumKernels - 8 * kNumPacked];
+    if (index < kNumKernels + 9 * kNumPacked) return kPacked8Lion[index - kNumKernels - 8 * kNumPacked];
+    return kF24F32Rec[index - kNumKernels - 9 * kNumPacked];
 }
 
 inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
@@ -1747,6 +1805,8 @@ inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
         return kNumKernels + 7 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
     if (pt == DT_PACKED8_LION)
         return kNumKernels + 8 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
+    if (pt == DT_PACKED_F24_F32)
+        return kNumKernels + 9 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
     const int mvi = mv == DT_F32 ? 0 : mv == DT_BF16 ? 1 : 2;
     const int pti = pt == DT_F24 ? 1 : 0;
     const int gti = gt == DT_BF16 ? 1 : 0;

@@ -25,6 +25,7 @@ lion-f32-rec.   Lion, FP32 master, FP32 moment         2048 per 256 (x2 double-b
 lion-fp8-rec.   Lion, FP32 master, FP8 moment          640 per 128 + one FP32 scale per 128
 f32-records     AdamW, FP32 master, FP32 moments       3072 per 256 (x2 double-buffered)
 f24-records     AdamW, FP24 master, BF16 moments       1792 per 256 (x2 double-buffered)
+f24-f32-rec.    AdamW, FP24 master, FP32 moments       2816 per 256 (x2 double-buffered)
 lion-f24-rec.   Lion, FP24 master, BF16 moment         1280 per 256 (x2 double-buffered)
 ==============  =====================================  ======================================
 
@@ -45,11 +46,11 @@ from . import formats as F
 from .precision import BF16Store, FP8Store, FP24Store, FP32Store, MomentStore, load_master_, make_master, make_store
 
 __all__ = ["ParamState", "SeparateState", "PairState", "AdamRecordState", "LionRecordState", "F32RecordState",
-           "F24RecordState", "LionF24RecordState", "AdamF24RecordState", "LionF32RecordState", "LionFP8RecordState", "choose_layout", "new_state", "new_states",
+           "F24RecordState", "LionF24RecordState", "AdamF24RecordState", "LionF32RecordState", "LionFP8RecordState", "F24F32RecordState", "choose_layout", "new_state", "new_states",
            "arena_plan", "arena_memory", "LAYOUTS"]
 
 LAYOUTS = ("separate", "pairs", "fp8-records", "lion-records", "f32-records", "f24-records", "lion-f24-records",
-           "fp8-f24-records", "lion-f32-records", "lion-fp8-records")
+           "fp8-f24-records", "lion-f32-records", "lion-fp8-records", "f24-f32-records")
 IN_PLACE = ("fp8-records", "fp8-f24-records", "lion-fp8-records")   # never double-buffered
 
 # Arenas of at least this many bytes follow an allocate/free of their own size (new_states); None: never.
@@ -64,7 +65,8 @@ def choose_layout(algorithm: str, precision: str, master_precision: str, request
         return "separate"
     if master_precision == "fp24":
         return {("adamw", "bf16"): "f24-records", ("lion", "bf16"): "lion-f24-records",
-                ("adamw", "fp8"): "fp8-f24-records"}.get((algorithm, precision), "separate")
+                ("adamw", "fp8"): "fp8-f24-records", ("adamw", "fp32"): "f24-f32-records"}.get((algorithm, precision),
+                                                                                            "separate")
     return {("adamw", "bf16"): "pairs", ("adamw", "fp8"): "fp8-records", ("adamw", "fp32"): "f32-records",
             ("lion", "bf16"): "lion-records", ("lion", "fp32"): "lion-f32-records",
             ("lion", "fp8"): "lion-fp8-records"}.get((algorithm, precision),
@@ -589,6 +591,45 @@ class F24RecordState(_Interleaved):
                 "m": self._column("m").reshape(-1)[lo:hi], "v": self._column("v").reshape(-1)[lo:hi]}
 
 
+class F24F32RecordState(F24RecordState):
+    """AdamW, FP24 master, FP32 moments: 2816-byte records of 256 elements, the 256 master high halves
+    (BF16 bits), the 256 master low bytes, the 256 m and the 256 v values (FP32), each in element
+    order (ADAMBRIDGE_DT_PACKED_F24_F32)."""
+
+    layout = "f24-f32-records"
+    precision = "fp32"
+    RECORD = 2816   # master_plane's record stride too
+
+    def __init__(self, numel, device, double_buffer: bool = False, memory: list[torch.Tensor] | None = None):
+        records = max(1, -(-int(numel) // 256))
+        bufs = [m.view(records, self.RECORD) for m in memory] if memory else \
+            [torch.zeros(records, self.RECORD, dtype=torch.uint8, device=device) for _ in range(2 if double_buffer else 1)]
+        _Interleaved.__init__(self, numel, device, ("m", "v"), bufs)
+
+    @staticmethod
+    def buffer_bytes(numel: int) -> int:
+        return max(1, -(-int(numel) // 256)) * F24F32RecordState.RECORD
+
+    def bind(self, seg):
+        super().bind(seg)
+        seg.p_dtype, seg.mv_dtype = _hip.DT_PACKED_F24_F32, _hip.DT_F32
+
+    def _column(self, role):
+        """'p' the hi plane (BF16 bits), 'lo' the lo plane (uint8), 'm' / 'v' the moments (FP32)."""
+        if role in ("p", "lo"):
+            return super()._column(role)
+        k = {"m": 768, "v": 1792}[role]
+        return self.current[:, k:k + 1024].view(torch.float32)
+
+    def moment(self, role):
+        return FP32Store(self.numel, init=self._column(role).reshape(-1)[: self.numel], device=self.device)
+
+    def load(self, master=None, moments=None):
+        super().load(master)
+        for role, store in (moments or {}).items():
+            self._put(role, store.to_fp32().to(self.device))
+
+
 class LionF24RecordState(F24RecordState):
     """Lion, FP24 master, BF16 moment: 1280-byte records of 256 elements, the 256 master high halves,
     the 256 low bytes and the 256 m values, each in element order (ADAMBRIDGE_DT_PACKED_LION_F24)."""
@@ -801,7 +842,7 @@ def _bf16_bits(store: MomentStore, device) -> torch.Tensor:
 _INTERLEAVED = {"pairs": PairState, "lion-records": LionRecordState, "fp8-records": AdamRecordState,
                 "f32-records": F32RecordState, "f24-records": F24RecordState, "lion-f24-records": LionF24RecordState,
                 "fp8-f24-records": AdamF24RecordState, "lion-f32-records": LionF32RecordState,
-                "lion-fp8-records": LionFP8RecordState}
+                "lion-fp8-records": LionFP8RecordState, "f24-f32-records": F24F32RecordState}
 ARENA_ALIGN = 2 << 20
 SMALL_ALIGN = 256
 

@@ -507,18 +507,31 @@ def unpack_f32_records(case: O.Case, rec: np.ndarray) -> list[np.ndarray]:
 # FP24-master record columns: key, byte range, element type, padding fill
 F24_COLUMNS = (("p", (0, 512), np.uint16, 0x7FA5), ("p_lo", (512, 768), np.uint8, 0xA5),
                ("m", (768, 1280), np.uint16, 0x7FA6), ("v", (1280, 1792), np.uint16, 0x7FA7))
+# with FP32 moments (ADAMBRIDGE_DT_PACKED_F24_F32, 2816-byte records)
+F24_F32_COLUMNS = F24_COLUMNS[:2] + (("m", (768, 1792), np.uint32, 0x7FA6A6A6),
+                                     ("v", (1792, 2816), np.uint32, 0x7FA7A7A7))
+
+
+def _f24_columns(case: O.Case):
+    """The case's FP24-master record columns and record size."""
+    if case.mv_dtype == O.DT_F32:
+        return F24_F32_COLUMNS, 2816
+    if case.algorithm == O.LION:   # ADAMBRIDGE_DT_PACKED_LION_F24: no v
+        return F24_COLUMNS[:3], 1280
+    return F24_COLUMNS, 1792
 
 
 def pack_f24_records(case: O.Case) -> np.ndarray:
     """Separate FP24 master planes, BF16 m and v -> ADAMBRIDGE_DT_PACKED_F24 records (records x 1792
     bytes): per 256 elements, the 256 hi halves, the 256 lo bytes, the 256 m, the 256 v, each in
-    element order.  Padding slots hold fixed patterns so that a test can see the kernel leave them
-    unchanged."""
+    element order (FP32 moments: ADAMBRIDGE_DT_PACKED_F24_F32, 2816 bytes; Lion:
+    ADAMBRIDGE_DT_PACKED_LION_F24, 1280 bytes, no v).  Padding slots hold fixed patterns so that a
+    test can see the kernel leave them unchanged."""
     n = case.n
     nr = max(1, -(-n // 256))
-    size = 1280 if case.algorithm == O.LION else 1792   # Lion (ADAMBRIDGE_DT_PACKED_LION_F24): no v
+    columns, size = _f24_columns(case)
     rec = np.zeros((nr, size), np.uint8)
-    for key, (a, b), dt, fill in F24_COLUMNS[: 3 if case.algorithm == O.LION else 4]:
+    for key, (a, b), dt, fill in columns:
         col = np.full(nr * 256, fill, dt)
         col[:n] = case.arrays[key].view(dt)
         rec[:, a:b] = col.reshape(nr, 256).view(np.uint8).reshape(nr, b - a)
@@ -529,9 +542,10 @@ def unpack_f24_records(case: O.Case, rec: np.ndarray) -> list[np.ndarray]:
     """ADAMBRIDGE_DT_PACKED_F24 records -> the case's separate planes, m and v (in place); returns
     the padding slots past n of each."""
     n = case.n
-    rec = np.ascontiguousarray(rec).reshape(-1, 1280 if case.algorithm == O.LION else 1792)
+    columns, size = _f24_columns(case)
+    rec = np.ascontiguousarray(rec).reshape(-1, size)
     pads = []
-    for key, (a, b), dt, _ in F24_COLUMNS[: 3 if case.algorithm == O.LION else 4]:
+    for key, (a, b), dt, _ in columns:
         col = np.ascontiguousarray(rec[:, a:b]).view(dt).reshape(-1)
         case.arrays[key] = col[:n].view(case.arrays[key].dtype).copy()
         pads.append(col[n:].copy())
@@ -544,7 +558,8 @@ _RECORDS = {"f32": (_hip.DT_PACKED_F32, O.DT_F32, O.DT_F32, pack_f32_records, un
             "lion-f24": (_hip.DT_PACKED_LION_F24, O.DT_BF16, O.DT_F24, pack_f24_records, unpack_f24_records,
                          O.LION),
             "lion-f32": (_hip.DT_PACKED_LION_F32, O.DT_F32, O.DT_F32, pack_f32_records, unpack_f32_records,
-                         O.LION)}
+                         O.LION),
+            "f24-f32": (_hip.DT_PACKED_F24_F32, O.DT_F32, O.DT_F24, pack_f24_records, unpack_f24_records, O.ADAMW)}
 
 
 def run_hip_lion_f32_records(cases: list[O.Case], width: int = 16, **kw) -> list[O.Case]:
@@ -553,11 +568,12 @@ def run_hip_lion_f32_records(cases: list[O.Case], width: int = 16, **kw) -> list
 
 
 def run_hip_f24_records(cases: list[O.Case], width: int = 16, **kw) -> list[O.Case]:
-    """run_hip through FP24-master records: ADAMBRIDGE_DT_PACKED_F24 (AdamW, BF16 moments) or, for
-    Lion cases, ADAMBRIDGE_DT_PACKED_LION_F24 (BF16 moment)."""
-    lion = [c.algorithm == O.LION for c in cases]
-    assert all(lion) or not any(lion)
-    return run_hip_f32_records(cases, width, kind="lion-f24" if any(lion) else "f24", **kw)
+    """run_hip through FP24-master records: ADAMBRIDGE_DT_PACKED_F24 (AdamW, BF16 moments),
+    ADAMBRIDGE_DT_PACKED_F24_F32 (AdamW, FP32 moments) or, for Lion cases,
+    ADAMBRIDGE_DT_PACKED_LION_F24 (BF16 moment)."""
+    kinds = {"lion-f24" if c.algorithm == O.LION else "f24-f32" if c.mv_dtype == O.DT_F32 else "f24" for c in cases}
+    assert len(kinds) == 1
+    return run_hip_f32_records(cases, width, kind=kinds.pop(), **kw)
 
 
 def run_hip_f32_records(cases: list[O.Case], width: int = 16, double_buffer: bool = False,

@@ -497,21 +497,25 @@ def test_f32_records_multi_step_groups_and_steps():
     check(run_steps(case, grads, oracle_runner, 16), run_steps(case, grads, run_hip_f32_records, 16))
 
 
-F24_PADDING = (0x7FA5, 0xA5, 0x7FA6, 0x7FA7)   # hi, lo, m, v fill of pack_f24_records
+# (algorithm, moments) of the FP24-master records: ADAMBRIDGE_DT_PACKED_F24, _LION_F24, _F24_F32
+F24_KINDS = [(O.ADAMW, O.DT_BF16), (O.LION, O.DT_BF16), (O.ADAMW, O.DT_F32)]
+F24_IDS = ["adamw-bf16", "lion-bf16", "adamw-f32"]
 
 
-@pytest.mark.parametrize("algo", [O.ADAMW, O.LION])
+@pytest.mark.parametrize("algo,mv", F24_KINDS, ids=F24_IDS)
 @pytest.mark.parametrize("double_buffer", [False, True])
-def test_f24_records_match_oracle(double_buffer, algo):
-    """ADAMBRIDGE_DT_PACKED_F24 (FP24 master planes and BF16 m, v in 1792-byte records) gives the
-    separate FP24 layout's bytes: sizes around the record and the lane's 4 elements, the reproduced
-    SIMD widths' tails, offsets, stochastic and nearest rounding, every grad/out dtype, delayed
-    (previous-weight) output; in place, the padding slots of the last record keep their bits."""
-    rng = np.random.default_rng(61 + algo)
+def test_f24_records_match_oracle(double_buffer, algo, mv):
+    """ADAMBRIDGE_DT_PACKED_F24 (FP24 master planes and BF16 m, v in 1792-byte records), its Lion form
+    and ADAMBRIDGE_DT_PACKED_F24_F32 (FP32 m, v in 2816-byte records) give the separate FP24 layout's
+    bytes: sizes around the record and the lane's 4 elements, the reproduced SIMD widths' tails,
+    offsets, stochastic and nearest rounding, every grad/out dtype, delayed (previous-weight)
+    output; in place, the padding slots of the last record keep their bits."""
+    from hip_cases import _f24_columns
+    rng = np.random.default_rng(61 + algo + 5 * (mv == O.DT_F32))
     cases = []
     for gt, ot, n in itertools.product([O.DT_BF16, O.DT_F32], [O.DT_NONE, O.DT_F32, O.DT_BF16],
                                        [1, 2, 3, 4, 5, 15, 16, 17, 255, 256, 257, 1000, 2048 + 77, 5001]):
-        cases.append(O.make_case(rng, n, algorithm=algo, mv_dtype=O.DT_BF16, p_dtype=O.DT_F24, g_dtype=gt,
+        cases.append(O.make_case(rng, n, algorithm=algo, mv_dtype=mv, p_dtype=O.DT_F24, g_dtype=gt,
                                  out_dtype=ot,
                                  stochastic=bool(rng.integers(0, 2)), offset=int(rng.integers(0, 2**32)),
                                  index=int(rng.integers(0, 999)), step=int(rng.integers(1, 30))))
@@ -523,16 +527,16 @@ def test_f24_records_match_oracle(double_buffer, algo):
             check(w, g)
         if not double_buffer:
             for pad, c in zip(pads, cases):
-                for col, fill in zip(pad, F24_PADDING):
+                for col, (_, _, _, fill) in zip(pad, _f24_columns(c)[0]):
                     assert (col == fill).all(), f"padding changed at n={c.n}"
 
 
-@pytest.mark.parametrize("algo", [O.ADAMW, O.LION])
-def test_f24_records_misaligned_gradient_specials_and_steps(algo):
+@pytest.mark.parametrize("algo,mv", F24_KINDS, ids=F24_IDS)
+def test_f24_records_misaligned_gradient_specials_and_steps(algo, mv):
     """Gradients shifted by one element and by two, non-finite inputs, several segments through the
     group path, and three consecutive steps of one segment."""
-    rng = np.random.default_rng(62 + algo)
-    cases = [O.make_case(rng, n, algorithm=algo, mv_dtype=O.DT_BF16, p_dtype=O.DT_F24, special=sp, stochastic=sr)
+    rng = np.random.default_rng(62 + algo + 5 * (mv == O.DT_F32))
+    cases = [O.make_case(rng, n, algorithm=algo, mv_dtype=mv, p_dtype=O.DT_F24, special=sp, stochastic=sr)
              for n, sp, sr in ((999, False, True), (4096, False, False), (4096, True, True), (5001, True, False))]
     want = O.run_many(cases, "oracle", 16)
     for shift in (1, 2):
@@ -540,16 +544,17 @@ def test_f24_records_misaligned_gradient_specials_and_steps(algo):
         for w, g in zip(want, got):
             bad = O.outputs_equal(w, g, nan_equiv=True)
             assert not bad, (shift, bad)
-    cases = [O.make_case(rng, 3000 + 64 * k + 3, algorithm=algo, mv_dtype=O.DT_BF16, p_dtype=O.DT_F24,
+    cases = [O.make_case(rng, 3000 + 64 * k + 3, algorithm=algo, mv_dtype=mv, p_dtype=O.DT_F24,
                          explicit=False, index=k, step=k + 2, seed=5) for k in range(12)]
     for w, g in zip(O.run_many(cases, "oracle", 16), run_hip_f24_records(cases, 16)):
         check(w, g)
-    case = O.make_case(rng, 5000, algorithm=algo, mv_dtype=O.DT_BF16, p_dtype=O.DT_F24)
-    grads = [O.make_case(rng, 5000, mv_dtype=O.DT_BF16).arrays["g"] for _ in range(3)]
+    case = O.make_case(rng, 5000, algorithm=algo, mv_dtype=mv, p_dtype=O.DT_F24)
+    grads = [O.make_case(rng, 5000, mv_dtype=mv).arrays["g"] for _ in range(3)]
     check(run_steps(case, grads, oracle_runner, 16), run_steps(case, grads, run_hip_f24_records, 16))
 
 
-def test_f32_records_reject_bad_segments():
+@pytest.mark.parametrize("layout", ["f32-records", "f24-f32-records"])
+def test_f32_records_reject_bad_segments(layout):
     """Lion (-12), BF16 moments (-4), a missing gradient (-2) and misaligned records (-14), before
     anything runs."""
     import ctypes
@@ -560,8 +565,9 @@ def test_f32_records_reject_bad_segments():
     rec = torch.zeros(2 * 3072 + 16, dtype=torch.uint8, device="cuda")
     g = torch.zeros(300, dtype=torch.bfloat16, device="cuda")
     hp = _hip.HParams(**{kk: case.hparams[kk] for kk, _ in _hip.HParams._fields_})
+    pt = _hip.DT_PACKED_F32 if layout == "f32-records" else _hip.DT_PACKED_F24_F32
     base = dict(p=rec.data_ptr(), g=g.data_ptr(), n=300, step=1, mv_dtype=O.DT_F32, g_dtype=O.DT_BF16,
-                out_dtype=0, algorithm=0, p_dtype=_hip.DT_PACKED_F32)
+                out_dtype=0, algorithm=0, p_dtype=pt)
     for change, code in ((dict(algorithm=1), -12), (dict(mv_dtype=O.DT_BF16), -4), (dict(g=None), -2),
                          (dict(p=rec.data_ptr() + 8), -14), (dict(p_lo=rec.data_ptr() + 4), -14)):
         seg = _hip.Segment(**{**base, **change})
@@ -796,7 +802,8 @@ def _previous_weight(case):
 
 
 @pytest.mark.parametrize("layout", ["separate", "pairs", "fp8-records", "lion-records", "f32-records", "f24-records",
-                                    "lion-f24-records", "fp8-f24-records", "lion-f32-records", "lion-fp8-records"])
+                                    "lion-f24-records", "fp8-f24-records", "lion-f32-records", "lion-fp8-records",
+                                    "f24-f32-records"])
 def test_out_previous_writes_the_weight_from_before_the_update(layout):
     """ADAMBRIDGE_SEG_OUT_PREVIOUS (delayed updates): out receives the weight of the master as stored
     before the update -- FP32, or bf16 by the kernels' rounding of FP32 and decoded FP24 masters,
@@ -811,12 +818,13 @@ def test_out_previous_writes_the_weight_from_before_the_update(layout):
               "lion-records": [(O.LION, O.DT_BF16, O.DT_F32)], "f32-records": [(O.ADAMW, O.DT_F32, O.DT_F32)],
               "f24-records": [(O.ADAMW, O.DT_BF16, O.DT_F24)], "lion-f24-records": [(O.LION, O.DT_BF16, O.DT_F24)],
               "fp8-f24-records": [(O.ADAMW, O.DT_FP8, O.DT_F24)],
-              "lion-f32-records": [(O.LION, O.DT_F32, O.DT_F32)], "lion-fp8-records": [(O.LION, O.DT_FP8, O.DT_F32)]}[layout]
+              "lion-f32-records": [(O.LION, O.DT_F32, O.DT_F32)], "lion-fp8-records": [(O.LION, O.DT_FP8, O.DT_F32)],
+              "f24-f32-records": [(O.ADAMW, O.DT_F32, O.DT_F24)]}[layout]
     runner = {"separate": run_hip, "pairs": run_hip_packed, "fp8-records": run_hip_records,
               "lion-records": run_hip_lion_records, "f32-records": run_hip_f32_records,
               "f24-records": run_hip_f24_records, "lion-f24-records": run_hip_f24_records,
               "fp8-f24-records": run_hip_records, "lion-f32-records": run_hip_lion_f32_records,
-              "lion-fp8-records": run_hip_records}[layout]
+              "lion-fp8-records": run_hip_records, "f24-f32-records": run_hip_f24_records}[layout]
     cases = []
     for (algo, mv, pt), gt, ot, sr, n in itertools.product(combos, [O.DT_BF16, O.DT_F32], [O.DT_F32, O.DT_BF16],
                                                              [True, False], [1, 15, 17, 129, 1000, 8192 + 77]):
