@@ -643,6 +643,8 @@ def main() -> int:
     ap.add_argument("--double-buffer", action="store_true", help="AdamBridge double_buffer=True")
     ap.add_argument("--master", default="fp32", choices=["fp32", "fp24"],
                     help="master weight precision (AdamBridge master_precision); the configurations' own is fp32")
+    ap.add_argument("--precision", default=None, choices=["fp32", "bf16", "fp8"],
+                    help="moment precision (AdamBridge / LionBridge precision); default: the configuration's own")
     ap.add_argument("--traffic", type=float, default=None,
                     help="HBM bytes per launch measured by rocprofv3 (FETCH_SIZE+WRITE_SIZE, scaled); "
                          "default: the figure measured for this configuration, when there is one")
@@ -670,6 +672,11 @@ def main() -> int:
     if args.config == "c5":
         return main_pipeline(args)
     cfg = dict(CONFIGS[args.config], master=args.master)
+    own = cfg["precision"] == (args.precision or cfg["precision"])   # the configuration's own moments
+    if not own:
+        names = {"fp32": "FP32", "bf16": "bf16", "fp8": "FP8"}
+        cfg["desc"] = cfg["desc"].replace(names[cfg["precision"]], names[args.precision], 1)
+        cfg["precision"] = args.precision
     print(f"[bench] config {args.config}: {cfg['desc']}; warmup {args.warmup}, steps {args.steps}",
           file=sys.stderr, flush=True)
     held: list = []
@@ -710,8 +717,10 @@ def main() -> int:
     # the traffic measured for each configuration and master
     measured, profiled = ((MEASURED_TRAFFIC, TRAFFIC_PROFILE) if args.master == "fp32" else
                           (MEASURED_TRAFFIC_FP24, TRAFFIC_PROFILE_FP24))
+    if not own:   # the measured traffic figures are the configurations' own moments'
+        measured, profiled = {}, {}
     line = {
-        "metric": METRIC if args.config == "c3p" and args.master == "fp32" else
+        "metric": METRIC if args.config == "c3p" and args.master == "fp32" and own else
         f"params updated/sec and achieved HBM GB/s (% roofline), {cfg['desc']} ({args.config}"
         f"{', FP24 master' if args.master == 'fp24' else ''})",
         "value": g["params"] * args.steps / g["wall"],
