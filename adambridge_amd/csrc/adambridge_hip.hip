@@ -1397,11 +1397,16 @@ __global__ __launch_bounds__(kThreads) void k_update_f24f32rec(Launch L)
 // Lion with an FP24 master and a BF16 moment in one 1280-byte record per 256 elements: the
 // record's 256 master high halves, its 256 low bytes and its 256 m values, each in element order.
 // The Lion-record kernel's lanes and arithmetic, with the FP24-master records' master access.
+// With an FP32 moment (MV = DT_F32, ADAMBRIDGE_DT_PACKED_LION_F24_F32): 1792-byte records, the m
+// values FP32 at 768 + 4j (a 16-byte access a lane), stored exactly.
 constexpr int64_t kLionF24RecordBytes = 1280;
+constexpr int64_t kLionF24F32RecordBytes = 1792;
 
-template <int GT, int OT, bool SR>
+template <int GT, int OT, bool SR, int MV = DT_BF16>
 __device__ __forceinline__ void update_tile_lion_f24rec(const DevSeg& s, int64_t tile, int64_t T)
 {
+    constexpr bool kF32 = MV == DT_F32;
+    constexpr int64_t kRecB = kF32 ? kLionF24F32RecordBytes : kLionF24RecordBytes;
     const int64_t n = s.n;
     const Coef c = s.c;
     const uint8_t* __restrict__ src = static_cast<const uint8_t*>(s.p);
@@ -1411,14 +1416,22 @@ __device__ __forceinline__ void update_tile_lion_f24rec(const DevSeg& s, int64_t
     const int64_t lo = (tile - s.tile_begin) * T;
     const int64_t hi = lo + T < n ? lo + T : n;
     for (int64_t i = lo + threadIdx.x * 4; i < hi; i += kThreads * 4) {
-        // i % 4 == 0: record i / 256; high halves at 2j, low bytes at 512 + j, m at 768 + 2j
-        const int64_t rec = (i / kF24RecordElems) * kLionF24RecordBytes;
+        // i % 4 == 0: record i / 256; high halves at 2j, low bytes at 512 + j, m at 768 + 2j (BF16)
+        // or 768 + 4j (FP32)
+        const int64_t rec = (i / kF24RecordElems) * kRecB;
         const int64_t j = i % kF24RecordElems;
-        const int64_t at_h = rec + 2 * j, at_l = rec + 512 + j, at_m = rec + 768 + 2 * j;
+        const int64_t at_h = rec + 2 * j, at_l = rec + 512 + j, at_m = rec + 768 + (kF32 ? 4 : 2) * j;
         const uint32_t idx = s.idx0 + (uint32_t)i;
         const u32x2 hw = ld(reinterpret_cast<const u32x2*>(src + at_h));
         const uint32_t lw = ld(reinterpret_cast<const uint32_t*>(src + at_l));
-        const u32x2 mw = ld(reinterpret_cast<const u32x2*>(src + at_m));
+        uint32_t m_in[4];
+        if constexpr (kF32) {
+            const u32x4 mw = ld(reinterpret_cast<const u32x4*>(src + at_m));
+            m_in[0] = mw.x; m_in[1] = mw.y; m_in[2] = mw.z; m_in[3] = mw.w;
+        } else {
+            const u32x2 mw = ld(reinterpret_cast<const u32x2*>(src + at_m));
+            m_in[0] = mw.x & 0xffffu; m_in[1] = mw.x >> 16; m_in[2] = mw.y & 0xffffu; m_in[3] = mw.y >> 16;
+        }
         const bool all = i + 4 <= n;
         float g[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (vec && all) {
@@ -1430,7 +1443,6 @@ __device__ __forceinline__ void update_tile_lion_f24rec(const DevSeg& s, int64_t
                 if (i + k < n) g[k] = load1<GT>(s.g, i + k);
         }
         const uint32_t h_in[4] = {hw.x & 0xffffu, hw.x >> 16, hw.y & 0xffffu, hw.y >> 16};
-        const uint32_t m_in[4] = {mw.x & 0xffffu, mw.x >> 16, mw.y & 0xffffu, mw.y >> 16};
         uint32_t p_in[4];   // the stored masters as FP32 bits: hi << 16 | lo << 8
 #pragma unroll
         for (int k = 0; k < 4; ++k) p_in[k] = (h_in[k] << 16) | (((lw >> (8 * k)) & 0xffu) << 8);
@@ -1438,17 +1450,19 @@ __device__ __forceinline__ void update_tile_lion_f24rec(const DevSeg& s, int64_t
         uint32_t p_out[4], m_out[4], l_out = 0u;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            float m = bitsf(m_in[k] << 16);
+            float m = bitsf(kF32 ? m_in[k] : m_in[k] << 16);
             const float p = lion(bitsf(p_in[k]), g[k], m, c);
             const bool in = all || i + k < n;   // padding keeps its bits
             p_out[k] = in ? f24_round<SR>(p, SR ? hash32((idx + k) ^ s.seed_p) : 0u) : p_in[k];
-            m_out[k] = in ? bf16_store<SR>(m, SR ? hash32((idx + k) ^ s.seed_m) : 0u) : m_in[k];
+            if constexpr (kF32) m_out[k] = in ? fbits(m) : m_in[k];
+            else m_out[k] = in ? bf16_store<SR>(m, SR ? hash32((idx + k) ^ s.seed_m) : 0u) : m_in[k];
             l_out |= ((p_out[k] >> 8) & 0xffu) << (8 * k);
         }
         st(reinterpret_cast<u32x2*>(dst + at_h),
            u32x2{(p_out[0] >> 16) | (p_out[1] & 0xffff0000u), (p_out[2] >> 16) | (p_out[3] & 0xffff0000u)});
         st(reinterpret_cast<uint32_t*>(dst + at_l), l_out);
-        st(reinterpret_cast<u32x2*>(dst + at_m), u32x2{m_out[0] | (m_out[1] << 16), m_out[2] | (m_out[3] << 16)});
+        if constexpr (kF32) st(reinterpret_cast<u32x4*>(dst + at_m), u32x4{m_out[0], m_out[1], m_out[2], m_out[3]});
+        else st(reinterpret_cast<u32x2*>(dst + at_m), u32x2{m_out[0] | (m_out[1] << 16), m_out[2] | (m_out[3] << 16)});
         if (!prev) store_quad_out<OT>(s.out, i, n, vec && all, p_out);
     }
 }
@@ -1461,6 +1475,17 @@ __global__ __launch_bounds__(kThreads) void k_update_lion_f24rec(Launch L)
     const DevSeg s = find_segment(L, tile);
     if (s.flags & kSR) update_tile_lion_f24rec<GT, OT, true>(s, tile, L.tile);
     else update_tile_lion_f24rec<GT, OT, false>(s, tile, L.tile);
+}
+
+// FP32 moment: only the master rounds (stochastically under kSR).
+template <int GT, int OT>
+__global__ __launch_bounds__(kThreads) void k_update_lion_f24f32rec(Launch L)
+{
+    const int64_t tile = block_tile(L);
+    if (tile >= L.ntiles) return;
+    const DevSeg s = find_segment(L, tile);
+    if (s.flags & kSR) update_tile_lion_f24rec<GT, OT, true, DT_F32>(s, tile, L.tile);
+    else update_tile_lion_f24rec<GT, OT, false, DT_F32>(s, tile, L.tile);
 }
 
 // ------------------------------------------------------- segment-table writer
@@ -1711,6 +1736,22 @@ constexpr auto make_f24f32rec_table(std::integer_sequence<int, I...>)
 
 static const auto kF24F32Rec = make_f24f32rec_table(std::make_integer_sequence<int, kNumPacked>{});
 
+// Lion FP24-master FP32-moment records follow: index kNumKernels + 10 * kNumPacked + gt * 3 + ot.
+template <int I>
+constexpr KernelFn lion_f24f32rec_entry()
+{
+    constexpr int ot = I % 3, gt = I / 3;
+    return &k_update_lion_f24f32rec<gt ? DT_BF16 : DT_F32, ot == 0 ? DT_NONE : ot == 1 ? DT_F32 : DT_BF16>;
+}
+
+template <int... I>
+constexpr auto make_lion_f24f32rec_table(std::integer_sequence<int, I...>)
+{
+    return std::array<KernelFn, sizeof...(I)>{lion_f24f32rec_entry<I>()...};
+}
+
+static const auto kLionF24F32Rec = make_lion_f24f32rec_table(std::make_integer_sequence<int, kNumPacked>{});
+
 // Kernel family of a table index: the FP8 block kernel, or a two-element-per-lane kernel.
 inline bool kernel_is_fp8(int index)
 {
@@ -1755,9 +1796,10 @@ inline size_t launch_lds(int index)
         return pt == 0 ? kCap5 : kCap6;   // Lion: FP32 / FP24 master
     }
     // 1: FP8 records, 3: FP32 records, 7: Lion records with an FP32 moment, 8: Lion FP8 records,
-    // 9: FP24-master FP32-moment records
+    // 9: FP24-master FP32-moment records, 10: their Lion form
     const int family = (index - kNumKernels) / kNumPacked;
     if (family == 8 || family == 9) return kCap5;
+    if (family == 10) return kCap6;
     return family == 1 || family == 3 || family == 7 ? kCap6 : 0;
 }
 
@@ -1782,7 +1824,8 @@ inline KernelFn kernel_at(int index)
     if (index < kNumKernels + 7 * kNumPacked) return kPacked8F24[index - kNumKernels - 6 * kNumPacked];
     if (index < kNumKernels + 8 * kNumPacked) return kLionF32Rec[index - kNumKernels - 7 * kNumPacked];
     if (index < kNumKernels + 9 * kNumPacked) return kPacked8Lion[index - kNumKernels - 8 * kNumPacked];
-    return kF24F32Rec[index - kNumKernels - 9 * kNumPacked];
+    if (index < kNumKernels + 10 * kNumPacked) return kF24F32Rec[index - kNumKernels - 9 * kNumPacked];
+    return kLionF24F32Rec[index - kNumKernels - 10 * kNumPacked];
 }
 
 inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
@@ -1807,6 +1850,8 @@ inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
         return kNumKernels + 8 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
     if (pt == DT_PACKED_F24_F32)
         return kNumKernels + 9 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
+    if (pt == DT_PACKED_LION_F24_F32)
+        return kNumKernels + 10 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
     const int mvi = mv == DT_F32 ? 0 : mv == DT_BF16 ? 1 : 2;
     const int pti = pt == DT_F24 ? 1 : 0;
     const int gti = gt == DT_BF16 ? 1 : 0;

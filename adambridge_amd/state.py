@@ -27,6 +27,7 @@ f32-records     AdamW, FP32 master, FP32 moments       3072 per 256 (x2 double-b
 f24-records     AdamW, FP24 master, BF16 moments       1792 per 256 (x2 double-buffered)
 f24-f32-rec.    AdamW, FP24 master, FP32 moments       2816 per 256 (x2 double-buffered)
 lion-f24-rec.   Lion, FP24 master, BF16 moment         1280 per 256 (x2 double-buffered)
+lion-f24-f32-r. Lion, FP24 master, FP32 moment         1792 per 256 (x2 double-buffered)
 ==============  =====================================  ======================================
 
 The interleaved layouts turn the master and moment streams into one stream of
@@ -46,11 +47,12 @@ from . import formats as F
 from .precision import BF16Store, FP8Store, FP24Store, FP32Store, MomentStore, load_master_, make_master, make_store
 
 __all__ = ["ParamState", "SeparateState", "PairState", "AdamRecordState", "LionRecordState", "F32RecordState",
-           "F24RecordState", "LionF24RecordState", "AdamF24RecordState", "LionF32RecordState", "LionFP8RecordState", "F24F32RecordState", "choose_layout", "new_state", "new_states",
+           "F24RecordState", "LionF24RecordState", "AdamF24RecordState", "LionF32RecordState", "LionFP8RecordState", "F24F32RecordState", "LionF24F32RecordState", "choose_layout", "new_state", "new_states",
            "arena_plan", "arena_memory", "LAYOUTS"]
 
 LAYOUTS = ("separate", "pairs", "fp8-records", "lion-records", "f32-records", "f24-records", "lion-f24-records",
-           "fp8-f24-records", "lion-f32-records", "lion-fp8-records", "f24-f32-records")
+           "fp8-f24-records", "lion-f32-records", "lion-fp8-records", "f24-f32-records",
+           "lion-f24-f32-records")
 IN_PLACE = ("fp8-records", "fp8-f24-records", "lion-fp8-records")   # never double-buffered
 
 # Arenas of at least this many bytes follow an allocate/free of their own size (new_states); None: never.
@@ -65,8 +67,8 @@ def choose_layout(algorithm: str, precision: str, master_precision: str, request
         return "separate"
     if master_precision == "fp24":
         return {("adamw", "bf16"): "f24-records", ("lion", "bf16"): "lion-f24-records",
-                ("adamw", "fp8"): "fp8-f24-records", ("adamw", "fp32"): "f24-f32-records"}.get((algorithm, precision),
-                                                                                            "separate")
+                ("adamw", "fp8"): "fp8-f24-records", ("adamw", "fp32"): "f24-f32-records",
+                ("lion", "fp32"): "lion-f24-f32-records"}.get((algorithm, precision), "separate")
     return {("adamw", "bf16"): "pairs", ("adamw", "fp8"): "fp8-records", ("adamw", "fp32"): "f32-records",
             ("lion", "bf16"): "lion-records", ("lion", "fp32"): "lion-f32-records",
             ("lion", "fp8"): "lion-fp8-records"}.get((algorithm, precision),
@@ -657,6 +659,38 @@ class LionF24RecordState(F24RecordState):
         return w
 
 
+class LionF24F32RecordState(LionF24RecordState):
+    """Lion, FP24 master, FP32 moment: 1792-byte records of 256 elements, the 256 master high halves,
+    the 256 low bytes and the 256 m values (FP32), each in element order
+    (ADAMBRIDGE_DT_PACKED_LION_F24_F32)."""
+
+    layout = "lion-f24-f32-records"
+    precision = "fp32"
+    RECORD = 1792   # master_plane's record stride too
+
+    @staticmethod
+    def buffer_bytes(numel: int) -> int:
+        return max(1, -(-int(numel) // 256)) * LionF24F32RecordState.RECORD
+
+    def bind(self, seg):
+        super().bind(seg)
+        seg.p_dtype, seg.mv_dtype = _hip.DT_PACKED_LION_F24_F32, _hip.DT_F32
+
+    def _column(self, role):
+        """'p' the hi plane (BF16 bits), 'lo' the lo plane (uint8), 'm' the moment (FP32)."""
+        if role == "m":
+            return self.current[:, 768:1792].view(torch.float32)
+        return super()._column(role)
+
+    def moment(self, role):
+        return FP32Store(self.numel, init=self._column(role).reshape(-1)[: self.numel], device=self.device)
+
+    def load(self, master=None, moments=None):
+        F24RecordState.load(self, master)
+        for role, store in (moments or {}).items():
+            self._put(role, store.to_fp32().to(self.device))
+
+
 class AdamRecordState(_Interleaved):
     """AdamW, FP32 master, FP8 moments: one 768-byte record per 128-element block
     (ADAMBRIDGE_DT_PACKED_FP8) -- lane l's elements 8l .. 8l + 7 keep their masters at 16l (first
@@ -842,7 +876,8 @@ def _bf16_bits(store: MomentStore, device) -> torch.Tensor:
 _INTERLEAVED = {"pairs": PairState, "lion-records": LionRecordState, "fp8-records": AdamRecordState,
                 "f32-records": F32RecordState, "f24-records": F24RecordState, "lion-f24-records": LionF24RecordState,
                 "fp8-f24-records": AdamF24RecordState, "lion-f32-records": LionF32RecordState,
-                "lion-fp8-records": LionFP8RecordState, "f24-f32-records": F24F32RecordState}
+                "lion-fp8-records": LionFP8RecordState, "f24-f32-records": F24F32RecordState,
+                "lion-f24-f32-records": LionF24F32RecordState}
 ARENA_ALIGN = 2 << 20
 SMALL_ALIGN = 256
 

@@ -41,7 +41,7 @@ enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, AD
        ADAMBRIDGE_DT_F24 = 4, ADAMBRIDGE_DT_PACKED = 5, ADAMBRIDGE_DT_PACKED_FP8 = 6,
        ADAMBRIDGE_DT_PACKED_LION = 7, ADAMBRIDGE_DT_PACKED_F32 = 8, ADAMBRIDGE_DT_PACKED_F24 = 9,
        ADAMBRIDGE_DT_PACKED_LION_F24 = 10, ADAMBRIDGE_DT_PACKED_FP8_F24 = 11, ADAMBRIDGE_DT_PACKED_LION_F32 = 12,
-       ADAMBRIDGE_DT_PACKED_LION_FP8 = 13, ADAMBRIDGE_DT_PACKED_F24_F32 = 14 };
+       ADAMBRIDGE_DT_PACKED_LION_FP8 = 13, ADAMBRIDGE_DT_PACKED_F24_F32 = 14, ADAMBRIDGE_DT_PACKED_LION_F24_F32 = 15 };
 
 /* ADAMBRIDGE_DT_PACKED (p_dtype; no counterpart in the reference): an HBM layout for
  * AdamW with an FP32 master and BF16 moments (mv_dtype DT_BF16).  p points at 16-byte
@@ -101,6 +101,9 @@ enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, AD
 /* ADAMBRIDGE_DT_PACKED_LION_F24 (p_dtype; no counterpart in the reference): the same for Lion with an
  * FP24 master and a BF16 moment: one 1280-byte record per 256 elements, the 256 master high halves
  * (bytes 0 .. 511), the 256 low bytes (512 .. 767) and the 256 m values (768 .. 1279). */
+/* ADAMBRIDGE_DT_PACKED_LION_F24_F32 (p_dtype; no counterpart in the reference): the same with an FP32
+ * moment (mv_dtype DT_F32): one 1792-byte record per 256 elements, the m values FP32 at 768 .. 1791,
+ * stored exactly. */
 /* ADAMBRIDGE_DT_PACKED_FP8_F24 (p_dtype; no counterpart in the reference): an HBM layout for AdamW
  * with an FP24 master and FP8 moments (mv_dtype DT_FP8).  p points at one 640-byte record per
  * 128-element block, ceil(n/128) records, 16-byte aligned.  The record of block b holds its 128
@@ -175,10 +178,12 @@ typedef struct adambridge_segment {
     void* p;                 /* FP32 master, the FP24 hi plane (uint16) when p_dtype is DT_F24, or the
                                 packed state when p_dtype is DT_PACKED / DT_PACKED_FP8 / DT_PACKED_LION /
                                 DT_PACKED_F32 / DT_PACKED_F24 / DT_PACKED_LION_F24 / DT_PACKED_FP8_F24 /
-                                DT_PACKED_LION_F32 / DT_PACKED_LION_FP8 / DT_PACKED_F24_F32 */
+                                DT_PACKED_LION_F32 / DT_PACKED_LION_FP8 / DT_PACKED_F24_F32 /
+                                DT_PACKED_LION_F24_F32 */
     uint8_t* p_lo;           /* FP24 lo plane (one byte per element); NULL for FP32; DT_PACKED,
                                 DT_PACKED_LION, DT_PACKED_F32, DT_PACKED_F24, DT_PACKED_LION_F24 and
-                                DT_PACKED_LION_F32, DT_PACKED_F24_F32: the destination state
+                                DT_PACKED_LION_F32, DT_PACKED_F24_F32, DT_PACKED_LION_F24_F32: the
+                                destination state
                                 (NULL: in place) */
     const void* g;           /* gradient, g_dtype */
     void* m;                 /* first moment, mv_dtype (FP8: E4M3 codes, padded to 128 per block) */
@@ -197,7 +202,7 @@ typedef struct adambridge_segment {
     int32_t algorithm;
     int32_t p_dtype;         /* DT_F32 (or 0), DT_F24, DT_PACKED, DT_PACKED_FP8, DT_PACKED_LION, DT_PACKED_F32,
                                 DT_PACKED_F24, DT_PACKED_LION_F24, DT_PACKED_FP8_F24, DT_PACKED_LION_F32,
-                                DT_PACKED_LION_FP8 or DT_PACKED_F24_F32 */
+                                DT_PACKED_LION_FP8, DT_PACKED_F24_F32 or DT_PACKED_LION_F24_F32 */
     int32_t reserved;        /* 0, or ADAMBRIDGE_SEG_OUT_PREVIOUS */
 } adambridge_segment;
 
@@ -226,6 +231,7 @@ ADAMBRIDGE_API int adambridge_abi_version(void);
 #define ADAMBRIDGE_CAP_LION_FP8_RECORDS 0x100u /* p_dtype DT_PACKED_LION_FP8 (13); record size in a
                                                  DT_PACKED_FP8 plane's stride */
 #define ADAMBRIDGE_CAP_F24_F32_RECORDS 0x200u /* p_dtype DT_PACKED_F24_F32 (14) */
+#define ADAMBRIDGE_CAP_LION_F24_F32_RECORDS 0x400u /* p_dtype DT_PACKED_LION_F24_F32 (15) */
 ADAMBRIDGE_API uint32_t adambridge_capabilities(void);
 
 /* kernels.c:1495-1510.  The level whose results are reproduced: its vector
@@ -350,7 +356,7 @@ ADAMBRIDGE_API int adambridge_convert(const void* src, const float* src_scale, i
  *     DT_PACKED           {s, NULL, 16, DT_F32, 1}       DT_PACKED_LION      {s, NULL, 1536, DT_F32, 8}
  *     DT_PACKED_F32       {s, NULL, 3072, DT_F32, 8}     DT_PACKED_F24       {s, s + 512, 1792, DT_F24, 8}
  *     DT_PACKED_LION_F24  {s, s + 512, 1280, DT_F24, 8}   DT_PACKED_LION_F32  {s, NULL, 2048, DT_F32, 8}
- *     DT_PACKED_F24_F32   {s, s + 512, 2816, DT_F24, 8}
+ *     DT_PACKED_F24_F32   {s, s + 512, 2816, DT_F24, 8}   DT_PACKED_LION_F24_F32 {s, s + 512, 1792, DT_F24, 8}
  * and a separate FP24 master is {hi, lo, 0, DT_F24, 0}.  data is aligned to its value size (16 bytes
  * for DT_PACKED_FP8) and stride a multiple of it. */
 typedef struct adambridge_plane {

@@ -514,8 +514,8 @@ F24_F32_COLUMNS = F24_COLUMNS[:2] + (("m", (768, 1792), np.uint32, 0x7FA6A6A6),
 
 def _f24_columns(case: O.Case):
     """The case's FP24-master record columns and record size."""
-    if case.mv_dtype == O.DT_F32:
-        return F24_F32_COLUMNS, 2816
+    if case.mv_dtype == O.DT_F32:   # Lion: ADAMBRIDGE_DT_PACKED_LION_F24_F32, no v
+        return (F24_F32_COLUMNS[:3], 1792) if case.algorithm == O.LION else (F24_F32_COLUMNS, 2816)
     if case.algorithm == O.LION:   # ADAMBRIDGE_DT_PACKED_LION_F24: no v
         return F24_COLUMNS[:3], 1280
     return F24_COLUMNS, 1792
@@ -559,7 +559,9 @@ _RECORDS = {"f32": (_hip.DT_PACKED_F32, O.DT_F32, O.DT_F32, pack_f32_records, un
                          O.LION),
             "lion-f32": (_hip.DT_PACKED_LION_F32, O.DT_F32, O.DT_F32, pack_f32_records, unpack_f32_records,
                          O.LION),
-            "f24-f32": (_hip.DT_PACKED_F24_F32, O.DT_F32, O.DT_F24, pack_f24_records, unpack_f24_records, O.ADAMW)}
+            "f24-f32": (_hip.DT_PACKED_F24_F32, O.DT_F32, O.DT_F24, pack_f24_records, unpack_f24_records, O.ADAMW),
+            "lion-f24-f32": (_hip.DT_PACKED_LION_F24_F32, O.DT_F32, O.DT_F24, pack_f24_records, unpack_f24_records,
+                             O.LION)}
 
 
 def run_hip_lion_f32_records(cases: list[O.Case], width: int = 16, **kw) -> list[O.Case]:
@@ -570,8 +572,8 @@ def run_hip_lion_f32_records(cases: list[O.Case], width: int = 16, **kw) -> list
 def run_hip_f24_records(cases: list[O.Case], width: int = 16, **kw) -> list[O.Case]:
     """run_hip through FP24-master records: ADAMBRIDGE_DT_PACKED_F24 (AdamW, BF16 moments),
     ADAMBRIDGE_DT_PACKED_F24_F32 (AdamW, FP32 moments) or, for Lion cases,
-    ADAMBRIDGE_DT_PACKED_LION_F24 (BF16 moment)."""
-    kinds = {"lion-f24" if c.algorithm == O.LION else "f24-f32" if c.mv_dtype == O.DT_F32 else "f24" for c in cases}
+    ADAMBRIDGE_DT_PACKED_LION_F24 (BF16 moment) and ADAMBRIDGE_DT_PACKED_LION_F24_F32 (FP32 moment)."""
+    kinds = {("lion-" if c.algorithm == O.LION else "") + ("f24-f32" if c.mv_dtype == O.DT_F32 else "f24") for c in cases}
     assert len(kinds) == 1
     return run_hip_f32_records(cases, width, kind=kinds.pop(), **kw)
 

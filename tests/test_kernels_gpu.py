@@ -498,8 +498,8 @@ def test_f32_records_multi_step_groups_and_steps():
 
 
 # (algorithm, moments) of the FP24-master records: ADAMBRIDGE_DT_PACKED_F24, _LION_F24, _F24_F32
-F24_KINDS = [(O.ADAMW, O.DT_BF16), (O.LION, O.DT_BF16), (O.ADAMW, O.DT_F32)]
-F24_IDS = ["adamw-bf16", "lion-bf16", "adamw-f32"]
+F24_KINDS = [(O.ADAMW, O.DT_BF16), (O.LION, O.DT_BF16), (O.ADAMW, O.DT_F32), (O.LION, O.DT_F32)]
+F24_IDS = ["adamw-bf16", "lion-bf16", "adamw-f32", "lion-f32"]
 
 
 @pytest.mark.parametrize("algo,mv", F24_KINDS, ids=F24_IDS)
@@ -511,7 +511,7 @@ def test_f24_records_match_oracle(double_buffer, algo, mv):
     offsets, stochastic and nearest rounding, every grad/out dtype, delayed (previous-weight)
     output; in place, the padding slots of the last record keep their bits."""
     from hip_cases import _f24_columns
-    rng = np.random.default_rng(61 + algo + 5 * (mv == O.DT_F32))
+    rng = np.random.default_rng(61 + algo + 5 * (mv == O.DT_F32))   # ADAMBRIDGE_DT_PACKED_LION_F24_F32 too
     cases = []
     for gt, ot, n in itertools.product([O.DT_BF16, O.DT_F32], [O.DT_NONE, O.DT_F32, O.DT_BF16],
                                        [1, 2, 3, 4, 5, 15, 16, 17, 255, 256, 257, 1000, 2048 + 77, 5001]):
@@ -803,7 +803,7 @@ def _previous_weight(case):
 
 @pytest.mark.parametrize("layout", ["separate", "pairs", "fp8-records", "lion-records", "f32-records", "f24-records",
                                     "lion-f24-records", "fp8-f24-records", "lion-f32-records", "lion-fp8-records",
-                                    "f24-f32-records"])
+                                    "f24-f32-records", "lion-f24-f32-records"])
 def test_out_previous_writes_the_weight_from_before_the_update(layout):
     """ADAMBRIDGE_SEG_OUT_PREVIOUS (delayed updates): out receives the weight of the master as stored
     before the update -- FP32, or bf16 by the kernels' rounding of FP32 and decoded FP24 masters,
@@ -819,12 +819,14 @@ def test_out_previous_writes_the_weight_from_before_the_update(layout):
               "f24-records": [(O.ADAMW, O.DT_BF16, O.DT_F24)], "lion-f24-records": [(O.LION, O.DT_BF16, O.DT_F24)],
               "fp8-f24-records": [(O.ADAMW, O.DT_FP8, O.DT_F24)],
               "lion-f32-records": [(O.LION, O.DT_F32, O.DT_F32)], "lion-fp8-records": [(O.LION, O.DT_FP8, O.DT_F32)],
-              "f24-f32-records": [(O.ADAMW, O.DT_F32, O.DT_F24)]}[layout]
+              "f24-f32-records": [(O.ADAMW, O.DT_F32, O.DT_F24)],
+              "lion-f24-f32-records": [(O.LION, O.DT_F32, O.DT_F24)]}[layout]
     runner = {"separate": run_hip, "pairs": run_hip_packed, "fp8-records": run_hip_records,
               "lion-records": run_hip_lion_records, "f32-records": run_hip_f32_records,
               "f24-records": run_hip_f24_records, "lion-f24-records": run_hip_f24_records,
               "fp8-f24-records": run_hip_records, "lion-f32-records": run_hip_lion_f32_records,
-              "lion-fp8-records": run_hip_records, "f24-f32-records": run_hip_f24_records}[layout]
+              "lion-fp8-records": run_hip_records, "f24-f32-records": run_hip_f24_records,
+              "lion-f24-f32-records": run_hip_f24_records}[layout]
     cases = []
     for (algo, mv, pt), gt, ot, sr, n in itertools.product(combos, [O.DT_BF16, O.DT_F32], [O.DT_F32, O.DT_BF16],
                                                              [True, False], [1, 15, 17, 129, 1000, 8192 + 77]):
