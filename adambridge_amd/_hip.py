@@ -21,7 +21,7 @@ import torch
 
 __all__ = ["HipKernels", "HParams", "Group", "Segment", "Plane", "plane_of", "fp24_plane", "load", "LIB_PATH", "DT_NONE", "DT_F32", "DT_BF16",
            "DT_FP8", "DT_F24", "DT_PACKED", "DT_PACKED8", "DT_PACKED_LION", "DT_PACKED_F32", "DT_PACKED_F24", "DT_PACKED_LION_F24",
-           "DT_PACKED8_F24", "DT_PACKED_LION_F32", "DT_PACKED8_LION", "DT_PACKED_F24_F32", "DT_PACKED_LION_F24_F32",
+           "DT_PACKED8_F24", "DT_PACKED_LION_F32", "DT_PACKED8_LION", "DT_PACKED_F24_F32", "DT_PACKED_LION_F24_F32", "DT_PACKED8_LION_F24",
            "SEG_OUT_PREVIOUS", "MOMENT_CODES", "MASTER_CODES",
            "ALGORITHMS", "SIMD_NAMES"]
 
@@ -30,7 +30,7 @@ ABI_VERSION = 5
 
 (DT_NONE, DT_F32, DT_BF16, DT_FP8, DT_F24, DT_PACKED, DT_PACKED8, DT_PACKED_LION, DT_PACKED_F32, DT_PACKED_F24,
  DT_PACKED_LION_F24, DT_PACKED8_F24, DT_PACKED_LION_F32, DT_PACKED8_LION, DT_PACKED_F24_F32,
- DT_PACKED_LION_F24_F32) = range(16)
+ DT_PACKED_LION_F24_F32, DT_PACKED8_LION_F24) = range(17)
 SEG_OUT_PREVIOUS = 1   # Segment.reserved: out receives the weight of the master before the update
 _DTYPE_CODES = {torch.float32: DT_F32, torch.bfloat16: DT_BF16}
 MOMENT_CODES = {"fp32": DT_F32, "bf16": DT_BF16, "fp8": DT_FP8}
@@ -77,7 +77,7 @@ CONVERT_STOCHASTIC = 1
 CAPABILITIES = {"packed_layouts": 0x01, "out_previous": 0x02, "noalloc": 0x04, "convert": 0x08,
                 "convert_plane": 0x10, "stream_copy": 0x20, "fp8_f24_records": 0x40, "lion_f32_records": 0x80,
                 "lion_fp8_records": 0x100, "f24_f32_records": 0x200,
-                "lion_f24_f32_records": 0x400}
+                "lion_f24_f32_records": 0x400, "lion_fp8_f24_records": 0x800}
 
 
 def plane_of(t: torch.Tensor) -> Plane:

@@ -19,7 +19,8 @@ namespace abh {
 enum : int { DT_NONE = 0, DT_F32 = 1, DT_BF16 = 2, DT_FP8 = 3, DT_F24 = 4, DT_PACKED = 5, DT_PACKED8 = 6,
              DT_PACKED_LION = 7, DT_PACKED_F32 = 8, DT_PACKED_F24 = 9,
              DT_PACKED_LION_F24 = 10, DT_PACKED8_F24 = 11, DT_PACKED_LION_F32 = 12,
-             DT_PACKED8_LION = 13, DT_PACKED_F24_F32 = 14, DT_PACKED_LION_F24_F32 = 15 };
+             DT_PACKED8_LION = 13, DT_PACKED_F24_F32 = 14, DT_PACKED_LION_F24_F32 = 15,
+             DT_PACKED8_LION_F24 = 16 };
 enum : int { ALGO_ADAMW = 0, ALGO_LION = 1 };
 constexpr int kFp8Block = 128;
 

@@ -251,8 +251,18 @@ __device__ __forceinline__ int64_t record_master_offset(int64_t i, int64_t rec =
 constexpr int64_t kRecordBytesF24 = 640;
 
 // Byte offsets of element i's master high half and low byte within those records.
-__device__ __forceinline__ int64_t record_f24_hi_offset(int64_t i) { return (i >> 7) * kRecordBytesF24 + (i & 127) * 2; }
-__device__ __forceinline__ int64_t record_f24_lo_offset(int64_t i) { return (i >> 7) * kRecordBytesF24 + 256 + (i & 127); }
+// Lion FP8 records with an FP24 master (p_dtype DT_PACKED8_LION_F24) are the same without the v codes:
+// 512 bytes, lane l's m codes at 384 + 8l (the block's codes in element order).
+constexpr int64_t kRecordBytesLion8F24 = 512;
+
+__device__ __forceinline__ int64_t record_f24_hi_offset(int64_t i, int64_t rec = kRecordBytesF24)
+{
+    return (i >> 7) * rec + (i & 127) * 2;
+}
+__device__ __forceinline__ int64_t record_f24_lo_offset(int64_t i, int64_t rec = kRecordBytesF24)
+{
+    return (i >> 7) * rec + 256 + (i & 127);
+}
 
 // The masters of 8 consecutive elements: the FP24 planes at p (high halves) and lo (low bytes),
 // a record's two 16-byte halves at p and p + 256 (DT_PACKED8), or FP32 at p.
@@ -417,10 +427,11 @@ __device__ __forceinline__ float load_master1(const DevSeg& s, int64_t i)
 {
     if constexpr (PT == DT_F24)
         return bitsf(((uint32_t)ld(static_cast<const uint16_t*>(s.p) + i) << 16) | ((uint32_t)ld(s.p_lo + i) << 8));
-    else if constexpr (PT == DT_PACKED8_F24) {
+    else if constexpr (PT == DT_PACKED8_F24 || PT == DT_PACKED8_LION_F24) {
+        constexpr int64_t rec = PT == DT_PACKED8_F24 ? kRecordBytesF24 : kRecordBytesLion8F24;
         const uint8_t* r = static_cast<const uint8_t*>(s.p);
-        return bitsf(((uint32_t)ld(reinterpret_cast<const uint16_t*>(r + record_f24_hi_offset(i))) << 16) |
-                     ((uint32_t)ld(r + record_f24_lo_offset(i)) << 8));
+        return bitsf(((uint32_t)ld(reinterpret_cast<const uint16_t*>(r + record_f24_hi_offset(i, rec))) << 16) |
+                     ((uint32_t)ld(r + record_f24_lo_offset(i, rec)) << 8));
     } else if constexpr (PT == DT_PACKED8 || PT == DT_PACKED8_LION)
         return ld(reinterpret_cast<const float*>(static_cast<const uint8_t*>(s.p) +
                                                  record_master_offset(i, PT == DT_PACKED8 ? kRecordBytes : kRecordBytesLion8)));
@@ -435,11 +446,12 @@ __device__ __forceinline__ float store_master1(const DevSeg& s, int64_t i, float
         st(static_cast<uint16_t*>(s.p) + i, (uint16_t)(b >> 16));
         st(s.p_lo + i, (uint8_t)(b >> 8));
         return bitsf(b);
-    } else if constexpr (PT == DT_PACKED8_F24) {
+    } else if constexpr (PT == DT_PACKED8_F24 || PT == DT_PACKED8_LION_F24) {
+        constexpr int64_t rec = PT == DT_PACKED8_F24 ? kRecordBytesF24 : kRecordBytesLion8F24;
         const uint32_t b = f24_round<SR>(x, SR ? hash32(idx ^ s.seed_p) : 0u);
         uint8_t* r = static_cast<uint8_t*>(s.p);
-        st(reinterpret_cast<uint16_t*>(r + record_f24_hi_offset(i)), (uint16_t)(b >> 16));
-        st(r + record_f24_lo_offset(i), (uint8_t)(b >> 8));
+        st(reinterpret_cast<uint16_t*>(r + record_f24_hi_offset(i, rec)), (uint16_t)(b >> 16));
+        st(r + record_f24_lo_offset(i, rec), (uint8_t)(b >> 8));
         return bitsf(b);
     } else if constexpr (PT == DT_PACKED8 || PT == DT_PACKED8_LION) {
         st(reinterpret_cast<float*>(static_cast<uint8_t*>(s.p) +
@@ -676,14 +688,18 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     constexpr bool kLion = ALGO == ALGO_LION;
     constexpr int kGB = GT == DT_BF16 ? 2 : 4, kOB = OT == DT_BF16 ? 2 : 4, kPB = PT == DT_F24 ? 2 : 4;
     // block records: AdamW with an FP32 master (DT_PACKED8) or an FP24 master (DT_PACKED8_F24), Lion
-    // with an FP32 master (DT_PACKED8_LION: the m codes in element order at 512)
-    constexpr bool kRec = PT == DT_PACKED8 || PT == DT_PACKED8_F24 || PT == DT_PACKED8_LION;
-    constexpr bool kRecLion = PT == DT_PACKED8_LION;
+    // with an FP32 master (DT_PACKED8_LION: the m codes in element order at 512) or an FP24 master
+    // (DT_PACKED8_LION_F24: at 384)
+    constexpr bool kRecF24 = PT == DT_PACKED8_F24 || PT == DT_PACKED8_LION_F24;
+    constexpr bool kRecLion = PT == DT_PACKED8_LION || PT == DT_PACKED8_LION_F24;
+    constexpr bool kRec = PT == DT_PACKED8 || kRecF24 || kRecLion;
     constexpr uint32_t kRecB = PT == DT_PACKED8 ? (uint32_t)kRecordBytes
-                             : kRecLion ? (uint32_t)kRecordBytesLion8 : (uint32_t)kRecordBytesF24;
+                             : PT == DT_PACKED8_LION ? (uint32_t)kRecordBytesLion8
+                             : PT == DT_PACKED8_LION_F24 ? (uint32_t)kRecordBytesLion8F24 : (uint32_t)kRecordBytesF24;
     constexpr uint32_t kCodesAt = PT == DT_PACKED8 ? 512u : 384u;   // the AdamW records' code slots
-    constexpr uint32_t kLoAt = kRecLion ? 512u : 256u;              // the 8-byte slots: low bytes, Lion codes
-    constexpr int kMaster = PT == DT_PACKED8_F24 ? DT_F24 : kRecLion ? DT_PACKED8 : PT;   // how the 8 masters are coded
+    constexpr uint32_t kLoAt = PT == DT_PACKED8_LION ? 512u : 256u; // the 8-byte slots: low bytes, Lion codes
+    constexpr uint32_t kLionCodes = PT == DT_PACKED8_LION_F24 ? 128u : 0u;   // Lion's codes past rec_lo
+    constexpr int kMaster = kRecF24 ? DT_F24 : kRecLion ? DT_PACKED8 : PT;   // how the 8 masters are coded
     const int64_t n = s.n, n_main = s.n_main;
     const bool vec = FULL || (s.flags & kVec) != 0;
     uint8_t* const mq = static_cast<uint8_t*>(s.m);
@@ -715,7 +731,7 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     };
     auto pl = [&](uint32_t o, uint32_t rl) -> uint8_t* {
         if constexpr (PT == DT_F24) return lane_ptr<uint8_t>(s.p_lo, base, o);
-        else if constexpr (PT == DT_PACKED8_F24) return lane_ptr<uint8_t>(s.p, ublk * kRecB, rl);
+        else if constexpr (kRecF24) return lane_ptr<uint8_t>(s.p, ublk * kRecB, rl);
         else return nullptr;
     };
     auto po = [&](uint32_t o) -> void* {
@@ -725,7 +741,7 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     // codes are stored padded to whole blocks, so all 8 of this lane's exist
     u32x2 cm, cv = {0u, 0u};
     if constexpr (kRecLion) {
-        cm = ld(lane_ptr<const u32x2>(s.p, ublk * kRecB, rec_lo));
+        cm = ld(lane_ptr<const u32x2>(s.p, ublk * kRecB, rec_lo + kLionCodes));
     } else if constexpr (kRec) {
         const u32x4 w = ld(lane_ptr<const u32x4>(s.p, ublk * kRecB, rec_lane + kCodesAt));
         cm = u32x2{w.x, w.y};
@@ -793,7 +809,7 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     }
     if (full) {
         const uint32_t o = fresh(off);
-        const uint32_t ro = kRec ? fresh(rec_lane) : 0u, rl = PT == DT_PACKED8_F24 ? fresh(rec_lo) : 0u;
+        const uint32_t ro = kRec ? fresh(rec_lane) : 0u, rl = kRecF24 ? fresh(rec_lo) : 0u;
         store_master8<kMaster, SR>(pm(o, ro), pl(o, rl), p, idx, s.seed_p, w8);
         if constexpr (!PREV) store_out8<OT>(po(o), p);
     } else {
@@ -888,7 +904,7 @@ __device__ __forceinline__ void fp8_block(const DevSeg& s, const Coef& c, int64_
     }
     const uint32_t o = fresh(off);
     if constexpr (kRecLion) {
-        st(lane_ptr<u32x2>(s.p, ublk * kRecB, fresh(rec_lo)), u32x2{qm[0], qm[1]});
+        st(lane_ptr<u32x2>(s.p, ublk * kRecB, fresh(rec_lo) + kLionCodes), u32x2{qm[0], qm[1]});
     } else if constexpr (kRec) {
         st(lane_ptr<u32x4>(s.p, ublk * kRecB, fresh(rec_lane) + kCodesAt), u32x4{qm[0], qm[1], qv[0], qv[1]});
     } else if (vec) {
@@ -1752,13 +1768,32 @@ constexpr auto make_lion_f24f32rec_table(std::integer_sequence<int, I...>)
 
 static const auto kLionF24F32Rec = make_lion_f24f32rec_table(std::make_integer_sequence<int, kNumPacked>{});
 
+// Lion FP8 records with an FP24 master follow: index kNumKernels + 11 * kNumPacked + gt * 3 + ot.
+template <int I, bool WIDE>
+constexpr KernelFn packed8_lion_f24_entry()
+{
+    constexpr int ot = I % 3, gt = I / 3;
+    return &k_update_fp8<ALGO_LION, DT_PACKED8_LION_F24, gt ? DT_BF16 : DT_F32,
+                         ot == 0 ? DT_NONE : ot == 1 ? DT_F32 : DT_BF16, WIDE>;
+}
+
+template <bool WIDE, int... I>
+constexpr auto make_packed8_lion_f24_table(std::integer_sequence<int, I...>)
+{
+    return std::array<KernelFn, sizeof...(I)>{packed8_lion_f24_entry<I, WIDE>()...};
+}
+
+static const auto kPacked8LionF24 = make_packed8_lion_f24_table<false>(std::make_integer_sequence<int, kNumPacked>{});
+static const auto kPacked8LionF24Wide = make_packed8_lion_f24_table<true>(std::make_integer_sequence<int, kNumPacked>{});
+
 // Kernel family of a table index: the FP8 block kernel, or a two-element-per-lane kernel.
 inline bool kernel_is_fp8(int index)
 {
     if (index < kNumKernels) return (index / 12) % 3 == 2;
     return (index >= kNumKernels + kNumPacked && index < kNumKernels + 2 * kNumPacked) ||
            (index >= kNumKernels + 6 * kNumPacked && index < kNumKernels + 7 * kNumPacked) ||
-           (index >= kNumKernels + 8 * kNumPacked && index < kNumKernels + 9 * kNumPacked);
+           (index >= kNumKernels + 8 * kNumPacked && index < kNumKernels + 9 * kNumPacked) ||
+           index >= kNumKernels + 11 * kNumPacked;
 }
 
 // Dynamic LDS (unused) per workgroup of a launch of kernel `index`: it caps the workgroups a CU holds
@@ -1779,7 +1814,8 @@ inline bool kernel_is_fp8(int index)
 // 4: 3.70, 3: 3.74, 6: 3.89, 8: 3.97, 2: 4.58) and at 6 with an FP24 master (3.15 ms; 5 and 4:
 // 3.18, 8: 3.21).  Lion FP8 records: 5 per CU 3.51 ms, 4: 3.50, 6: 3.69, 8: 3.75.  FP24-master
 // FP32-moment records (6.74G elements in 8 tensors): 5 per CU 27.12 ms (the copy of their bytes:
-// 27.14), 6: 27.73, 8: 27.93.  The
+// 27.14), 6: 27.73, 8: 27.93.  Lion FP8 records with an FP24 master: 6 per CU 3.04 ms, 4: 3.10,
+// 5: 3.11, 8: 3.12.  The
 // BF16 pairs lose with fewer workgroups (the 0.5B list: 1.76 against 1.67 ms with 6), and the
 // FP24-master FP8 kernels keep 8 (records, the 7B list: 8 per CU 16.28-16.66, 7: 16.18-16.55, 6:
 // 16.44-16.65, 5: 17.56-17.91).  Those run at the speed of their accesses alone: a form that makes
@@ -1796,10 +1832,10 @@ inline size_t launch_lds(int index)
         return pt == 0 ? kCap5 : kCap6;   // Lion: FP32 / FP24 master
     }
     // 1: FP8 records, 3: FP32 records, 7: Lion records with an FP32 moment, 8: Lion FP8 records,
-    // 9: FP24-master FP32-moment records, 10: their Lion form
+    // 9: FP24-master FP32-moment records, 10: their Lion form, 11: Lion FP8 records with an FP24 master
     const int family = (index - kNumKernels) / kNumPacked;
     if (family == 8 || family == 9) return kCap5;
-    if (family == 10) return kCap6;
+    if (family == 10 || family == 11) return kCap6;
     return family == 1 || family == 3 || family == 7 ? kCap6 : 0;
 }
 
@@ -1809,7 +1845,8 @@ inline KernelFn wide_kernel_at(int index)
     if (index < kNumKernels) return kKernelsWide[index];
     if (index < kNumKernels + 2 * kNumPacked) return kPacked8Wide[index - kNumKernels - kNumPacked];
     if (index < kNumKernels + 7 * kNumPacked) return kPacked8F24Wide[index - kNumKernels - 6 * kNumPacked];
-    return kPacked8LionWide[index - kNumKernels - 8 * kNumPacked];
+    if (index < kNumKernels + 9 * kNumPacked) return kPacked8LionWide[index - kNumKernels - 8 * kNumPacked];
+    return kPacked8LionF24Wide[index - kNumKernels - 11 * kNumPacked];
 }
 
 inline KernelFn kernel_at(int index)
@@ -1825,7 +1862,8 @@ inline KernelFn kernel_at(int index)
     if (index < kNumKernels + 8 * kNumPacked) return kLionF32Rec[index - kNumKernels - 7 * kNumPacked];
     if (index < kNumKernels + 9 * kNumPacked) return kPacked8Lion[index - kNumKernels - 8 * kNumPacked];
     if (index < kNumKernels + 10 * kNumPacked) return kF24F32Rec[index - kNumKernels - 9 * kNumPacked];
-    return kLionF24F32Rec[index - kNumKernels - 10 * kNumPacked];
+    if (index < kNumKernels + 11 * kNumPacked) return kLionF24F32Rec[index - kNumKernels - 10 * kNumPacked];
+    return kPacked8LionF24[index - kNumKernels - 11 * kNumPacked];
 }
 
 inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
@@ -1852,6 +1890,8 @@ inline int kernel_index(int algo, int mv, int pt, int gt, int ot)
         return kNumKernels + 9 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
     if (pt == DT_PACKED_LION_F24_F32)
         return kNumKernels + 10 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
+    if (pt == DT_PACKED8_LION_F24)
+        return kNumKernels + 11 * kNumPacked + (gt == DT_BF16 ? 1 : 0) * 3 + (ot == DT_NONE ? 0 : ot == DT_F32 ? 1 : 2);
     const int mvi = mv == DT_F32 ? 0 : mv == DT_BF16 ? 1 : 2;
     const int pti = pt == DT_F24 ? 1 : 0;
     const int gti = gt == DT_BF16 ? 1 : 0;

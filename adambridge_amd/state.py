@@ -23,6 +23,7 @@ fp8-f24-rec.    AdamW, FP24 master, FP8 moments        640 per 128 + two FP32 sc
 lion-records    Lion, FP32 master, BF16 moment         1536 per 256 (x2 double-buffered)
 lion-f32-rec.   Lion, FP32 master, FP32 moment         2048 per 256 (x2 double-buffered)
 lion-fp8-rec.   Lion, FP32 master, FP8 moment          640 per 128 + one FP32 scale per 128
+lion-fp8-f24-r. Lion, FP24 master, FP8 moment          512 per 128 + one FP32 scale per 128
 f32-records     AdamW, FP32 master, FP32 moments       3072 per 256 (x2 double-buffered)
 f24-records     AdamW, FP24 master, BF16 moments       1792 per 256 (x2 double-buffered)
 f24-f32-rec.    AdamW, FP24 master, FP32 moments       2816 per 256 (x2 double-buffered)
@@ -47,13 +48,13 @@ from . import formats as F
 from .precision import BF16Store, FP8Store, FP24Store, FP32Store, MomentStore, load_master_, make_master, make_store
 
 __all__ = ["ParamState", "SeparateState", "PairState", "AdamRecordState", "LionRecordState", "F32RecordState",
-           "F24RecordState", "LionF24RecordState", "AdamF24RecordState", "LionF32RecordState", "LionFP8RecordState", "F24F32RecordState", "LionF24F32RecordState", "choose_layout", "new_state", "new_states",
+           "F24RecordState", "LionF24RecordState", "AdamF24RecordState", "LionF32RecordState", "LionFP8RecordState", "F24F32RecordState", "LionF24F32RecordState", "LionFP8F24RecordState", "choose_layout", "new_state", "new_states",
            "arena_plan", "arena_memory", "LAYOUTS"]
 
 LAYOUTS = ("separate", "pairs", "fp8-records", "lion-records", "f32-records", "f24-records", "lion-f24-records",
            "fp8-f24-records", "lion-f32-records", "lion-fp8-records", "f24-f32-records",
-           "lion-f24-f32-records")
-IN_PLACE = ("fp8-records", "fp8-f24-records", "lion-fp8-records")   # never double-buffered
+           "lion-f24-f32-records", "lion-fp8-f24-records")
+IN_PLACE = ("fp8-records", "fp8-f24-records", "lion-fp8-records", "lion-fp8-f24-records")   # never double-buffered
 
 # Arenas of at least this many bytes follow an allocate/free of their own size (new_states); None: never.
 RECYCLE_MIN_BYTES: int | None = 256 << 20
@@ -68,7 +69,8 @@ def choose_layout(algorithm: str, precision: str, master_precision: str, request
     if master_precision == "fp24":
         return {("adamw", "bf16"): "f24-records", ("lion", "bf16"): "lion-f24-records",
                 ("adamw", "fp8"): "fp8-f24-records", ("adamw", "fp32"): "f24-f32-records",
-                ("lion", "fp32"): "lion-f24-f32-records"}.get((algorithm, precision), "separate")
+                ("lion", "fp32"): "lion-f24-f32-records", ("lion", "fp8"): "lion-fp8-f24-records"}.get(
+                    (algorithm, precision), "separate")
     return {("adamw", "bf16"): "pairs", ("adamw", "fp8"): "fp8-records", ("adamw", "fp32"): "f32-records",
             ("lion", "bf16"): "lion-records", ("lion", "fp32"): "lion-f32-records",
             ("lion", "fp8"): "lion-fp8-records"}.get((algorithm, precision),
@@ -864,6 +866,42 @@ class LionFP8RecordState(AdamRecordState):
                 "m_scale": self.scales["m"][b0:b1]}
 
 
+class LionFP8F24RecordState(AdamF24RecordState):
+    """Lion, FP24 master, FP8 moment: one 512-byte record per 128-element block
+    (ADAMBRIDGE_DT_PACKED_LION_FP8_F24) -- the block's 128 master high halves at 0 and 128 low bytes at
+    256, then its 128 m codes at 384, each in element order -- plus the FP32 m block scales.  Updated
+    in place."""
+
+    layout = "lion-fp8-f24-records"
+    RECORD = 512   # master_plane's record stride too
+
+    def __init__(self, numel, device, double_buffer: bool = False, memory: list[torch.Tensor] | None = None):
+        self.blocks = F.fp8_blocks(int(numel))
+        rec = memory[0].view(self.blocks, self.RECORD) if memory else \
+            torch.zeros(self.blocks, self.RECORD, dtype=torch.uint8, device=device)
+        _Interleaved.__init__(self, numel, device, ("m",), [rec])   # updated in place: never double-buffered
+        self.scales = {"m": torch.ones(self.blocks, dtype=torch.float32, device=device)}
+
+    @staticmethod
+    def buffer_bytes(numel: int) -> int:
+        return F.fp8_blocks(int(numel)) * LionFP8F24RecordState.RECORD
+
+    def bind(self, seg):
+        seg.p, seg.p_lo, seg.m, seg.v = self.current.data_ptr(), None, None, None
+        seg.m_scale, seg.v_scale = self.scales["m"].data_ptr(), None
+        seg.p_dtype, seg.mv_dtype = _hip.DT_PACKED8_LION_F24, _hip.DT_FP8
+
+    def _column(self, role):
+        if role == "m":
+            return self.current[:, 384:].view(self.blocks, 16, 8)   # element order
+        return super()._column(role)
+
+    def window(self, lo, hi):
+        b0, b1 = lo // 128, -(-hi // 128)
+        return {"p": self._column("p").reshape(-1)[lo:hi], "p_lo": self._column("lo").reshape(-1)[lo:hi],
+                "m": self._column("m")[b0:b1].reshape(-1), "m_scale": self.scales["m"][b0:b1]}
+
+
 def _bf16_bits(store: MomentStore, device) -> torch.Tensor:
     """A moment's values as BF16 (the store's own bits when it is BF16, nearest-even otherwise)."""
     if isinstance(store, BF16Store):
@@ -877,7 +915,7 @@ _INTERLEAVED = {"pairs": PairState, "lion-records": LionRecordState, "fp8-record
                 "f32-records": F32RecordState, "f24-records": F24RecordState, "lion-f24-records": LionF24RecordState,
                 "fp8-f24-records": AdamF24RecordState, "lion-f32-records": LionF32RecordState,
                 "lion-fp8-records": LionFP8RecordState, "f24-f32-records": F24F32RecordState,
-                "lion-f24-f32-records": LionF24F32RecordState}
+                "lion-f24-f32-records": LionF24F32RecordState, "lion-fp8-f24-records": LionFP8F24RecordState}
 ARENA_ALIGN = 2 << 20
 SMALL_ALIGN = 256
 

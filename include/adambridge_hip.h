@@ -41,7 +41,8 @@ enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, AD
        ADAMBRIDGE_DT_F24 = 4, ADAMBRIDGE_DT_PACKED = 5, ADAMBRIDGE_DT_PACKED_FP8 = 6,
        ADAMBRIDGE_DT_PACKED_LION = 7, ADAMBRIDGE_DT_PACKED_F32 = 8, ADAMBRIDGE_DT_PACKED_F24 = 9,
        ADAMBRIDGE_DT_PACKED_LION_F24 = 10, ADAMBRIDGE_DT_PACKED_FP8_F24 = 11, ADAMBRIDGE_DT_PACKED_LION_F32 = 12,
-       ADAMBRIDGE_DT_PACKED_LION_FP8 = 13, ADAMBRIDGE_DT_PACKED_F24_F32 = 14, ADAMBRIDGE_DT_PACKED_LION_F24_F32 = 15 };
+       ADAMBRIDGE_DT_PACKED_LION_FP8 = 13, ADAMBRIDGE_DT_PACKED_F24_F32 = 14, ADAMBRIDGE_DT_PACKED_LION_F24_F32 = 15,
+       ADAMBRIDGE_DT_PACKED_LION_FP8_F24 = 16 };
 
 /* ADAMBRIDGE_DT_PACKED (p_dtype; no counterpart in the reference): an HBM layout for
  * AdamW with an FP32 master and BF16 moments (mv_dtype DT_BF16).  p points at 16-byte
@@ -121,6 +122,10 @@ enum { ADAMBRIDGE_DT_NONE = 0, ADAMBRIDGE_DT_F32 = 1, ADAMBRIDGE_DT_BF16 = 2, AD
  * are padding (codes written as 0, master left as it is).  m_scale holds the usual block scales;
  * m, v, v_scale and p_lo are unused (p_lo must be NULL: updated in place).  Same arithmetic,
  * rounding and rounding streams as the separate FP8 layout. */
+/* ADAMBRIDGE_DT_PACKED_LION_FP8_F24 (p_dtype; no counterpart in the reference): the same for Lion with
+ * an FP24 master: one 512-byte record per 128-element block, the master high halves (bytes 0 .. 255)
+ * and low bytes (256 .. 383) as in DT_PACKED_FP8_F24, then the block's 128 m codes in element order
+ * (384 .. 511). */
 enum { ADAMBRIDGE_ALGO_ADAMW = 0, ADAMBRIDGE_ALGO_LION = 1 };
 
 /* Error codes (kernels.c:1537-1553, 1582-1584, 1620-1621), plus the HIP-side ones. */
@@ -179,7 +184,7 @@ typedef struct adambridge_segment {
                                 packed state when p_dtype is DT_PACKED / DT_PACKED_FP8 / DT_PACKED_LION /
                                 DT_PACKED_F32 / DT_PACKED_F24 / DT_PACKED_LION_F24 / DT_PACKED_FP8_F24 /
                                 DT_PACKED_LION_F32 / DT_PACKED_LION_FP8 / DT_PACKED_F24_F32 /
-                                DT_PACKED_LION_F24_F32 */
+                                DT_PACKED_LION_F24_F32 / DT_PACKED_LION_FP8_F24 */
     uint8_t* p_lo;           /* FP24 lo plane (one byte per element); NULL for FP32; DT_PACKED,
                                 DT_PACKED_LION, DT_PACKED_F32, DT_PACKED_F24, DT_PACKED_LION_F24 and
                                 DT_PACKED_LION_F32, DT_PACKED_F24_F32, DT_PACKED_LION_F24_F32: the
@@ -202,7 +207,8 @@ typedef struct adambridge_segment {
     int32_t algorithm;
     int32_t p_dtype;         /* DT_F32 (or 0), DT_F24, DT_PACKED, DT_PACKED_FP8, DT_PACKED_LION, DT_PACKED_F32,
                                 DT_PACKED_F24, DT_PACKED_LION_F24, DT_PACKED_FP8_F24, DT_PACKED_LION_F32,
-                                DT_PACKED_LION_FP8, DT_PACKED_F24_F32 or DT_PACKED_LION_F24_F32 */
+                                DT_PACKED_LION_FP8, DT_PACKED_F24_F32, DT_PACKED_LION_F24_F32 or
+                                DT_PACKED_LION_FP8_F24 */
     int32_t reserved;        /* 0, or ADAMBRIDGE_SEG_OUT_PREVIOUS */
 } adambridge_segment;
 
@@ -232,6 +238,7 @@ ADAMBRIDGE_API int adambridge_abi_version(void);
                                                  DT_PACKED_FP8 plane's stride */
 #define ADAMBRIDGE_CAP_F24_F32_RECORDS 0x200u /* p_dtype DT_PACKED_F24_F32 (14) */
 #define ADAMBRIDGE_CAP_LION_F24_F32_RECORDS 0x400u /* p_dtype DT_PACKED_LION_F24_F32 (15) */
+#define ADAMBRIDGE_CAP_LION_FP8_F24_RECORDS 0x800u /* p_dtype DT_PACKED_LION_FP8_F24 (16) */
 ADAMBRIDGE_API uint32_t adambridge_capabilities(void);
 
 /* kernels.c:1495-1510.  The level whose results are reproduced: its vector
@@ -357,6 +364,7 @@ ADAMBRIDGE_API int adambridge_convert(const void* src, const float* src_scale, i
  *     DT_PACKED_F32       {s, NULL, 3072, DT_F32, 8}     DT_PACKED_F24       {s, s + 512, 1792, DT_F24, 8}
  *     DT_PACKED_LION_F24  {s, s + 512, 1280, DT_F24, 8}   DT_PACKED_LION_F32  {s, NULL, 2048, DT_F32, 8}
  *     DT_PACKED_F24_F32   {s, s + 512, 2816, DT_F24, 8}   DT_PACKED_LION_F24_F32 {s, s + 512, 1792, DT_F24, 8}
+ *     DT_PACKED_FP8_F24   {s, s + 256, 640, DT_F24, 7}    DT_PACKED_LION_FP8_F24 {s, s + 256, 512, DT_F24, 7}
  * and a separate FP24 master is {hi, lo, 0, DT_F24, 0}.  data is aligned to its value size (16 bytes
  * for DT_PACKED_FP8) and stride a multiple of it. */
 typedef struct adambridge_plane {

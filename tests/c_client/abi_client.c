@@ -75,7 +75,7 @@ static int run_abi(void)
     struct { const char* what; int field; int value; int code; } cases[] = {
         {"negative n", 0, -1, ADAMBRIDGE_EBADN},
         {"unknown algorithm", 1, 7, ADAMBRIDGE_EALGO},
-        {"unknown p_dtype", 2, 16, ADAMBRIDGE_EPDTYPE},
+        {"unknown p_dtype", 2, 17, ADAMBRIDGE_EPDTYPE},
         {"NULL gradient", 3, 0, ADAMBRIDGE_ENULL},
         {"gradient dtype FP8", 4, ADAMBRIDGE_DT_FP8, ADAMBRIDGE_EGDTYPE},
         {"moment dtype F24", 5, ADAMBRIDGE_DT_F24, ADAMBRIDGE_EMVDTYPE},

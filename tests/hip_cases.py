@@ -302,6 +302,38 @@ def pack_lion8_records(case: O.Case) -> np.ndarray:
     return rec
 
 
+def pack_lion8f24_records(case: O.Case) -> np.ndarray:
+    """Separate FP24 master planes + FP8 m codes -> ADAMBRIDGE_DT_PACKED_LION_FP8_F24 records (blocks x
+    512 bytes): the planes as in pack_f8f24_records, then the 128 m codes in element order."""
+    n = case.n
+    nb = max(1, -(-n // 128))
+    hi = np.full(nb * 128, 0xA5A5, np.uint16)
+    hi[:n] = case.arrays["p"].view(np.uint16)
+    lo = np.full(nb * 128, 0x5A, np.uint8)
+    lo[:n] = case.arrays["p_lo"]
+    c = np.zeros(nb * 128, np.uint8)
+    src = case.arrays["m"]
+    c[:min(src.size, nb * 128)] = src[:nb * 128]
+    rec = np.zeros((nb, 512), np.uint8)
+    rec[:, :256] = hi.reshape(nb, 128).view(np.uint8)
+    rec[:, 256:384] = lo.reshape(nb, 128)
+    rec[:, 384:] = c.reshape(nb, 128)
+    return rec
+
+
+def unpack_lion8f24_records(case: O.Case, rec: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """ADAMBRIDGE_DT_PACKED_LION_FP8_F24 records -> the case's master planes and m codes (in place);
+    returns the padding masters' (high halves, low bytes) past n."""
+    n, nb = case.n, rec.shape[0]
+    hi = np.ascontiguousarray(rec[:, :256]).view(np.uint16).reshape(-1)
+    lo = np.ascontiguousarray(rec[:, 256:384]).reshape(-1)
+    case.arrays["p"] = hi[:n].view(case.arrays["p"].dtype).copy()
+    case.arrays["p_lo"] = lo[:n].copy()
+    size = case.arrays["m"].size
+    case.arrays["m"] = np.ascontiguousarray(rec[:, 384:]).reshape(-1)[:size].copy()
+    return hi[n:].copy(), lo[n:].copy()
+
+
 def unpack_lion8_records(case: O.Case, rec: np.ndarray) -> np.ndarray:
     """ADAMBRIDGE_DT_PACKED_LION_FP8 records -> the case's separate master and m codes (in place);
     returns the padding masters' bits past n."""
@@ -317,19 +349,21 @@ def run_hip_records(cases: list[O.Case], width: int = 16, misalign_g: bool = Fal
                     seg_flags: int = 0, padding: list | None = None) -> list[O.Case]:
     """Like run_hip for FP8 moment cases, through the block-record layouts: AdamW with an FP32 master
     (ADAMBRIDGE_DT_PACKED_FP8) or an FP24 master (ADAMBRIDGE_DT_PACKED_FP8_F24), by the case's
-    p_dtype, and Lion with an FP32 master (ADAMBRIDGE_DT_PACKED_LION_FP8).  Pack on the host, one
-    call, unpack the result; ``padding`` receives each FP24 or Lion case's padding masters after the
-    call."""
+    p_dtype, and Lion with an FP32 or FP24 master (ADAMBRIDGE_DT_PACKED_LION_FP8, _LION_FP8_F24).  Pack
+    on the host, one call, unpack the result; ``padding`` receives each FP24 or Lion case's padding
+    masters after the call."""
     kernels = _hip.load()
     work = [c.copy() for c in cases]
     keep, segs = [], []
     by_group = all(c.group is not None for c in work)
     for c in work:
         lion = c.algorithm == O.LION
-        assert c.mv_dtype == O.DT_FP8 and c.p_dtype in ((O.DT_F32,) if lion else (O.DT_F32, O.DT_F24))
+        assert c.mv_dtype == O.DT_FP8 and c.p_dtype in (O.DT_F32, O.DT_F24)
         O.check_sizes(c)
         f24 = c.p_dtype == O.DT_F24
-        rec = torch.from_numpy(pack_lion8_records(c) if lion else pack_f8f24_records(c) if f24 else pack_records(c)).cuda()
+        pack = {(True, True): pack_lion8f24_records, (True, False): pack_lion8_records,
+                (False, True): pack_f8f24_records, (False, False): pack_records}[(lion, f24)]
+        rec = torch.from_numpy(pack(c)).cuda()
         g = to_device(c.arrays["g"])
         if misalign_g:
             buf = torch.empty(g.numel() + 1, dtype=g.dtype, device=g.device)
@@ -350,7 +384,8 @@ def run_hip_records(cases: list[O.Case], width: int = 16, misalign_g: bool = Fal
                                  group=ctypes.pointer(grp) if grp is not None else None, n=c.n, step=c.step,
                                  index=c.index, offset=c.offset, g_dtype=c.g_dtype, mv_dtype=O.DT_FP8,
                                  out_dtype=c.out_dtype, algorithm=c.algorithm,
-                                 p_dtype=_hip.DT_PACKED8_LION if lion else _hip.DT_PACKED8_F24 if f24 else _hip.DT_PACKED8,
+                                 p_dtype={(True, True): _hip.DT_PACKED8_LION_F24, (True, False): _hip.DT_PACKED8_LION,
+                                          (False, True): _hip.DT_PACKED8_F24, (False, False): _hip.DT_PACKED8}[(lion, f24)],
                                  reserved=seg_flags))
     arr = kernels.segment_array([ctypes.pointer(s) for s in segs])
     kernels.set_simd_level(WIDTH_LEVEL[width])
@@ -370,7 +405,8 @@ def run_hip_records(cases: list[O.Case], width: int = 16, misalign_g: bool = Fal
             next(it)
         rec, g, ms, vs, out, grp = (next(it) for _ in range(6))
         if c.algorithm == O.LION:
-            pad = unpack_lion8_records(c, rec.cpu().numpy())
+            unpack = unpack_lion8f24_records if c.p_dtype == O.DT_F24 else unpack_lion8_records
+            pad = unpack(c, rec.cpu().numpy())
             if padding is not None:
                 padding.append(pad)
         elif c.p_dtype == O.DT_F24:

@@ -56,7 +56,8 @@ def test_header_codes_match_the_python_mirror():
               "DT_PACKED_F24": _hip.DT_PACKED_F24, "DT_PACKED_LION_F24": _hip.DT_PACKED_LION_F24,
               "DT_PACKED_FP8_F24": _hip.DT_PACKED8_F24, "DT_PACKED_LION_F32": _hip.DT_PACKED_LION_F32,
               "DT_PACKED_LION_FP8": _hip.DT_PACKED8_LION, "DT_PACKED_F24_F32": _hip.DT_PACKED_F24_F32,
-              "DT_PACKED_LION_F24_F32": _hip.DT_PACKED_LION_F24_F32}
+              "DT_PACKED_LION_F24_F32": _hip.DT_PACKED_LION_F24_F32,
+              "DT_PACKED_LION_FP8_F24": _hip.DT_PACKED8_LION_F24}
     assert codes == mirror
     flag = re.search(r"#define ADAMBRIDGE_SEG_OUT_PREVIOUS (\d+)", text)
     assert flag and int(flag.group(1)) == _hip.SEG_OUT_PREVIOUS
@@ -100,7 +101,7 @@ def _segment_variants():
     return [
         ("negative n", m(n=-1), -1),
         ("unknown algorithm", m(algorithm=5), -12),
-        ("unknown master format", m(p_dtype=16), -13),
+        ("unknown master format", m(p_dtype=17), -13),
         ("no master", m(p=None), -2),
         ("no gradient", m(g=None), -2),
         ("no first moment", m(m=None), -2),

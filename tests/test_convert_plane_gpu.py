@@ -113,7 +113,7 @@ LAYOUTS = [("pairs", "adamw", "bf16", "fp32"), ("lion-records", "lion", "bf16", 
            ("lion-f24-records", "lion", "bf16", "fp24"), ("fp8-records", "adamw", "fp8", "fp32"),
            ("fp8-f24-records", "adamw", "fp8", "fp24"), ("lion-f32-records", "lion", "fp32", "fp32"),
            ("lion-fp8-records", "lion", "fp8", "fp32"), ("f24-f32-records", "adamw", "fp32", "fp24"),
-           ("lion-f24-f32-records", "lion", "fp32", "fp24"),
+           ("lion-f24-f32-records", "lion", "fp32", "fp24"), ("lion-fp8-f24-records", "lion", "fp8", "fp24"),
            ("separate", "adamw", "bf16", "fp24"), ("separate", "adamw", "fp8", "fp32")]
 
 

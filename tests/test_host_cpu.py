@@ -631,9 +631,8 @@ def test_large_state_arenas_follow_an_allocate_free_of_their_size(monkeypatch):
 def test_layout_choice_for_every_algorithm_precision_and_master():
     """Each (algorithm, moment precision) with an FP32 master of the optimizer's own gets its
     interleaved layout (Lion with a BF16, FP32 or FP8 moment), and AdamW with BF16, FP8 or FP32 moments
-    and Lion with a BF16 or FP32 moment their FP24 records under an FP24 master; Lion with an FP8 moment
-    and an FP24 master, an FP32 parameter updated in place, and state_layout='separate' keep the
-    reference's arrays."""
+    and Lion with a BF16, FP32 or FP8 moment their FP24 records under an FP24 master; an FP32 parameter
+    updated in place and state_layout='separate' keep the reference's arrays."""
     from adambridge_amd.state import choose_layout
     want = {("adamw", "bf16"): "pairs", ("adamw", "fp8"): "fp8-records", ("adamw", "fp32"): "f32-records",
             ("lion", "bf16"): "lion-records", ("lion", "fp8"): "lion-fp8-records", ("lion", "fp32"): "lion-f32-records"}
@@ -643,7 +642,8 @@ def test_layout_choice_for_every_algorithm_precision_and_master():
                                                      ("lion", "bf16"): "lion-f24-records",
                                                      ("adamw", "fp8"): "fp8-f24-records",
                                                      ("adamw", "fp32"): "f24-f32-records",
-                                                     ("lion", "fp32"): "lion-f24-f32-records"}.get((algo, prec), "separate")
+                                                     ("lion", "fp32"): "lion-f24-f32-records",
+                                                     ("lion", "fp8"): "lion-fp8-f24-records"}.get((algo, prec), "separate")
         assert choose_layout(algo, prec, "fp24", requested="separate") == "separate"
         assert choose_layout(algo, prec, "fp32", master_is_param=True) == "separate"
         assert choose_layout(algo, prec, "fp32", requested="separate") == "separate"
@@ -651,7 +651,7 @@ def test_layout_choice_for_every_algorithm_precision_and_master():
 
 @pytest.mark.parametrize("layout", ["pairs", "fp8-records", "lion-records", "f32-records", "f24-records",
                                     "lion-f24-records", "fp8-f24-records", "lion-f32-records", "lion-fp8-records",
-                                    "f24-f32-records", "lion-f24-f32-records"])
+                                    "f24-f32-records", "lion-f24-f32-records", "lion-fp8-f24-records"])
 def test_arena_plan_aligns_large_buffers_and_packs_small_ones(layout):
     """Buffers of 2 MiB or more start on 2 MiB boundaries, smaller ones on 256-byte boundaries (16-byte
     state access needs 16); no two buffers overlap, and many small tensors take little more than

@@ -269,8 +269,8 @@ from hip_cases import run_hip_records  # noqa: E402
 
 
 # (algorithm, master): ADAMBRIDGE_DT_PACKED_FP8, ADAMBRIDGE_DT_PACKED_FP8_F24, ADAMBRIDGE_DT_PACKED_LION_FP8
-RECORD_KINDS = [(O.ADAMW, O.DT_F32), (O.ADAMW, O.DT_F24), (O.LION, O.DT_F32)]
-RECORD_IDS = ["adamw-f32", "adamw-f24", "lion-f32"]
+RECORD_KINDS = [(O.ADAMW, O.DT_F32), (O.ADAMW, O.DT_F24), (O.LION, O.DT_F32), (O.LION, O.DT_F24)]
+RECORD_IDS = ["adamw-f32", "adamw-f24", "lion-f32", "lion-f24"]   # the last: ADAMBRIDGE_DT_PACKED_LION_FP8_F24
 
 
 @pytest.mark.parametrize("algo,pt", RECORD_KINDS, ids=RECORD_IDS)
@@ -295,7 +295,7 @@ def test_fp8_records_match_oracle(algo, pt):
         for w, g in zip(want, got):
             check(w, g)
         for pad in padding:
-            if algo == O.LION:
+            if algo == O.LION and pt == O.DT_F32:
                 assert np.all(pad == 0x7F8A5A5A), "a Lion record's padding master was written"
             else:
                 hi, lo = pad
@@ -329,7 +329,7 @@ def test_fp8_records_multi_step_groups_and_steps(algo, pt):
     check(run_steps(case, grads, oracle_runner, 16), run_steps(case, grads, run_hip_records, 16))
 
 
-@pytest.mark.parametrize("layout", ["fp8-records", "fp8-f24-records", "lion-fp8-records"])
+@pytest.mark.parametrize("layout", ["fp8-records", "fp8-f24-records", "lion-fp8-records", "lion-fp8-f24-records"])
 def test_fp8_records_reject_bad_segments(layout):
     """The other algorithm (-12), a second state buffer (-13), BF16 moments (-4) and a misaligned
     record (-14)."""
@@ -343,8 +343,8 @@ def test_fp8_records_reject_bad_segments(layout):
     sc = torch.ones(3, dtype=torch.float32, device="cuda")
     hp = _hip.HParams(**{kk: case.hparams[kk] for kk, _ in _hip.HParams._fields_})
     pt = {"fp8-records": _hip.DT_PACKED8, "fp8-f24-records": _hip.DT_PACKED8_F24,
-          "lion-fp8-records": _hip.DT_PACKED8_LION}[layout]
-    algo = 1 if layout == "lion-fp8-records" else 0
+          "lion-fp8-records": _hip.DT_PACKED8_LION, "lion-fp8-f24-records": _hip.DT_PACKED8_LION_F24}[layout]
+    algo = 1 if layout.startswith("lion") else 0
     base = dict(p=rec.data_ptr(), g=g.data_ptr(), m_scale=sc.data_ptr(), v_scale=sc.data_ptr(), n=300, step=1,
                 mv_dtype=O.DT_FP8, g_dtype=O.DT_BF16, out_dtype=0, algorithm=algo, p_dtype=pt)
     for change, code in ((dict(algorithm=1 - algo), -12), (dict(p_lo=rec.data_ptr()), -13),
@@ -760,7 +760,7 @@ cases = [O.make_case(rng, n, algorithm=algo, mv_dtype=O.DT_FP8, p_dtype=pt, stoc
                      offset=128 * int(rng.integers(0, 2**20)), index=int(rng.integers(0, 999)), step=3)
          for algo, pt, sr, n in itertools.product([O.ADAMW, O.LION], [O.DT_F32, O.DT_F24], [True, False],
                                                   [129, 4096 + 77, 3 * 4096, 20000 + 5])]
-records = [c for c in cases if c.algorithm == O.ADAMW or c.p_dtype == O.DT_F32]   # the block-record layouts
+records = cases   # every combination has its block records
 bad = 0
 for runner, subset in ((run_hip, cases), (run_hip_records, records)):
     for w, g in zip(O.run_many(subset, "oracle", 16), runner(subset, 16)):
@@ -803,7 +803,7 @@ def _previous_weight(case):
 
 @pytest.mark.parametrize("layout", ["separate", "pairs", "fp8-records", "lion-records", "f32-records", "f24-records",
                                     "lion-f24-records", "fp8-f24-records", "lion-f32-records", "lion-fp8-records",
-                                    "f24-f32-records", "lion-f24-f32-records"])
+                                    "f24-f32-records", "lion-f24-f32-records", "lion-fp8-f24-records"])
 def test_out_previous_writes_the_weight_from_before_the_update(layout):
     """ADAMBRIDGE_SEG_OUT_PREVIOUS (delayed updates): out receives the weight of the master as stored
     before the update -- FP32, or bf16 by the kernels' rounding of FP32 and decoded FP24 masters,
@@ -820,13 +820,14 @@ def test_out_previous_writes_the_weight_from_before_the_update(layout):
               "fp8-f24-records": [(O.ADAMW, O.DT_FP8, O.DT_F24)],
               "lion-f32-records": [(O.LION, O.DT_F32, O.DT_F32)], "lion-fp8-records": [(O.LION, O.DT_FP8, O.DT_F32)],
               "f24-f32-records": [(O.ADAMW, O.DT_F32, O.DT_F24)],
-              "lion-f24-f32-records": [(O.LION, O.DT_F32, O.DT_F24)]}[layout]
+              "lion-f24-f32-records": [(O.LION, O.DT_F32, O.DT_F24)],
+              "lion-fp8-f24-records": [(O.LION, O.DT_FP8, O.DT_F24)]}[layout]
     runner = {"separate": run_hip, "pairs": run_hip_packed, "fp8-records": run_hip_records,
               "lion-records": run_hip_lion_records, "f32-records": run_hip_f32_records,
               "f24-records": run_hip_f24_records, "lion-f24-records": run_hip_f24_records,
               "fp8-f24-records": run_hip_records, "lion-f32-records": run_hip_lion_f32_records,
               "lion-fp8-records": run_hip_records, "f24-f32-records": run_hip_f24_records,
-              "lion-f24-f32-records": run_hip_f24_records}[layout]
+              "lion-f24-f32-records": run_hip_f24_records, "lion-fp8-f24-records": run_hip_records}[layout]
     cases = []
     for (algo, mv, pt), gt, ot, sr, n in itertools.product(combos, [O.DT_BF16, O.DT_F32], [O.DT_F32, O.DT_BF16],
                                                              [True, False], [1, 15, 17, 129, 1000, 8192 + 77]):
