@@ -1793,7 +1793,7 @@ inline bool kernel_is_fp8(int index)
     return (index >= kNumKernels + kNumPacked && index < kNumKernels + 2 * kNumPacked) ||
            (index >= kNumKernels + 6 * kNumPacked && index < kNumKernels + 7 * kNumPacked) ||
            (index >= kNumKernels + 8 * kNumPacked && index < kNumKernels + 9 * kNumPacked) ||
-           index >= kNumKernels + 11 * kNumPacked;
+           (index >= kNumKernels + 11 * kNumPacked && index < kNumKernels + 12 * kNumPacked);
 }
 
 // Dynamic LDS (unused) per workgroup of a launch of kernel `index`: it caps the workgroups a CU holds
