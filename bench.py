@@ -625,6 +625,18 @@ def cpu_bench(cfg: dict, budget_params: int, steps: int) -> dict:
 
 # --------------------------------------------------------------------- main
 
+def config_of(name: str, master: str = "fp32", precision: str | None = None) -> tuple[dict, bool]:
+    """The workload of configuration ``name`` with ``master`` and, when given, ``precision`` for its
+    moments; and whether the moments are the configuration's own (its measured traffic applies)."""
+    cfg = dict(CONFIGS[name], master=master)
+    own = cfg["precision"] == (precision or cfg["precision"])
+    if not own:
+        names = {"fp32": "FP32", "bf16": "bf16", "fp8": "FP8"}
+        cfg["desc"] = cfg["desc"].replace(names[cfg["precision"]], names[precision], 1)
+        cfg["precision"] = precision
+    return cfg, own
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -671,12 +683,7 @@ def main() -> int:
         calibrate_copy(args.calibrate_copy)
     if args.config == "c5":
         return main_pipeline(args)
-    cfg = dict(CONFIGS[args.config], master=args.master)
-    own = cfg["precision"] == (args.precision or cfg["precision"])   # the configuration's own moments
-    if not own:
-        names = {"fp32": "FP32", "bf16": "bf16", "fp8": "FP8"}
-        cfg["desc"] = cfg["desc"].replace(names[cfg["precision"]], names[args.precision], 1)
-        cfg["precision"] = args.precision
+    cfg, own = config_of(args.config, args.master, args.precision)
     print(f"[bench] config {args.config}: {cfg['desc']}; warmup {args.warmup}, steps {args.steps}",
           file=sys.stderr, flush=True)
     held: list = []

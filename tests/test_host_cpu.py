@@ -756,3 +756,25 @@ def test_memory_report_keys():
     rep = ab.AdamBridge.memory_report(opt)
     assert set(rep) == {"master", "moments", "staging", "reserved", "total", "gpu_state"}
     assert rep["reserved"] == 1024 and rep["total"] == 1024 and rep["gpu_state"] == rep["total"]
+
+
+def test_bench_precision_override_and_one_gpu_only():
+    """bench.py's --precision: the configuration's workload with other moments, its description
+    renamed and its measured traffic set aside; and --gpus above 1 exits with a message before
+    touching a device."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parents[1]
+    sys.path.insert(0, str(root))
+    import bench
+    cfg, own = bench.config_of("c4", "fp32", "fp8")
+    assert not own and cfg["precision"] == "fp8" and cfg["desc"].startswith("Lion, FP8 moment")
+    assert bench.CONFIGS["c4"]["precision"] == "bf16"   # the table itself is unchanged
+    cfg, own = bench.config_of("c3p", "fp24", None)
+    assert own and cfg["master"] == "fp24" and cfg["precision"] == "bf16"
+    cfg, own = bench.config_of("c1", "fp32", "fp32")
+    assert own and cfg["desc"] == bench.CONFIGS["c1"]["desc"]
+    run = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                         timeout=120, cwd=root)
+    assert run.returncode != 0 and "one GPU" in (run.stdout + run.stderr)
